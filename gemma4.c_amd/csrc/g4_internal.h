@@ -1,0 +1,94 @@
+// g4_internal.h -- shared between the HIP translation units of libg4.so.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "g4.h"
+
+namespace g4 {
+
+// ---- errors ---------------------------------------------------------------
+
+// Records a message for g4_last_error() and returns `status`.
+int set_error(int status, const char *fmt, ...);
+
+#define G4_HIP(call)                                                                    \
+    do {                                                                                \
+        hipError_t e_ = (call);                                                         \
+        if (e_ != hipSuccess)                                                           \
+            return ::g4::set_error(G4_ERR_DEVICE, "%s: %s (%s:%d)", #call,              \
+                                   hipGetErrorString(e_), __FILE__, __LINE__);          \
+    } while (0)
+
+#define G4_CHECK(cond, ...)                                                             \
+    do {                                                                                \
+        if (!(cond)) return ::g4::set_error(G4_ERR_ARG, __VA_ARGS__);                   \
+    } while (0)
+
+// ---- device helpers ---------------------------------------------------------
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+    return __half2float(__ushort_as_half(h));  // exact
+}
+
+// ---- scratch owned by the library ------------------------------------------
+
+// Device scratch for split-K matmul dot products, their arrival counters and
+// attention partials.  Grows on demand (allocation happens outside any kernel
+// sequence that a caller might capture).
+struct Scratch {
+    int32_t *dots = nullptr;       // split-K exact group dot products
+    size_t dots_bytes = 0;
+    unsigned *counters = nullptr;  // per 16-row block arrival counters (kept zero)
+    size_t counters_count = 0;
+    float *attn = nullptr;         // attention partials (m, l, o per chunk)
+    size_t attn_bytes = 0;
+};
+Scratch &scratch();
+int scratch_reserve(size_t dots_bytes, size_t counters, size_t attn_bytes);
+
+// ---- launchers (asynchronous on `stream`; shapes validated by callers) -------
+
+// gemma4.c:265-279
+void launch_quantize(hipStream_t s, int8_t *q, float *scales, const float *x, size_t groups);
+
+// gemma4.c:257-262; rows <= 8 takes the split-K GEMV, larger the MFMA GEMM.
+// out row stride is out_stride (>= N).
+int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq,
+                  const float *xs, const int8_t *w, const uint16_t *ws, int n_out, int k,
+                  int rows);
+
+// gemma4.c:360-373 (weight may be null)
+void launch_rmsnorm(hipStream_t s, float *out, const float *in, const float *weight, int width,
+                    float eps, size_t rows);
+// gemma4.c:375-378
+void launch_add_and_scale(hipStream_t s, float *out, const float *add, size_t n, float scale);
+// gemma4.c:381-398 (rows of v are heads*head_dim wide)
+void launch_rope(hipStream_t s, const float *cosines, const float *sines, int pairs, float *v,
+                 int heads, int head_dim, int start_pos, size_t n);
+// gemma4.c:310-331
+void launch_geglu(hipStream_t s, float *gate, const float *up, int rows, int width,
+                  int up_stride, const float *table, int table_size, float lower, float upper);
+// gemma4.c:337-358
+// Tokens outside [0, table_rows) produce NaN rows instead of reading outside.
+void launch_embedding(hipStream_t s, float *out, const int8_t *table, const uint16_t *scales,
+                      int width, int table_rows, const int *tokens, size_t n, float multiplier);
+// gemma4.c:443-456: attention over a ring cache.
+int launch_attend(hipStream_t s, float *out, const float *q, const float *key_cache,
+                  const float *value_cache, int cache_len, int head_dim, int heads, int full,
+                  int start_pos, size_t n);
+// Fused tail of the K/V projections (gemma4.c:437-440): rmsnorm+rope of the n
+// new keys and rmsnorm of the new values, written into the rings at
+// (start_pos + t) & (cache_len - 1).
+void launch_kv_finish(hipStream_t s, float *key_cache, float *value_cache, const float *k_new,
+                      const float *v_new, const float *k_norm, const float *cosines,
+                      const float *sines, int pairs, int head_dim, int cache_len, int start_pos,
+                      size_t n);
+// gemma4.c:518-519: 30 * tanh(x / 30) in place.
+void launch_softcap(hipStream_t s, float *x, size_t n);
+// First index of the maximum (gemma4.c:537-541) of each of `rows` rows.
+void launch_argmax(hipStream_t s, int *out, const float *x, size_t rows, size_t width);
+
+}  // namespace g4

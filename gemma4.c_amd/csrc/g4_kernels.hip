@@ -1,0 +1,852 @@
+// g4_kernels.hip -- gfx950 kernels of the W8A8 forward path and the per-op
+// entry points of include/g4.h.
+//
+// Arithmetic contract (parity with gemma4.c):
+//   quantize, the matmul (exact int32 group dots + the group-ordered fp32
+//   fold), rope, geglu, embedding, add_and_scale and the attention scores are
+//   bit-identical to the reference on identical inputs; rmsnorm sums, softmax
+//   and the value sums use a parallel order (rounding differs in the last
+//   bits); expf/tanhf come from the device math library.
+//   Built with -ffp-contract=off: a*b+c rounds twice unless fmaf() is written.
+#include <float.h>
+#include <math.h>
+
+#include "g4_internal.h"
+
+namespace g4 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Scratch
+
+static Scratch g_scratch;
+Scratch &scratch() { return g_scratch; }
+
+int scratch_reserve(size_t dots_bytes, size_t counters, size_t attn_bytes) {
+    Scratch &s = g_scratch;
+    if (dots_bytes > s.dots_bytes) {
+        if (s.dots) G4_HIP(hipFree(s.dots));
+        s.dots = nullptr;
+        s.dots_bytes = 0;
+        G4_HIP(hipMalloc(&s.dots, dots_bytes));
+        s.dots_bytes = dots_bytes;
+    }
+    if (counters > s.counters_count) {
+        if (s.counters) G4_HIP(hipFree(s.counters));
+        s.counters = nullptr;
+        s.counters_count = 0;
+        G4_HIP(hipMalloc(&s.counters, counters * sizeof(unsigned)));
+        G4_HIP(hipMemset(s.counters, 0, counters * sizeof(unsigned)));
+        G4_HIP(hipDeviceSynchronize());
+        s.counters_count = counters;
+    }
+    if (attn_bytes > s.attn_bytes) {
+        if (s.attn) G4_HIP(hipFree(s.attn));
+        s.attn = nullptr;
+        s.attn_bytes = 0;
+        G4_HIP(hipMalloc(&s.attn, attn_bytes));
+        s.attn_bytes = attn_bytes;
+    }
+    return G4_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Reductions
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Sum over a 256-thread block; every thread gets the result.
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// ---------------------------------------------------------------------------
+// Quantize (gemma4.c:265-279): 16 lanes per 64-value group, 4 values a lane.
+
+__global__ __launch_bounds__(256) void k_quantize(int8_t *__restrict__ q, float *__restrict__ scales,
+                                                  const float *__restrict__ x, size_t groups) {
+    const size_t gid = (size_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int sub = threadIdx.x & 15;
+    if (gid >= groups) return;  // all 16 lanes of a group leave together
+    const float4 v = reinterpret_cast<const float4 *>(x + gid * 64)[sub];
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+    const float scale = m / 127.0f;
+    const float inverse = scale > 0.0f ? 1.0f / scale : 0.0f;
+    char4 out;
+    out.x = (signed char)(int)rintf(v.x * inverse);
+    out.y = (signed char)(int)rintf(v.y * inverse);
+    out.z = (signed char)(int)rintf(v.z * inverse);
+    out.w = (signed char)(int)rintf(v.w * inverse);
+    reinterpret_cast<char4 *>(q + gid * 64)[sub] = out;
+    if (sub == 0) scales[gid] = scale;
+}
+
+void launch_quantize(hipStream_t s, int8_t *q, float *scales, const float *x, size_t groups) {
+    if (!groups) return;
+    hipLaunchKernelGGL(k_quantize, dim3((unsigned)((groups + 15) / 16)), dim3(256), 0, s, q, scales,
+                       x, groups);
+}
+
+// ---------------------------------------------------------------------------
+// W8A8 matmul, few rows (decode): split-K GEMV, one wave per (16-row block,
+// group range).
+//
+// A wave reads one 1024-byte tile per group with one 16-byte load per lane:
+// lane l holds chunk c = l/4 (k = 4c..4c+3) of rows 4(l%4)..4(l%4)+3.  Four
+// v_dot4_i32_i8 give the lane's partial dots; a transposing butterfly over the
+// 16 lanes that share l%4 leaves the exact int32 group dot of row
+// 4(l%4) + 2 b2 + b3 (b2, b3 = bits 2, 3 of l) in lanes 0..15.  The fold
+// acc = fma((float)dot, f32(ws) * xs, acc) runs over groups in ascending
+// order as in gemma4.c:216-218, so results are bit-identical.  With several
+// splits per block, each wave stores its exact dots and the last wave to
+// arrive on the block's counter folds all groups in order.
+
+template <int M>
+__global__ __launch_bounds__(64) void k_gemv(float *__restrict__ out, size_t out_stride,
+                                             const int8_t *__restrict__ xq,
+                                             const float *__restrict__ xs,
+                                             const int8_t *__restrict__ w,
+                                             const uint16_t *__restrict__ ws, int k, int splits,
+                                             int rows, int32_t *__restrict__ dots,
+                                             unsigned *__restrict__ counters) {
+    const int groups = k >> 6;
+    const int block = blockIdx.x / splits, split = blockIdx.x % splits;
+    const int g_begin = (int)((long)split * groups / splits);
+    const int g_end = (int)((long)(split + 1) * groups / splits);
+    const int lane = threadIdx.x;
+    const int chunk = lane >> 2, b2 = (lane >> 2) & 1, b3 = (lane >> 3) & 1;
+    const int row = 4 * (lane & 3) + 2 * b2 + b3;
+    const uint4 *tiles = reinterpret_cast<const uint4 *>(w + (size_t)block * 16 * k);
+    const uint16_t *wscale = ws + (size_t)block * groups * 16;
+
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) acc[m] = 0.0f;
+
+    constexpr int U = 4;
+    for (int g = g_begin; g < g_end; g += U) {
+        uint4 t[U];
+        int x4[U][M];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (g + u < g_end) {
+                t[u] = tiles[(size_t)(g + u) * 64 + lane];
+#pragma unroll
+                for (int m = 0; m < M; m++)
+                    x4[u][m] = m < rows ? *reinterpret_cast<const int *>(xq + (size_t)m * k +
+                                                                         (g + u) * 64 + 4 * chunk)
+                                        : 0;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (g + u >= g_end) break;
+            const int gg = g + u;
+            int d[M];
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const int p0 = __builtin_amdgcn_sdot4((int)t[u].x, x4[u][m], 0, false);
+                const int p1 = __builtin_amdgcn_sdot4((int)t[u].y, x4[u][m], 0, false);
+                const int p2 = __builtin_amdgcn_sdot4((int)t[u].z, x4[u][m], 0, false);
+                const int p3 = __builtin_amdgcn_sdot4((int)t[u].w, x4[u][m], 0, false);
+                int k0 = b2 ? p2 : p0, k1 = b2 ? p3 : p1;
+                const int s0 = b2 ? p0 : p2, s1 = b2 ? p1 : p3;
+                k0 += __shfl_xor(s0, 4);
+                k1 += __shfl_xor(s1, 4);
+                int kk = b3 ? k1 : k0;
+                const int ss = b3 ? k0 : k1;
+                kk += __shfl_xor(ss, 8);
+                kk += __shfl_xor(kk, 16);
+                kk += __shfl_xor(kk, 32);
+                d[m] = kk;
+            }
+            if (splits == 1) {
+                const float wsf = half_bits_to_float(wscale[gg * 16 + row]);
+#pragma unroll
+                for (int m = 0; m < M; m++)
+                    if (m < rows) acc[m] = fmaf((float)d[m], wsf * xs[(size_t)m * groups + gg], acc[m]);
+            } else if (lane < 16) {
+#pragma unroll
+                for (int m = 0; m < M; m++)
+                    dots[(((size_t)block * groups + gg) * M + m) * 16 + row] = d[m];
+            }
+        }
+    }
+
+    if (splits > 1) {
+        __threadfence();
+        unsigned previous = 0;
+        if (lane == 0) previous = atomicAdd(&counters[block], 1u);
+        previous = __shfl(previous, 0);
+        if (previous != (unsigned)(splits - 1)) return;
+        __threadfence();
+        if (lane < 16) {
+            for (int g = 0; g < groups; g++) {
+                const float wsf = half_bits_to_float(wscale[g * 16 + row]);
+#pragma unroll
+                for (int m = 0; m < M; m++)
+                    if (m < rows)
+                        acc[m] = fmaf((float)dots[(((size_t)block * groups + g) * M + m) * 16 + row],
+                                      wsf * xs[(size_t)m * groups + g], acc[m]);
+            }
+        }
+        if (lane == 0) atomicExch(&counters[block], 0u);
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int m = 0; m < M; m++)
+            if (m < rows) out[(size_t)m * out_stride + (size_t)block * 16 + row] = acc[m];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// W8A8 matmul, many rows (prefill): int8 MFMA GEMM, 64x64 output tile per
+// 256-thread block, one 64-deep K step per quantization group.
+//
+// v_mfma_i32_16x16x64_i8: lane l supplies 16 bytes of A row (l%16) and of B
+// column (l%16), both for k-slots 16(l/16)..16(l/16)+15; the output element
+// (i, j) = (4(l/16)+v, l%16) comes back in lane l, register v.  B comes straight
+// from the packed tiles: column n, k = 16q + b lives at chunk 4q + b/4, so a
+// lane gathers 4 dwords from the staged tile.  Every MFMA covers exactly one
+// group, so the group-ordered fp32 fold is the reference's.
+
+__global__ __launch_bounds__(256) void k_gemm(float *__restrict__ out, size_t out_stride,
+                                              const int8_t *__restrict__ xq,
+                                              const float *__restrict__ xs,
+                                              const int8_t *__restrict__ w,
+                                              const uint16_t *__restrict__ ws, int rows,
+                                              int n_out, int k) {
+    const int groups = k >> 6;
+    const int m0 = blockIdx.y * 64, nb0 = blockIdx.x * 4, n_blocks = n_out >> 4;
+    __shared__ __attribute__((aligned(16))) int8_t s_a[64 * 64];
+    __shared__ __attribute__((aligned(16))) int8_t s_b[4 * 1024];
+    __shared__ float s_xs[64], s_ws[64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, q = lane >> 4, l16 = lane & 15;
+    float acc[2][2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[i][j][v] = 0.0f;
+    const v4i zero = {0, 0, 0, 0};
+
+    for (int g = 0; g < groups; g++) {
+        {
+            const int r = tid >> 2, part = tid & 3;
+            v4i v = zero;
+            if (m0 + r < rows)
+                v = *reinterpret_cast<const v4i *>(xq + (size_t)(m0 + r) * k + g * 64 + part * 16);
+            *reinterpret_cast<v4i *>(s_a + r * 64 + part * 16) = v;
+        }
+        {
+            const int t = tid >> 6;
+            v4i v = zero;
+            if (nb0 + t < n_blocks)
+                v = *reinterpret_cast<const v4i *>(w + ((size_t)(nb0 + t) * groups + g) * 1024 +
+                                                   lane * 16);
+            *reinterpret_cast<v4i *>(s_b + t * 1024 + lane * 16) = v;
+        }
+        if (tid < 64) {
+            s_xs[tid] = m0 + tid < rows ? xs[(size_t)(m0 + tid) * groups + g] : 0.0f;
+        } else if (tid < 128) {
+            const int n = tid - 64, t = n >> 4;
+            s_ws[n] = nb0 + t < n_blocks
+                          ? half_bits_to_float(ws[((size_t)(nb0 + t) * groups + g) * 16 + (n & 15)])
+                          : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+            const v4i a = *reinterpret_cast<const v4i *>(s_a + (wm * 32 + mi * 16 + l16) * 64 + q * 16);
+#pragma unroll
+            for (int ni = 0; ni < 2; ni++) {
+                const int t = wn * 2 + ni;
+                const int *bt = reinterpret_cast<const int *>(s_b + t * 1024);
+                v4i b;
+                b.x = bt[(4 * q + 0) * 16 + l16];
+                b.y = bt[(4 * q + 1) * 16 + l16];
+                b.z = bt[(4 * q + 2) * 16 + l16];
+                b.w = bt[(4 * q + 3) * 16 + l16];
+                const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, zero, 0, 0, 0);
+                const float wsf = s_ws[t * 16 + l16];
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    acc[mi][ni][v] = fmaf((float)d[v], wsf * s_xs[wm * 32 + mi * 16 + 4 * q + v],
+                                          acc[mi][ni][v]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < 2; ni++) {
+            const int t = wn * 2 + ni;
+            if (nb0 + t >= n_blocks) continue;
+            const size_t n = (size_t)(nb0 + t) * 16 + l16;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = m0 + wm * 32 + mi * 16 + 4 * q + v;
+                if (m < rows) out[(size_t)m * out_stride + n] = acc[mi][ni][v];
+            }
+        }
+}
+
+int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq, const float *xs,
+                  const int8_t *w, const uint16_t *ws, int n_out, int k, int rows) {
+    if (rows <= 0) return G4_OK;
+    const int blocks = n_out / 16, groups = k / 64;
+    if (rows > 8) {
+        dim3 grid((unsigned)((blocks + 3) / 4), (unsigned)((rows + 63) / 64));
+        hipLaunchKernelGGL(k_gemm, grid, dim3(256), 0, s, out, out_stride, xq, xs, w, ws, rows,
+                           n_out, k);
+        return G4_OK;
+    }
+    const int m_pad = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+    int splits = 1;
+    if (blocks < 1024) {
+        splits = (1024 + blocks - 1) / blocks;
+        const int max_splits = groups / 4 > 0 ? groups / 4 : 1;
+        if (splits > max_splits) splits = max_splits;
+    }
+    int32_t *dots = nullptr;
+    unsigned *counters = nullptr;
+    if (splits > 1) {
+        const size_t need = (size_t)n_out * groups * m_pad * sizeof(int32_t);
+        int rc = scratch_reserve(need, (size_t)blocks, 0);
+        if (rc) return rc;
+        dots = scratch().dots;
+        counters = scratch().counters;
+    }
+    dim3 grid((unsigned)(blocks * splits));
+#define G4_GEMV(MM)                                                                            \
+    hipLaunchKernelGGL(k_gemv<MM>, grid, dim3(64), 0, s, out, out_stride, xq, xs, w, ws, k,    \
+                       splits, rows, dots, counters)
+    switch (m_pad) {
+    case 1: G4_GEMV(1); break;
+    case 2: G4_GEMV(2); break;
+    case 4: G4_GEMV(4); break;
+    default: G4_GEMV(8); break;
+    }
+#undef G4_GEMV
+    return G4_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise kernels
+
+// gemma4.c:360-373, one block per row.  Parallel sum of squares (each square
+// rounded, then added, as the reference does; only the order differs).
+__global__ __launch_bounds__(256) void k_rmsnorm(float *out, const float *in,
+                                                 const float *__restrict__ weight, int width,
+                                                 float eps) {
+    __shared__ float red[4];
+    const float *x = in + (size_t)blockIdx.x * width;
+    float *y = out + (size_t)blockIdx.x * width;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < width; i += 256) s += x[i] * x[i];
+    s = block_sum256(s, red);
+    const float inverse = 1.0f / sqrtf(s / (float)width + eps);
+    for (int i = threadIdx.x; i < width; i += 256)
+        y[i] = (weight ? weight[i] : 1.0f) * (inverse * x[i]);
+}
+
+void launch_rmsnorm(hipStream_t s, float *out, const float *in, const float *weight, int width,
+                    float eps, size_t rows) {
+    if (!rows) return;
+    hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, s, out, in, weight, width, eps);
+}
+
+__global__ __launch_bounds__(256) void k_add_and_scale(float *out, const float *add, size_t n,
+                                                       float scale) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = (out[i] + add[i]) * scale;
+}
+
+void launch_add_and_scale(hipStream_t s, float *out, const float *add, size_t n, float scale) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_add_and_scale, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out,
+                       add, n, scale);
+}
+
+// gemma4.c:381-398, one thread per (token, head, pair).
+__global__ __launch_bounds__(256) void k_rope(const float *__restrict__ cosines,
+                                              const float *__restrict__ sines, int pairs, float *v,
+                                              int heads, int head_dim, int start_pos, size_t total) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const int j = (int)(i % pairs);
+    const size_t th = i / pairs;  // token * heads + head
+    const size_t t = th / heads;
+    const float c = cosines[((size_t)start_pos + t) * pairs + j];
+    const float s = sines[((size_t)start_pos + t) * pairs + j];
+    float *x = v + th * head_dim;
+    const float a = x[j], b = x[j + head_dim / 2];
+    x[j] = a * c - b * s;
+    x[j + head_dim / 2] = b * c + a * s;
+}
+
+void launch_rope(hipStream_t s, const float *cosines, const float *sines, int pairs, float *v,
+                 int heads, int head_dim, int start_pos, size_t n) {
+    const size_t total = n * (size_t)heads * pairs;
+    if (!total) return;
+    hipLaunchKernelGGL(k_rope, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, cosines,
+                       sines, pairs, v, heads, head_dim, start_pos, total);
+}
+
+// gemma4.c:310-331.
+__device__ __forceinline__ float gelu_table_lookup(float x, const float *table, int size,
+                                                   float lower, float upper) {
+    const float scale = (float)(size - 1) / (upper - lower);
+    if (x <= lower) return table[0];
+    if (!(x >= upper)) {
+        const float position = (x - lower) * scale;
+        const int index = (int)position;
+        // x just below `upper` can round to position == size - 1 (x + 8 -> 16);
+        // the fraction is then 0 and the reference's result is table[size - 1].
+        if (index >= size - 1) return table[size - 1];
+        const float fraction = position - (float)index;
+        return table[index] + fraction * (table[index + 1] - table[index]);
+    }
+    return x;
+}
+
+__global__ __launch_bounds__(256) void k_geglu(float *gate, const float *up, int width, int up_stride,
+                                               size_t total, const float *__restrict__ table,
+                                               int size, float lower, float upper) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const size_t r = i / width, c = i % width;
+    const float x = gelu_table_lookup(gate[i], table, size, lower, upper);
+    gate[i] = x * up[r * up_stride + c];
+}
+
+void launch_geglu(hipStream_t s, float *gate, const float *up, int rows, int width, int up_stride,
+                  const float *table, int table_size, float lower, float upper) {
+    const size_t total = (size_t)rows * width;
+    if (!total) return;
+    hipLaunchKernelGGL(k_geglu, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, gate, up,
+                       width, up_stride, total, table, table_size, lower, upper);
+}
+
+// gemma4.c:337-358, one thread per output value.
+__global__ __launch_bounds__(256) void k_embedding(float *out, const int8_t *__restrict__ table,
+                                                   const uint16_t *__restrict__ scales, int width,
+                                                   int table_rows, const int *__restrict__ tokens,
+                                                   size_t total, float multiplier) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const size_t t = i / width;
+    const int e = (int)(i % width), g = e >> 6, j = e & 63;
+    const int token = tokens[t];
+    if (token < 0 || token >= table_rows) {  // never read outside the table
+        out[i] = __int_as_float(0x7fc00000);
+        return;
+    }
+    const size_t block = (size_t)(token / 16);
+    const int row = token % 16, groups = width / 64;
+    const int8_t qv = table[block * 16 * width + (size_t)g * 1024 + (j / 4) * 64 + row * 4 + (j & 3)];
+    const float s = half_bits_to_float(scales[(block * groups + g) * 16 + row]) * multiplier;
+    out[i] = (float)qv * s;
+}
+
+void launch_embedding(hipStream_t s, float *out, const int8_t *table, const uint16_t *scales,
+                      int width, int table_rows, const int *tokens, size_t n, float multiplier) {
+    const size_t total = n * (size_t)width;
+    if (!total) return;
+    hipLaunchKernelGGL(k_embedding, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, out,
+                       table, scales, width, table_rows, tokens, total, multiplier);
+}
+
+// gemma4.c:437-440: new keys get rmsnorm(k_norm) then RoPE, new values a
+// weightless rmsnorm; rows land in the rings at (start_pos + t) & mask.
+__global__ __launch_bounds__(256) void k_kv_finish(float *key_cache, float *value_cache,
+                                                   const float *k_new, const float *v_new,
+                                                   const float *__restrict__ k_norm,
+                                                   const float *__restrict__ cosines,
+                                                   const float *__restrict__ sines, int pairs,
+                                                   int head_dim, int cache_len, int start_pos) {
+    __shared__ float red[4];
+    __shared__ float row[512];
+    const int t = blockIdx.x, is_value = blockIdx.y;
+    const float *x = (is_value ? v_new : k_new) + (size_t)t * head_dim;
+    const float *weight = is_value ? nullptr : k_norm;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < head_dim; i += 256) s += x[i] * x[i];
+    s = block_sum256(s, red);
+    const float inverse = 1.0f / sqrtf(s / (float)head_dim + 1e-6f);
+    for (int i = threadIdx.x; i < head_dim; i += 256)
+        row[i] = (weight ? weight[i] : 1.0f) * (inverse * x[i]);
+    __syncthreads();
+    const int pos = start_pos + t;
+    float *dst = (is_value ? value_cache : key_cache) + (size_t)(pos & (cache_len - 1)) * head_dim;
+    if (!is_value) {
+        const float *c = cosines + (size_t)pos * pairs, *sn = sines + (size_t)pos * pairs;
+        for (int i = threadIdx.x; i < head_dim; i += 256) {
+            float v = row[i];
+            const int half = head_dim / 2;
+            if (i < pairs) {
+                v = row[i] * c[i] - row[i + half] * sn[i];
+            } else if (i >= half && i - half < pairs) {
+                const int j = i - half;
+                v = row[i] * c[j] + row[j] * sn[j];
+            }
+            dst[i] = v;
+        }
+    } else {
+        for (int i = threadIdx.x; i < head_dim; i += 256) dst[i] = row[i];
+    }
+}
+
+void launch_kv_finish(hipStream_t s, float *key_cache, float *value_cache, const float *k_new,
+                      const float *v_new, const float *k_norm, const float *cosines,
+                      const float *sines, int pairs, int head_dim, int cache_len, int start_pos,
+                      size_t n) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_kv_finish, dim3((unsigned)n, 2), dim3(256), 0, s, key_cache, value_cache,
+                       k_new, v_new, k_norm, cosines, sines, pairs, head_dim, cache_len, start_pos);
+}
+
+__global__ __launch_bounds__(256) void k_softcap(float *x, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = 30.0f * tanhf(x[i] / 30.0f);
+}
+
+void launch_softcap(hipStream_t s, float *x, size_t n) {
+    if (!n) return;
+    hipLaunchKernelGGL(k_softcap, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n);
+}
+
+// First index of the row maximum (strict '>' scan of gemma4.c:537-541).
+__global__ __launch_bounds__(256) void k_argmax(int *out, const float *x, size_t width) {
+    const float *r = x + (size_t)blockIdx.x * width;
+    float best = -INFINITY;
+    int index = -1;
+    for (size_t i = threadIdx.x; i < width; i += 256)
+        if (index < 0 || r[i] > best) {
+            best = r[i];
+            index = (int)i;
+        }
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    sv[threadIdx.x] = best;
+    si[threadIdx.x] = index;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            const float v2 = sv[threadIdx.x + o];
+            const int i2 = si[threadIdx.x + o];
+            const float v1 = sv[threadIdx.x];
+            const int i1 = si[threadIdx.x];
+            if (i2 >= 0 && (i1 < 0 || v2 > v1 || (v2 == v1 && i2 < i1))) {
+                sv[threadIdx.x] = v2;
+                si[threadIdx.x] = i2;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = si[0];
+}
+
+void launch_argmax(hipStream_t s, int *out, const float *x, size_t rows, size_t width) {
+    if (!rows) return;
+    hipLaunchKernelGGL(k_argmax, dim3((unsigned)rows), dim3(256), 0, s, out, x, width);
+}
+
+// ---------------------------------------------------------------------------
+// Attention (gemma4.c:443-456) as split-KV flash decoding over the ring cache.
+//
+// Phase 1: one 256-thread block per (query token, chunk of 64 visible keys),
+// all heads at once so every K/V row is read once per block.  Scores follow the
+// reference bit for bit: lane m of a 16-lane group accumulates fma(q_j, k_j)
+// over j = m, m+16, ... and the group sums with the fixed tree
+// ((l + l^8) -> +4 -> +2 -> +1).  Each head's chunk keeps its max m, the sum l
+// of expf(s - m) and o = sum of expf(s - m) * v.
+// Phase 2: per (token, head), rescale the chunks to the global max and divide.
+
+constexpr int kAttnChunk = 64;
+constexpr int kMaxHeads = 8;
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_partial(const float *__restrict__ q,
+                                                      const float *__restrict__ key_cache,
+                                                      const float *__restrict__ value_cache,
+                                                      int cache_len, int heads, int full,
+                                                      int start_pos, int max_chunks,
+                                                      float *__restrict__ part_o,
+                                                      float *__restrict__ part_ml) {
+    __shared__ float s_q[kMaxHeads][HD];
+    __shared__ float s_p[kMaxHeads][kAttnChunk];
+    const int t = blockIdx.y, chunk = blockIdx.x;
+    const int pos = start_pos + t;
+    const int first = !full && pos + 1 > G4_WINDOW ? pos + 1 - G4_WINDOW : 0;
+    const int keys = pos + 1 - first;
+    const int k0 = chunk * kAttnChunk;
+    if (k0 >= keys) return;
+    const int kn = keys - k0 < kAttnChunk ? keys - k0 : kAttnChunk;
+    const int mask = cache_len - 1;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *qt = q + (size_t)t * heads * HD;
+    for (int i = tid; i < heads * HD; i += 256) s_q[i / HD][i % HD] = qt[i];
+    __syncthreads();
+
+    // Scores: 16 lanes per key, 16 keys in flight per block.
+    const int m16 = lane & 15, kg = lane >> 4;
+    for (int kk = wave * 4 + kg; kk < kn; kk += 16) {
+        const float *kr = key_cache + (size_t)((first + k0 + kk) & mask) * HD;
+        float acc[kMaxHeads];
+#pragma unroll
+        for (int h = 0; h < kMaxHeads; h++) acc[h] = 0.0f;
+        for (int j = m16; j < HD; j += 16) {
+            const float kv = kr[j];
+#pragma unroll
+            for (int h = 0; h < kMaxHeads; h++)
+                if (h < heads) acc[h] = fmaf(s_q[h][j], kv, acc[h]);
+        }
+#pragma unroll
+        for (int h = 0; h < kMaxHeads; h++) {
+            float v = acc[h];
+            v += __shfl_down(v, 8, 16);
+            v += __shfl_down(v, 4, 16);
+            v += __shfl_down(v, 2, 16);
+            v += __shfl_down(v, 1, 16);
+            if (m16 == 0 && h < heads) s_p[h][kk] = v;
+        }
+    }
+    __syncthreads();
+
+    // Chunk softmax statistics: wave w takes heads w, w+4.
+    for (int h = wave; h < heads; h += 4) {
+        float m = -INFINITY;
+        for (int i = lane; i < kn; i += 64) m = fmaxf(m, s_p[h][i]);
+        m = wave_max(m);
+        float l = 0.0f;
+        for (int i = lane; i < kn; i += 64) {
+            const float p = expf(s_p[h][i] - m);
+            s_p[h][i] = p;
+            l += p;
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+            float *ml = part_ml + (((size_t)t * max_chunks + chunk) * heads + h) * 2;
+            ml[0] = m;
+            ml[1] = l;
+        }
+    }
+    __syncthreads();
+
+    // Values: thread owns channels tid, tid+256, ... for every head.
+    constexpr int PER = (HD + 255) / 256;
+    float o[kMaxHeads][PER];
+#pragma unroll
+    for (int h = 0; h < kMaxHeads; h++)
+#pragma unroll
+        for (int e = 0; e < PER; e++) o[h][e] = 0.0f;
+    for (int k = 0; k < kn; k++) {
+        const float *vr = value_cache + (size_t)((first + k0 + k) & mask) * HD;
+#pragma unroll
+        for (int e = 0; e < PER; e++) {
+            const int d = tid + e * 256;
+            if (d < HD) {
+                const float vv = vr[d];
+#pragma unroll
+                for (int h = 0; h < kMaxHeads; h++)
+                    if (h < heads) o[h][e] = fmaf(s_p[h][k], vv, o[h][e]);
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < kMaxHeads; h++) {
+        if (h >= heads) break;
+        float *dst = part_o + (((size_t)t * max_chunks + chunk) * heads + h) * HD;
+#pragma unroll
+        for (int e = 0; e < PER; e++) {
+            const int d = tid + e * 256;
+            if (d < HD) dst[d] = o[h][e];
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_attn_combine(float *__restrict__ out,
+                                                      const float *__restrict__ part_o,
+                                                      const float *__restrict__ part_ml,
+                                                      int head_dim, int heads, int full,
+                                                      int start_pos, int max_chunks) {
+    extern __shared__ float s_w[];
+    __shared__ float red[4];
+    const int h = blockIdx.x, t = blockIdx.y;
+    const int pos = start_pos + t;
+    const int first = !full && pos + 1 > G4_WINDOW ? pos + 1 - G4_WINDOW : 0;
+    const int keys = pos + 1 - first;
+    const int chunks = (keys + kAttnChunk - 1) / kAttnChunk;
+    const float *ml = part_ml + ((size_t)t * max_chunks * heads + h) * 2;
+    float m = -INFINITY;
+    for (int c = threadIdx.x; c < chunks; c += 256) m = fmaxf(m, ml[(size_t)c * heads * 2]);
+    m = wave_max(m);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float l = 0.0f;
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        const float wgt = expf(ml[(size_t)c * heads * 2] - m);
+        s_w[c] = wgt;
+        l += ml[(size_t)c * heads * 2 + 1] * wgt;
+    }
+    l = block_sum256(l, red);
+    for (int d = threadIdx.x; d < head_dim; d += 256) {
+        float acc = 0.0f;
+        for (int c = 0; c < chunks; c++)
+            acc = fmaf(part_o[(((size_t)t * max_chunks + c) * heads + h) * head_dim + d], s_w[c], acc);
+        out[((size_t)t * heads + h) * head_dim + d] = acc / l;
+    }
+}
+
+int launch_attend(hipStream_t s, float *out, const float *q, const float *key_cache,
+                  const float *value_cache, int cache_len, int head_dim, int heads, int full,
+                  int start_pos, size_t n) {
+    if (!n) return G4_OK;
+    const int last_pos = start_pos + (int)n - 1;
+    const int max_keys = full ? last_pos + 1 : (last_pos + 1 < G4_WINDOW ? last_pos + 1 : G4_WINDOW);
+    const int max_chunks = (max_keys + kAttnChunk - 1) / kAttnChunk;
+    const size_t o_floats = n * (size_t)max_chunks * heads * head_dim;
+    const size_t ml_floats = n * (size_t)max_chunks * heads * 2;
+    int rc = scratch_reserve(0, 0, (o_floats + ml_floats) * sizeof(float));
+    if (rc) return rc;
+    float *part_o = scratch().attn, *part_ml = part_o + o_floats;
+    dim3 grid1((unsigned)max_chunks, (unsigned)n);
+    if (head_dim == 256)
+        hipLaunchKernelGGL(k_attn_partial<256>, grid1, dim3(256), 0, s, q, key_cache, value_cache,
+                           cache_len, heads, full, start_pos, max_chunks, part_o, part_ml);
+    else
+        hipLaunchKernelGGL(k_attn_partial<512>, grid1, dim3(256), 0, s, q, key_cache, value_cache,
+                           cache_len, heads, full, start_pos, max_chunks, part_o, part_ml);
+    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)heads, (unsigned)n), dim3(256),
+                       (size_t)max_chunks * sizeof(float), s, out, part_o, part_ml, head_dim,
+                       heads, full, start_pos, max_chunks);
+    return G4_OK;
+}
+
+}  // namespace g4
+
+// ---------------------------------------------------------------------------
+// Per-op entry points (include/g4.h)
+
+using namespace g4;
+
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+extern "C" int g4_quantize(void *stream, int8_t *q, float *scales, const float *x, size_t rows,
+                           size_t width) {
+    G4_CHECK(q && scales && x, "g4_quantize: null pointer");
+    G4_CHECK(width % 64 == 0, "g4_quantize: width %zu is not a multiple of 64", width);
+    G4_CHECK(aligned16(x) && aligned16(q), "g4_quantize: x and q must be 16-byte aligned");
+    launch_quantize((hipStream_t)stream, q, scales, x, rows * (width / 64));
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+extern "C" int g4_matmul_int8(void *stream, float *out, const int8_t *xq, const float *xs,
+                              const g4_tensor *w, size_t rows) {
+    G4_CHECK(out && xq && xs && w && w->data && w->scales, "g4_matmul_int8: null pointer");
+    const int n = w->shape[0], k = w->shape[1];
+    G4_CHECK(n > 0 && k > 0 && n % 16 == 0 && k % 64 == 0,
+             "g4_matmul_int8: weight shape %d x %d is not packable", n, k);
+    G4_CHECK(rows <= (size_t)1 << 24, "g4_matmul_int8: too many rows");
+    G4_CHECK(aligned16(xq) && aligned16(w->data), "g4_matmul_int8: xq and data must be 16-byte aligned");
+    int rc = launch_matmul((hipStream_t)stream, out, (size_t)n, xq, xs, (const int8_t *)w->data,
+                           w->scales, n, k, (int)rows);
+    if (rc) return rc;
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+extern "C" int g4_rmsnorm(void *stream, float *out, const float *in, const float *weight,
+                          int width, float epsilon, size_t rows) {
+    G4_CHECK(out && in && width > 0, "g4_rmsnorm: bad arguments");
+    launch_rmsnorm((hipStream_t)stream, out, in, weight, width, epsilon, rows);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+extern "C" int g4_add_and_scale(void *stream, float *out, const float *add, size_t n, float scale) {
+    G4_CHECK(out && add, "g4_add_and_scale: null pointer");
+    launch_add_and_scale((hipStream_t)stream, out, add, n, scale);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+extern "C" int g4_apply_rope(void *stream, const float *cosines, const float *sines, int pairs,
+                             float *v, int heads, int head_dim, int start_pos, size_t n) {
+    G4_CHECK(cosines && sines && v, "g4_apply_rope: null pointer");
+    G4_CHECK(heads > 0 && head_dim > 0 && head_dim % 2 == 0 && pairs >= 0 && pairs <= head_dim / 2,
+             "g4_apply_rope: bad geometry");
+    G4_CHECK(start_pos >= 0, "g4_apply_rope: negative position");
+    launch_rope((hipStream_t)stream, cosines, sines, pairs, v, heads, head_dim, start_pos, n);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+extern "C" int g4_geglu(void *stream, float *gate, const float *up, int rows, int width,
+                        int up_stride, const float *table, int table_size, float lower,
+                        float upper) {
+    G4_CHECK(gate && up && table, "g4_geglu: null pointer");
+    G4_CHECK(rows >= 0 && width >= 0 && up_stride >= width && table_size >= 2 && upper > lower,
+             "g4_geglu: bad arguments");
+    launch_geglu((hipStream_t)stream, gate, up, rows, width, up_stride, table, table_size, lower,
+                 upper);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+extern "C" int g4_embedding(void *stream, float *out, const g4_tensor *table, const int *tokens,
+                            size_t n, float multiplier) {
+    G4_CHECK(out && table && table->data && table->scales && tokens, "g4_embedding: null pointer");
+    G4_CHECK(table->shape[0] % 16 == 0 && table->shape[1] % 64 == 0 && table->shape[1] > 0,
+             "g4_embedding: table is not packed");
+    launch_embedding((hipStream_t)stream, out, (const int8_t *)table->data, table->scales,
+                     table->shape[1], table->shape[0], tokens, n, multiplier);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+extern "C" int g4_attend(void *stream, float *out, const float *q, const float *key_cache,
+                         const float *value_cache, int cache_len, int head_dim, int heads,
+                         int full_attention, int start_pos, size_t n) {
+    G4_CHECK(out && q && key_cache && value_cache, "g4_attend: null pointer");
+    G4_CHECK(head_dim == 256 || head_dim == 512, "g4_attend: head_dim must be 256 or 512");
+    G4_CHECK(heads >= 1 && heads <= 8, "g4_attend: heads must be 1..8");
+    G4_CHECK(cache_len > 0 && (cache_len & (cache_len - 1)) == 0, "g4_attend: cache_len must be a power of two");
+    G4_CHECK(start_pos >= 0, "g4_attend: negative position");
+    // Keys visible to the batch span positions max(0, start_pos - 511) ..
+    // start_pos + n - 1 (sliding) or 0 .. start_pos + n - 1 (full); the ring
+    // must hold them all.
+    const long span = full_attention ? (long)start_pos + (long)n
+                                     : (long)(start_pos < G4_WINDOW - 1 ? start_pos : G4_WINDOW - 1) + (long)n;
+    G4_CHECK(span <= cache_len, "g4_attend: %ld visible keys exceed the %d-row ring", span, cache_len);
+    int rc = launch_attend((hipStream_t)stream, out, q, key_cache, value_cache, cache_len, head_dim,
+                           heads, full_attention, start_pos, n);
+    if (rc) return rc;
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}

@@ -1,0 +1,459 @@
+// g4_model.hip -- the device-resident model context behind g4_init /
+// g4_forward / g4_logits (include/g4.h).
+//
+// Weights are uploaded once into one HBM arena in the exporter's packed layout
+// (the same bytes as the .bin); the fp32 KV rings (3 global owners x 131072 x
+// 512, 12 sliding owners x 1024 x 256, keys then values) and every activation
+// live on the device, so a token step moves only token ids in and one logits
+// row (or one argmax) out.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <vector>
+
+#include "g4_internal.h"
+
+namespace g4 {
+
+static char g_error[512] = "no error";
+
+int set_error(int status, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof(g_error), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+struct Weight {
+    const int8_t *data = nullptr;
+    const uint16_t *scales = nullptr;
+    int n = 0, k = 0;
+};
+
+struct Layer {
+    const float *input_ln, *post_attn_ln, *pre_ffn_ln, *post_ffn_ln, *post_ple_ln, *q_norm, *k_norm;
+    Weight q, k, v, o, gate, up, down, ple_gate, ple_proj;
+    const float *rope_cos, *rope_sin;
+    int pairs, head_dim, query_width, full, owner, ffn;
+    float layer_scalar;
+};
+
+struct Context {
+    bool ready = false;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    char *arena = nullptr;
+    Layer layers[G4_LAYERS];
+    Weight embed, embed_ple, ple_model_proj;
+    const float *final_norm = nullptr, *ple_norm = nullptr, *gelu = nullptr;
+    int gelu_size = 0;
+    float gelu_lower = 0, gelu_upper = 0;
+    float *residual = nullptr, *hidden = nullptr, *aux = nullptr, *ple = nullptr;
+    float *k_new = nullptr, *v_new = nullptr, *logits = nullptr, *logits_all = nullptr;
+    int8_t *q8 = nullptr;
+    float *qs = nullptr;
+    float *cache[15] = {};
+    int cache_len[15] = {}, cache_dim[15] = {};
+    int *tokens_dev = nullptr, *argmax_dev = nullptr;
+    int *tokens_pinned = nullptr;
+    int last_n = 0;
+};
+
+static Context g_ctx;
+
+static size_t record_bytes(const g4_tensor &t, int index, size_t *scale_bytes) {
+    *scale_bytes = 0;
+    if (!t.data) return 0;
+    if (t.scales) {
+        const size_t count = (size_t)t.shape[0] * (size_t)t.shape[1];
+        *scale_bytes = count / 64 * 2;
+        return count;
+    }
+    if (index == G4_RECORDS - 1) return (size_t)t.shape[0] * 4;  // GELU table (4096, lo, hi)
+    return (size_t)t.shape[0] * (size_t)(t.shape[1] > 0 ? t.shape[1] : 1) * 4;
+}
+
+static size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static void release(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+static void free_all(Context &c) {
+    if (c.stream) (void)hipStreamSynchronize(c.stream);
+    release(c.arena);
+    release(c.residual);
+    release(c.hidden);
+    release(c.aux);
+    release(c.ple);
+    release(c.k_new);
+    release(c.v_new);
+    release(c.logits);
+    release(c.logits_all);
+    release(c.q8);
+    release(c.qs);
+    for (int i = 0; i < 15; i++) release(c.cache[i]);
+    release(c.tokens_dev);
+    release(c.argmax_dev);
+    if (c.tokens_pinned) (void)hipHostFree(c.tokens_pinned);
+    if (c.stream) (void)hipStreamDestroy(c.stream);
+    c = Context();
+}
+
+static int check_weight(const g4_tensor &t, int n, int k, const char *what, int layer) {
+    if (!t.data || !t.scales || t.shape[0] != n || t.shape[1] != k)
+        return set_error(G4_ERR_ARG, "g4_init: %s of layer %d must be an int8 [%d x %d] record (got %d x %d)",
+                         what, layer, n, k, t.shape[0], t.shape[1]);
+    return G4_OK;
+}
+
+static int check_vector(const g4_tensor &t, int n, const char *what, int layer) {
+    if (!t.data || t.scales || t.shape[0] != n)
+        return set_error(G4_ERR_ARG, "g4_init: %s of layer %d must be fp32 [%d]", what, layer, n);
+    return G4_OK;
+}
+
+#define G4_TRY(x)                  \
+    do {                           \
+        int rc_ = (x);             \
+        if (rc_) return rc_;       \
+    } while (0)
+
+// Shape checks for everything the forward pass relies on (the reference trusts
+// the image; gemma4.c:414-421, 464, 131-140 of exporter.py).
+static int validate(const g4_tensor *r) {
+    G4_TRY(check_weight(r[0], G4_VOCAB, G4_HIDDEN, "embed", -1));
+    G4_TRY(check_weight(r[1], G4_VOCAB, G4_LAYERS * G4_PLE, "embed_per_layer", -1));
+    G4_TRY(check_vector(r[667], G4_HIDDEN, "norm", -1));
+    G4_TRY(check_weight(r[668], G4_LAYERS * G4_PLE, G4_HIDDEN, "per_layer_model_projection", -1));
+    G4_TRY(check_vector(r[669], G4_PLE, "per_layer_projection_norm", -1));
+    const g4_tensor &gelu = r[670];
+    if (!gelu.data || gelu.scales || gelu.shape[0] < 2 || gelu.shape[2] <= gelu.shape[1])
+        return set_error(G4_ERR_ARG, "g4_init: bad GELU table record");
+    bool have_sliding_owner = false, have_full_owner = false;
+    for (int l = 0; l < G4_LAYERS; l++) {
+        const g4_tensor *f = r + 2 + l * 19;
+        const int full = l % 5 == 4;
+        const int hd = f[8].shape[0];
+        if (hd != (full ? 512 : 256))
+            return set_error(G4_ERR_ARG, "g4_init: q_norm of layer %d has width %d", l, hd);
+        G4_TRY(check_vector(f[0], G4_HIDDEN, "input_layernorm", l));
+        if (!f[1].data) return set_error(G4_ERR_ARG, "g4_init: layer %d has no layer_scalar", l);
+        G4_TRY(check_vector(f[2], G4_HIDDEN, "pre_ffn_layernorm", l));
+        G4_TRY(check_vector(f[3], G4_HIDDEN, "post_attn_layernorm", l));
+        G4_TRY(check_vector(f[4], G4_HIDDEN, "post_ffn_layernorm", l));
+        G4_TRY(check_vector(f[5], G4_HIDDEN, "post_per_layer_input_norm", l));
+        G4_TRY(check_weight(f[6], G4_PLE, G4_HIDDEN, "per_layer_input_gate", l));
+        G4_TRY(check_weight(f[7], G4_HIDDEN, G4_PLE, "per_layer_projection", l));
+        G4_TRY(check_vector(f[8], hd, "q_norm", l));
+        G4_TRY(check_weight(f[10], G4_HEADS * hd, G4_HIDDEN, "q_proj", l));
+        if (f[11].data) {
+            G4_TRY(check_vector(f[9], hd, "k_norm", l));
+            G4_TRY(check_weight(f[11], hd, G4_HIDDEN, "k_proj", l));
+            G4_TRY(check_weight(f[12], hd, G4_HIDDEN, "v_proj", l));
+            if (l >= 15) return set_error(G4_ERR_ARG, "g4_init: layer %d owns K/V; only layers 0-14 may", l);
+            (full ? have_full_owner : have_sliding_owner) = true;
+        } else if (!(full ? have_full_owner : have_sliding_owner)) {
+            return set_error(G4_ERR_ARG, "g4_init: layer %d has no earlier K/V owner of its type", l);
+        }
+        G4_TRY(check_weight(f[13], G4_HIDDEN, G4_HEADS * hd, "o_proj", l));
+        const int ffn = f[14].shape[0];
+        G4_TRY(check_weight(f[14], ffn, G4_HIDDEN, "gate_proj", l));
+        G4_TRY(check_weight(f[15], ffn, G4_HIDDEN, "up_proj", l));
+        G4_TRY(check_weight(f[16], G4_HIDDEN, ffn, "down_proj", l));
+        if (ffn > 8 * G4_HIDDEN || ffn % 64)
+            return set_error(G4_ERR_ARG, "g4_init: FFN width %d of layer %d unsupported", ffn, l);
+        const int pairs = f[17].shape[1];
+        if (!f[17].data || !f[18].data || f[17].shape[0] < G4_MAX_CONTEXT || pairs <= 0 || pairs > hd / 2 ||
+            f[18].shape[1] != pairs)
+            return set_error(G4_ERR_ARG, "g4_init: bad RoPE tables for layer %d", l);
+    }
+    return G4_OK;
+}
+
+static int init(const g4_tensor *records, int device) {
+    Context &c = g_ctx;
+    int count = 0;
+    G4_HIP(hipGetDeviceCount(&count));
+    G4_CHECK(device >= 0 && device < count, "g4_init: device %d not present (%d devices)", device, count);
+    G4_TRY(validate(records));
+    c.device = device;
+    G4_HIP(hipSetDevice(device));
+    G4_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+
+    // One arena for all weights; records that share host data (the RoPE
+    // tables) share device data.
+    std::map<const void *, size_t> offsets;
+    size_t total = 0;
+    for (int i = 0; i < G4_RECORDS; i++) {
+        size_t sb = 0, db = record_bytes(records[i], i, &sb);
+        if (!db || offsets.count(records[i].data)) continue;
+        offsets[records[i].data] = total;
+        total += round256(db);
+        if (sb) {
+            offsets[records[i].scales] = total;
+            total += round256(sb);
+        }
+    }
+    G4_HIP(hipMalloc(&c.arena, total));
+    for (int i = 0; i < G4_RECORDS; i++) {
+        size_t sb = 0, db = record_bytes(records[i], i, &sb);
+        if (!db) continue;
+        G4_HIP(hipMemcpy(c.arena + offsets[records[i].data], records[i].data, db, hipMemcpyHostToDevice));
+        if (sb)
+            G4_HIP(hipMemcpy(c.arena + offsets[records[i].scales], records[i].scales, sb,
+                             hipMemcpyHostToDevice));
+    }
+    auto dev_f = [&](const g4_tensor &t) -> const float * {
+        return t.data ? (const float *)(c.arena + offsets[t.data]) : nullptr;
+    };
+    auto dev_w = [&](const g4_tensor &t) {
+        Weight w;
+        if (!t.data) return w;
+        w.data = (const int8_t *)(c.arena + offsets[t.data]);
+        w.scales = (const uint16_t *)(c.arena + offsets[t.scales]);
+        w.n = t.shape[0];
+        w.k = t.shape[1];
+        return w;
+    };
+    c.embed = dev_w(records[0]);
+    c.embed_ple = dev_w(records[1]);
+    c.final_norm = dev_f(records[667]);
+    c.ple_model_proj = dev_w(records[668]);
+    c.ple_norm = dev_f(records[669]);
+    c.gelu = dev_f(records[670]);
+    c.gelu_size = records[670].shape[0];
+    c.gelu_lower = (float)records[670].shape[1];
+    c.gelu_upper = (float)records[670].shape[2];
+    for (int l = 0; l < G4_LAYERS; l++) {
+        const g4_tensor *f = records + 2 + l * 19;
+        Layer &L = c.layers[l];
+        L.input_ln = dev_f(f[0]);
+        L.layer_scalar = ((const float *)f[1].data)[0];
+        L.pre_ffn_ln = dev_f(f[2]);
+        L.post_attn_ln = dev_f(f[3]);
+        L.post_ffn_ln = dev_f(f[4]);
+        L.post_ple_ln = dev_f(f[5]);
+        L.ple_gate = dev_w(f[6]);
+        L.ple_proj = dev_w(f[7]);
+        L.q_norm = dev_f(f[8]);
+        L.k_norm = dev_f(f[9]);
+        L.q = dev_w(f[10]);
+        L.k = dev_w(f[11]);
+        L.v = dev_w(f[12]);
+        L.o = dev_w(f[13]);
+        L.gate = dev_w(f[14]);
+        L.up = dev_w(f[15]);
+        L.down = dev_w(f[16]);
+        L.rope_cos = dev_f(f[17]);
+        L.rope_sin = dev_f(f[18]);
+        L.pairs = f[17].shape[1];
+        L.head_dim = f[8].shape[0];
+        L.query_width = f[10].shape[0];
+        L.full = l % 5 == 4;
+        L.ffn = f[14].shape[0];
+        int owner = l;  // gemma4.c:419-420
+        while (!records[2 + owner * 19 + 11].data || (owner % 5 == 4) != L.full) owner--;
+        L.owner = owner;
+    }
+
+    const size_t wide = (size_t)G4_BATCH * 8 * G4_HIDDEN;
+    G4_HIP(hipMalloc(&c.residual, (size_t)G4_BATCH * G4_HIDDEN * sizeof(float)));
+    G4_HIP(hipMalloc(&c.hidden, wide * sizeof(float)));
+    G4_HIP(hipMalloc(&c.aux, wide * sizeof(float)));
+    G4_HIP(hipMalloc(&c.ple, (size_t)G4_BATCH * G4_LAYERS * G4_PLE * sizeof(float)));
+    G4_HIP(hipMalloc(&c.k_new, (size_t)G4_BATCH * 512 * sizeof(float)));
+    G4_HIP(hipMalloc(&c.v_new, (size_t)G4_BATCH * 512 * sizeof(float)));
+    G4_HIP(hipMalloc(&c.logits, (size_t)G4_VOCAB * sizeof(float)));
+    G4_HIP(hipMalloc(&c.q8, wide));
+    G4_HIP(hipMalloc(&c.qs, wide / 64 * sizeof(float)));
+    for (int l = 0; l < 15; l++) {
+        if (!records[2 + l * 19 + 11].data) continue;
+        const int full = l % 5 == 4;
+        c.cache_len[l] = full ? G4_MAX_CONTEXT : G4_WINDOW + G4_BATCH;
+        c.cache_dim[l] = full ? 512 : 256;
+        const size_t bytes = 2 * (size_t)c.cache_len[l] * c.cache_dim[l] * sizeof(float);
+        G4_HIP(hipMalloc(&c.cache[l], bytes));
+        G4_HIP(hipMemset(c.cache[l], 0, bytes));
+    }
+    G4_HIP(hipMalloc(&c.tokens_dev, G4_BATCH * sizeof(int)));
+    G4_HIP(hipMalloc(&c.argmax_dev, G4_BATCH * sizeof(int)));
+    G4_HIP(hipHostMalloc((void **)&c.tokens_pinned, G4_BATCH * sizeof(int), hipHostMallocDefault));
+    // Split-K scratch for the widest few-row product (1536 x 12288) and the
+    // decode attention partials for a full-length context.
+    G4_TRY(scratch_reserve((size_t)G4_HIDDEN * (8 * G4_HIDDEN / 64) * 8 * sizeof(int32_t),
+                           (size_t)G4_VOCAB / 16,
+                           (size_t)(G4_MAX_CONTEXT / 64) * 8 * (512 + 2) * sizeof(float)));
+    G4_HIP(hipDeviceSynchronize());
+    c.ready = true;
+    return G4_OK;
+}
+
+static int matmul(Context &c, float *out, size_t stride, const Weight &w, int rows) {
+    return launch_matmul(c.stream, out, stride, c.q8, c.qs, w.data, w.scales, w.n, w.k, rows);
+}
+
+// The sequence of gemma4.c:463-509 (attention: 411-461).
+static int forward(Context &c, const int *tokens, int n, int start_pos) {
+    hipStream_t s = c.stream;
+    memcpy(c.tokens_pinned, tokens, (size_t)n * sizeof(int));
+    G4_HIP(hipMemcpyAsync(c.tokens_dev, c.tokens_pinned, (size_t)n * sizeof(int),
+                          hipMemcpyHostToDevice, s));
+    const int ple_width = G4_LAYERS * G4_PLE;
+
+    launch_embedding(s, c.residual, c.embed.data, c.embed.scales, G4_HIDDEN, c.embed.n, c.tokens_dev,
+                     n, sqrtf((float)G4_HIDDEN));
+    launch_quantize(s, c.q8, c.qs, c.residual, (size_t)n * G4_HIDDEN / 64);
+    G4_TRY(matmul(c, c.ple, ple_width, c.ple_model_proj, n));
+    launch_rmsnorm(s, c.ple, c.ple, c.ple_norm, G4_PLE, 1e-6f * G4_HIDDEN, (size_t)n * G4_LAYERS);
+    launch_embedding(s, c.hidden, c.embed_ple.data, c.embed_ple.scales, ple_width, c.embed_ple.n,
+                     c.tokens_dev, n, sqrtf((float)G4_PLE));
+    launch_add_and_scale(s, c.ple, c.hidden, (size_t)n * ple_width, 1.0f / sqrtf(2.0f));
+
+    for (int l = 0; l < G4_LAYERS; l++) {
+        const Layer &L = c.layers[l];
+        const int hd = L.head_dim, qw = L.query_width, heads = qw / hd;
+        launch_rmsnorm(s, c.hidden, c.residual, L.input_ln, G4_HIDDEN, 1e-6f, n);
+
+        // attention
+        launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_HIDDEN / 64);
+        G4_TRY(matmul(c, c.aux, qw, L.q, n));
+        launch_rmsnorm(s, c.aux, c.aux, L.q_norm, hd, 1e-6f, (size_t)n * heads);
+        launch_rope(s, L.rope_cos, L.rope_sin, L.pairs, c.aux, heads, hd, start_pos, n);
+        float *keys = c.cache[L.owner];
+        const int cache_len = c.cache_len[L.owner];
+        float *values = keys + (size_t)cache_len * hd;
+        if (L.k.data) {
+            G4_TRY(matmul(c, c.k_new, hd, L.k, n));
+            G4_TRY(matmul(c, c.v_new, hd, L.v, n));
+            launch_kv_finish(s, keys, values, c.k_new, c.v_new, L.k_norm, L.rope_cos, L.rope_sin,
+                             L.pairs, hd, cache_len, start_pos, n);
+        }
+        G4_TRY(launch_attend(s, c.hidden, c.aux, keys, values, cache_len, hd, heads, L.full,
+                             start_pos, n));
+        launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * qw / 64);
+        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.o, n));
+        launch_rmsnorm(s, c.hidden, c.hidden, L.post_attn_ln, G4_HIDDEN, 1e-6f, n);
+        launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, 1.0f);
+
+        // feed-forward
+        launch_rmsnorm(s, c.hidden, c.residual, L.pre_ffn_ln, G4_HIDDEN, 1e-6f, n);
+        launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_HIDDEN / 64);
+        G4_TRY(matmul(c, c.hidden, L.ffn, L.gate, n));
+        G4_TRY(matmul(c, c.aux, L.ffn, L.up, n));
+        launch_geglu(s, c.hidden, c.aux, n, L.ffn, L.ffn, c.gelu, c.gelu_size, c.gelu_lower,
+                     c.gelu_upper);
+        launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * L.ffn / 64);
+        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.down, n));
+        launch_rmsnorm(s, c.hidden, c.hidden, L.post_ffn_ln, G4_HIDDEN, 1e-6f, n);
+        launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, 1.0f);
+
+        // per-layer embedding
+        launch_quantize(s, c.q8, c.qs, c.residual, (size_t)n * G4_HIDDEN / 64);
+        G4_TRY(matmul(c, c.hidden, G4_PLE, L.ple_gate, n));
+        launch_geglu(s, c.hidden, c.ple + (size_t)l * G4_PLE, n, G4_PLE, ple_width, c.gelu,
+                     c.gelu_size, c.gelu_lower, c.gelu_upper);
+        launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_PLE / 64);
+        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.ple_proj, n));
+        launch_rmsnorm(s, c.hidden, c.hidden, L.post_ple_ln, G4_HIDDEN, 1e-6f, n);
+        launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, L.layer_scalar);
+    }
+    G4_HIP(hipGetLastError());
+    G4_HIP(hipStreamSynchronize(s));
+    c.last_n = n;
+    return G4_OK;
+}
+
+// gemma4.c:512-522 for `rows` consecutive rows starting at `row`, into dst.
+static int logits_rows(Context &c, float *dst, size_t row, int rows) {
+    hipStream_t s = c.stream;
+    launch_rmsnorm(s, c.aux, c.residual + row * G4_HIDDEN, c.final_norm, G4_HIDDEN, 1e-6f, rows);
+    launch_quantize(s, c.q8, c.qs, c.aux, (size_t)rows * G4_HIDDEN / 64);
+    G4_TRY(matmul(c, dst, G4_VOCAB, c.embed, rows));
+    launch_softcap(s, dst, (size_t)rows * G4_VOCAB);
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" const char *g4_last_error(void) { return g4::g_error; }
+
+extern "C" int g4_init(const g4_tensor *records, int device) {
+    G4_CHECK(records, "g4_init: null records");
+    if (g_ctx.ready) return set_error(G4_ERR_STATE, "g4_init: already initialised (call g4_shutdown first)");
+    int rc = init(records, device);
+    if (rc) {
+        char saved[sizeof(g_error)];
+        memcpy(saved, g_error, sizeof(saved));
+        free_all(g_ctx);
+        memcpy(g_error, saved, sizeof(saved));
+    }
+    return rc;
+}
+
+extern "C" int g4_forward(const int *tokens, size_t token_count, int start_pos) {
+    Context &c = g_ctx;
+    if (!c.ready) return set_error(G4_ERR_STATE, "g4_forward: g4_init has not succeeded");
+    G4_CHECK(tokens, "g4_forward: null tokens");
+    G4_CHECK(token_count >= 1 && token_count <= G4_BATCH, "g4_forward: token_count %zu not in 1..%d",
+             token_count, G4_BATCH);
+    G4_CHECK(start_pos >= 0 && (long)start_pos + (long)token_count <= G4_MAX_CONTEXT,
+             "g4_forward: positions %d..%ld exceed the %d-token context", start_pos,
+             (long)start_pos + (long)token_count - 1, G4_MAX_CONTEXT);
+    for (size_t i = 0; i < token_count; i++)
+        G4_CHECK(tokens[i] >= 0 && tokens[i] < G4_VOCAB, "g4_forward: token %d at index %zu out of range",
+                 tokens[i], i);
+    G4_HIP(hipSetDevice(c.device));
+    return forward(c, tokens, (int)token_count, start_pos);
+}
+
+extern "C" int g4_logits(size_t token, float *out) {
+    Context &c = g_ctx;
+    if (!c.ready || !c.last_n) return set_error(G4_ERR_STATE, "g4_logits: no forward pass yet");
+    G4_CHECK(out, "g4_logits: null output");
+    G4_CHECK(token < (size_t)c.last_n, "g4_logits: row %zu not in the last forward (%d rows)", token,
+             c.last_n);
+    G4_HIP(hipSetDevice(c.device));
+    G4_TRY(logits_rows(c, c.logits, token, 1));
+    G4_HIP(hipMemcpyAsync(out, c.logits, G4_VOCAB * sizeof(float), hipMemcpyDeviceToHost, c.stream));
+    G4_HIP(hipStreamSynchronize(c.stream));
+    return G4_OK;
+}
+
+extern "C" int g4_logits_all(float *out) {
+    Context &c = g_ctx;
+    if (!c.ready || !c.last_n) return set_error(G4_ERR_STATE, "g4_logits_all: no forward pass yet");
+    G4_CHECK(out, "g4_logits_all: null output");
+    G4_HIP(hipSetDevice(c.device));
+    if (!c.logits_all) G4_HIP(hipMalloc(&c.logits_all, (size_t)G4_BATCH * G4_VOCAB * sizeof(float)));
+    G4_TRY(logits_rows(c, c.logits_all, 0, c.last_n));
+    G4_HIP(hipMemcpyAsync(out, c.logits_all, (size_t)c.last_n * G4_VOCAB * sizeof(float),
+                          hipMemcpyDeviceToHost, c.stream));
+    G4_HIP(hipStreamSynchronize(c.stream));
+    return G4_OK;
+}
+
+extern "C" int g4_argmax(size_t token, int *out_token) {
+    Context &c = g_ctx;
+    if (!c.ready || !c.last_n) return set_error(G4_ERR_STATE, "g4_argmax: no forward pass yet");
+    G4_CHECK(out_token, "g4_argmax: null output");
+    G4_CHECK(token < (size_t)c.last_n, "g4_argmax: row %zu not in the last forward", token);
+    G4_HIP(hipSetDevice(c.device));
+    G4_TRY(logits_rows(c, c.logits, token, 1));
+    launch_argmax(c.stream, c.argmax_dev, c.logits, 1, G4_VOCAB);
+    G4_HIP(hipMemcpyAsync(out_token, c.argmax_dev, sizeof(int), hipMemcpyDeviceToHost, c.stream));
+    G4_HIP(hipStreamSynchronize(c.stream));
+    return G4_OK;
+}
+
+extern "C" void g4_shutdown(void) {
+    if (g_ctx.ready || g_ctx.arena) free_all(g_ctx);
+}
+
+extern "C" void *g4_stream(void) { return g_ctx.stream; }

@@ -1,0 +1,139 @@
+/*
+ * g4.h -- C ABI of the MI355X (gfx950) W8A8 forward path for gemma4.c.
+ *
+ * Drop-in boundary.  The reference's inference path is a set of plain C
+ * functions called from serial host code (gemma4.c:566, 569, 600, 605, 632-633,
+ * 640-641).  The model-level entry points below replace forward() and logits();
+ * the per-op entry points replace the kernels underneath them and exist so the
+ * parity tests can check each one in isolation.
+ *
+ * Conventions:
+ *   - every function returns G4_OK (0) or a nonzero status; g4_last_error()
+ *     then holds a one-line message (the reference's error style is a message
+ *     on stderr plus exit(1) in its main(); the host keeps that);
+ *   - per-op entry points take DEVICE pointers and a hipStream_t passed as
+ *     void* (NULL = the null stream), and are asynchronous on that stream;
+ *   - model-level entry points take host pointers, run on the library's own
+ *     stream and return when their result is ready;
+ *   - one model context per process, not thread-safe (the reference likewise
+ *     has one Model and one InferenceState).
+ */
+#ifndef G4_H
+#define G4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Shape constants of the reference (gemma4.c:26-31) and its exporter. */
+#define G4_LAYERS 35
+#define G4_HIDDEN 1536
+#define G4_VOCAB 262144
+#define G4_MAX_CONTEXT 131072
+#define G4_WINDOW 512
+#define G4_BATCH 512
+#define G4_PLE 256
+#define G4_HEADS 8
+#define G4_RECORDS 671 /* 2 + 35*19 + 4 tensor records */
+
+#define G4_OK 0
+#define G4_ERR_ARG 1    /* invalid argument (shape, size, null pointer, range) */
+#define G4_ERR_DEVICE 2 /* HIP runtime error or no device */
+#define G4_ERR_STATE 3  /* call order (e.g. forward before init) */
+
+/* One tensor record of the memory image: identical layout to the reference's
+ * Tensor (gemma4.c:119-123), 32 bytes.  Quantized matrices [rows x cols] keep
+ * int8 data in 1024-byte tiles (16 rows x 64 columns; byte (chunk c, row r, j)
+ * at c*64 + r*4 + j) in row-block-major order, and fp16 scales per (row,
+ * 64-column group) ordered [row block][group][16] (exporter.py:304-316).
+ * fp32 tensors have scales == NULL. */
+typedef struct {
+    void *data;
+    uint16_t *scales;
+    int32_t shape[4];
+} g4_tensor;
+
+/* Message for the last nonzero status (never NULL). */
+const char *g4_last_error(void);
+
+/* ---- Model-level entry points ------------------------------------------ */
+
+/* Upload the model once.  `records` is the reference's ModelWeights viewed as
+ * G4_RECORDS tensors (gemma4.c:147-155) with data/scales already turned into
+ * host pointers (gemma4.c:681-685).  Allocates the device KV caches (fp32) and
+ * activations.  Replaces nothing in the reference: it is the new init step a
+ * host calls after its loader (gemma4.c:686). `device` is the HIP ordinal. */
+int g4_init(const g4_tensor *records, int device);
+
+/* Replaces forward() (gemma4.c:463): runs token_count (1..G4_BATCH) tokens at
+ * positions start_pos.. through all 35 layers, updating the device KV caches.
+ * Requires start_pos + token_count <= G4_MAX_CONTEXT. */
+int g4_forward(const int *tokens, size_t token_count, int start_pos);
+
+/* Replaces logits() (gemma4.c:512): final norm, tied lm_head and soft cap for
+ * row `token` (< last token_count) of the last forward; writes G4_VOCAB floats
+ * to host memory `out`. */
+int g4_logits(size_t token, float *out);
+
+/* Logits of every row of the last forward in one batched lm_head pass:
+ * writes token_count x G4_VOCAB floats (row-major) to host memory `out`.  Same
+ * values as calling g4_logits(i, ...) for each row (the --dump-logits loop,
+ * gemma4.c:567-570). */
+int g4_logits_all(float *out);
+
+/* Greedy next token for row `token` (first maximum, gemma4.c:537-541),
+ * computed on the device so only one int crosses the bus. */
+int g4_argmax(size_t token, int *out_token);
+
+/* Free every device resource of the model context. */
+void g4_shutdown(void);
+
+/* The library's HIP stream (a hipStream_t) for timing with HIP events. */
+void *g4_stream(void);
+
+/* ---- Per-op entry points (device pointers) ------------------------------ */
+
+/* gemma4.c:265-279: per 64-value group, scale = max|x|/127, q = rint(x/scale). */
+int g4_quantize(void *stream, int8_t *q, float *scales, const float *x, size_t rows,
+                size_t width);
+
+/* gemma4.c:257-262: out[rows x N] = W8A8 product of the quantized rows with the
+ * packed matrix w (N = w->shape[0], K = w->shape[1]; data/scales are device
+ * pointers).  Output row stride is N. */
+int g4_matmul_int8(void *stream, float *out, const int8_t *xq, const float *xs,
+                   const g4_tensor *w, size_t rows);
+
+/* gemma4.c:360-373: y = w * (x / sqrt(mean(x^2) + eps)); weight may be NULL. */
+int g4_rmsnorm(void *stream, float *out, const float *in, const float *weight, int width,
+               float epsilon, size_t rows);
+
+/* gemma4.c:375-378: out = (out + add) * scale. */
+int g4_add_and_scale(void *stream, float *out, const float *add, size_t n, float scale);
+
+/* gemma4.c:381-398: rotate channel pairs (j, j + head_dim/2), j < pairs, with
+ * rows start_pos.. of the [positions x pairs] cos/sin tables. */
+int g4_apply_rope(void *stream, const float *cosines, const float *sines, int pairs, float *v,
+                  int heads, int head_dim, int start_pos, size_t n);
+
+/* gemma4.c:310-331: gate = GELU_table(gate) * up (row stride of up: up_stride). */
+int g4_geglu(void *stream, float *gate, const float *up, int rows, int width, int up_stride,
+             const float *table, int table_size, float lower, float upper);
+
+/* gemma4.c:337-358: gather and dequantize packed rows; tokens is a device array. */
+int g4_embedding(void *stream, float *out, const g4_tensor *table, const int *tokens,
+                 size_t n, float multiplier);
+
+/* gemma4.c:443-456: causal attention of n query tokens (heads x head_dim each,
+ * row-major) at positions start_pos.. over a ring KV cache of cache_len rows;
+ * sliding layers (full_attention = 0) see the last G4_WINDOW positions. */
+int g4_attend(void *stream, float *out, const float *q, const float *key_cache,
+              const float *value_cache, int cache_len, int head_dim, int heads,
+              int full_attention, int start_pos, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

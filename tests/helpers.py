@@ -1,0 +1,129 @@
+"""Test plumbing: packed weights as host (numpy) or device (torch) records."""
+
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import os
+import re
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def gelu_table_exporter() -> np.ndarray:
+    """exporter.py:73-75 in float32 (numpy's tanh)."""
+    x = np.linspace(-8.0, 8.0, 4096, dtype=np.float32)
+    return (0.5 * x * (1.0 + np.tanh(0.7978845608 * (x + 0.044715 * x * x * x)))).astype(np.float32)
+
+
+def aligned(a: np.ndarray, alignment: int = 64) -> np.ndarray:
+    """Copy of `a` whose data starts on an `alignment`-byte boundary (the
+    reference's VNNI kernel uses aligned 64-byte loads, gemma4.c:207)."""
+    a = np.ascontiguousarray(a)
+    raw = np.empty(a.nbytes + alignment, dtype=np.uint8)
+    off = (-raw.ctypes.data) % alignment
+    out = raw[off:off + a.nbytes].view(a.dtype).reshape(a.shape)
+    out[...] = a
+    return out
+
+
+class HostWeight:
+    """A packed int8 matrix with fp16 scales in host memory plus its record."""
+
+    def __init__(self, pkg, w: np.ndarray, s: np.ndarray):
+        self.w, self.s = w, s
+        self.n, self.k = w.shape
+        self.packed = aligned(pkg.pack_weight(w))
+        self.scales = aligned(pkg.pack_scales(s.astype(np.float16)).view(np.uint16))
+        self.record = pkg.Tensor()
+        self.record.data = self.packed.ctypes.data
+        self.record.scales = self.scales.ctypes.data
+        self.record.shape[0], self.record.shape[1] = self.n, self.k
+
+
+class HostF32:
+    """An fp32 record (norm weights, tables) in host memory."""
+
+    def __init__(self, pkg, a: np.ndarray, shape=None):
+        self.a = np.ascontiguousarray(a, dtype=np.float32)
+        self.record = pkg.Tensor()
+        self.record.data = self.a.ctypes.data
+        self.record.scales = None
+        shp = shape if shape is not None else self.a.shape
+        for i, v in enumerate(shp):
+            self.record.shape[i] = v
+
+
+class DeviceWeight:
+    """The same packed matrix copied to the GPU (torch memory)."""
+
+    def __init__(self, pkg, torch, host: HostWeight):
+        self.data = torch.from_numpy(host.packed.copy()).cuda()
+        self.scales = torch.from_numpy(host.scales.view(np.int16).copy()).cuda()
+        self.record = pkg.Tensor()
+        self.record.data = self.data.data_ptr()
+        self.record.scales = self.scales.data_ptr()
+        self.record.shape[0], self.record.shape[1] = host.n, host.k
+
+
+def header_functions(path: str) -> list[str]:
+    """Function names declared in a C header (for the export check)."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\**\s*(g4[a-z_0-9]*)\s*\(", text, flags=re.M)
+
+
+def load_golden(name: str) -> dict[str, np.ndarray]:
+    with np.load(os.path.join(GOLDEN, name), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def stream_ptr(torch) -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(t) -> int:
+    return t.data_ptr()
+
+
+def as_tensor_record(pkg, data_ptr: int, scales_ptr: int, n: int, k: int):
+    rec = pkg.Tensor()
+    rec.data = data_ptr
+    rec.scales = scales_ptr
+    rec.shape[0], rec.shape[1] = n, k
+    return rec
+
+
+def c_float_p(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def record_sizes(t, index: int) -> tuple[int, int]:
+    """(data bytes, scales bytes) of a record (exporter.py:61-70)."""
+    if not t.data:
+        return 0, 0
+    if t.scales:
+        count = t.shape[0] * t.shape[1]
+        return count, count // 32
+    if index == 670:  # GELU table: shape (4096, lo, hi)
+        return t.shape[0] * 4, 0
+    return t.shape[0] * max(t.shape[1], 1) * 4, 0
+
+
+def image_digest(image) -> np.ndarray:
+    """SHA-256 over every record's shape, data/scales offsets and the first
+    4 KiB (at most) of its data and of its scales: pins the synthetic writer's
+    bytes across hosts without hashing 5 GB."""
+    h = hashlib.sha256()
+    for i in range(671):
+        t = image.records[i]
+        h.update(np.array(list(t.shape), dtype=np.int32).tobytes())
+        for p, size in zip((t.data, t.scales), record_sizes(t, i)):
+            if not p:
+                continue
+            h.update(np.int64(p - image.base).tobytes())
+            h.update(ctypes.string_at(p, min(size, 4096)))
+    return np.frombuffer(h.digest(), dtype=np.uint8)

@@ -1,0 +1,143 @@
+"""Whole-step parity: g4_forward / g4_logits / g4_argmax on the synthetic
+Gemma-4-E2B image against the oracle's forward()/logits() on the same image.
+
+Bars (the path's stated tolerances): logits within 1e-3 max-abs of the CPU
+reference on every compared row, greedy tokens identical (128 decode steps
+after a 512-token prefill), and the reference's own golden logits samples.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import rng
+from helpers import load_golden
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def model(pkg, g4lib, image):
+    pkg.check(g4lib.g4_init(image.records, 0))
+    yield g4lib
+    g4lib.g4_shutdown()
+
+
+def gpu_forward(pkg, lib, tokens, start):
+    tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+    pkg.check(lib.g4_forward(tokens.ctypes.data, tokens.size, start))
+
+
+def gpu_logits(pkg, lib, row):
+    out = np.empty(pkg.VOCAB, np.float32)
+    pkg.check(lib.g4_logits(row, out.ctypes.data))
+    return out
+
+
+def gpu_argmax(pkg, lib, row):
+    t = ctypes.c_int()
+    pkg.check(lib.g4_argmax(row, ctypes.byref(t)))
+    return t.value
+
+
+def prefill(pkg, lib, cpu, tokens):
+    """512-token chunks (gemma4.c:563-566) on both sides."""
+    for pos in range(0, len(tokens), 512):
+        chunk = tokens[pos:pos + 512]
+        gpu_forward(pkg, lib, chunk, pos)
+        cpu.forward(chunk, pos)
+    return (len(tokens) - 1) % 512
+
+
+def test_golden_rows(pkg, model, image):
+    gold = load_golden("model.npz")
+    gpu_forward(pkg, model, gold["tokens"], 0)
+    for r in (0, 7):
+        lg = gpu_logits(pkg, model, r)
+        err = np.abs(lg[gold["sample_idx"]] - gold[f"row{r}_sample"]).max()
+        assert err <= TOL, (r, err)
+    assert gpu_argmax(pkg, model, 7) == int(gold["row7_argmax"])
+    pos = gold["tokens"].size
+    for tok in gold["decode_tokens"]:
+        gpu_forward(pkg, model, [tok], pos)
+        pos += 1
+    lg = gpu_logits(pkg, model, 0)
+    assert np.abs(lg[gold["sample_idx"]] - gold["decode_last_sample"]).max() <= TOL
+
+
+def test_prefill_512_and_128_greedy_steps(pkg, model, image, oracle_lib):
+    cpu = oracle_lib.Model(image)
+    tokens = rng(53).integers(0, pkg.VOCAB, 512).astype(np.int32)
+    row = prefill(pkg, model, cpu, tokens)
+    worst = 0.0
+    for r in (0, 100, 511):
+        worst = max(worst, float(np.abs(gpu_logits(pkg, model, r) - cpu.logits(r)).max()))
+    assert worst <= TOL, worst
+    pos = len(tokens)
+    margins = []
+    for step in range(128):
+        g_lg = gpu_logits(pkg, model, row)
+        c_lg = cpu.logits(row)
+        err = float(np.abs(g_lg - c_lg).max())
+        worst = max(worst, err)
+        top2 = np.partition(c_lg, -2)[-2:]
+        margins.append(float(top2[1] - top2[0]))
+        g_tok, c_tok = int(np.argmax(g_lg)), int(np.argmax(c_lg))
+        assert gpu_argmax(pkg, model, row) == g_tok
+        assert g_tok == c_tok, (step, g_tok, c_tok, err, margins[-1])
+        gpu_forward(pkg, model, [g_tok], pos)
+        cpu.forward(np.array([c_tok], np.int32), pos)
+        pos += 1
+        row = 0
+    print(f"128 greedy steps identical; max |dlogit| {worst:.3g}; min top-2 margin {min(margins):.3g}")
+    assert worst <= TOL
+    cpu.close()
+
+
+def test_long_prefill_ring_wrap(pkg, model, image, oracle_lib):
+    """1100 tokens: the sliding rings wrap (positions >= 1024) and global
+    layers attend past 512; then 8 decode steps."""
+    cpu = oracle_lib.Model(image)
+    tokens = rng(59).integers(0, pkg.VOCAB, 1100).astype(np.int32)
+    row = prefill(pkg, model, cpu, tokens)
+    for r in (0, 37, row):
+        err = float(np.abs(gpu_logits(pkg, model, r) - cpu.logits(r)).max())
+        assert err <= TOL, (r, err)
+    pos = len(tokens)
+    for step in range(8):
+        c_lg = cpu.logits(row)
+        g_lg = gpu_logits(pkg, model, row)
+        assert float(np.abs(g_lg - c_lg).max()) <= TOL
+        tok = int(np.argmax(c_lg))
+        assert int(np.argmax(g_lg)) == tok
+        gpu_forward(pkg, model, [tok], pos)
+        cpu.forward(np.array([tok], np.int32), pos)
+        pos += 1
+        row = 0
+    cpu.close()
+
+
+def test_logits_all_matches_rows(pkg, model):
+    tokens = rng(61).integers(0, pkg.VOCAB, 24).astype(np.int32)
+    gpu_forward(pkg, model, tokens, 0)
+    allrows = np.empty((24, pkg.VOCAB), np.float32)
+    pkg.check(model.g4_logits_all(allrows.ctypes.data))
+    for r in (0, 11, 23):
+        assert np.array_equal(allrows[r], gpu_logits(pkg, model, r))
+
+
+def test_errors(pkg, model):
+    bad = np.array([pkg.VOCAB], np.int32)
+    assert model.g4_forward(bad.ctypes.data, 1, 0) == 1
+    ok = np.array([3], np.int32)
+    assert model.g4_forward(ok.ctypes.data, 1, pkg.MAX_CONTEXT) == 1
+    assert model.g4_forward(ok.ctypes.data, 0, 0) == 1
+    gpu_forward(pkg, model, ok, 0)
+    out = np.empty(pkg.VOCAB, np.float32)
+    assert model.g4_logits(1, out.ctypes.data) == 1  # only one row
+    assert model.g4_init(None, 0) == 1

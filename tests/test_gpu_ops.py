@@ -1,0 +1,215 @@
+"""Per-op parity of the HIP kernels (through the C ABI) with the oracle and
+with the reference's golden vectors.
+
+Bars: bit-exact for quantize, matmul_int8 (int32 group dots + ordered fold),
+rope, geglu, embedding and add_and_scale; rmsnorm within 4 ulp-scale relative
+error (parallel sum order); attention within 2e-5 relative of the output scale
+(parallel softmax/value-sum order, device expf).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import random_weight, rng
+from helpers import DeviceWeight, HostF32, HostWeight, load_golden
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def ok(oracle_lib):
+    return oracle_lib.Kernels()
+
+
+def gpu_quantize(pkg, lib, torch, x):
+    xd = dev(torch, x)
+    q = torch.empty(x.shape, dtype=torch.int8, device="cuda")
+    s = torch.empty((x.shape[0], x.shape[1] // 64), dtype=torch.float32, device="cuda")
+    pkg.check(lib.g4_quantize(None, q.data_ptr(), s.data_ptr(), xd.data_ptr(), x.shape[0], x.shape[1]))
+    torch.cuda.synchronize()
+    return host(q), host(s)
+
+
+def gpu_matmul(pkg, lib, torch, dw, xq, xs):
+    rows = xq.shape[0]
+    out = torch.empty((rows, dw.record.shape[0]), dtype=torch.float32, device="cuda")
+    pkg.check(lib.g4_matmul_int8(None, out.data_ptr(), dev(torch, xq).data_ptr(), dev(torch, xs).data_ptr(),
+                                 dw.record, rows))
+    torch.cuda.synchronize()
+    return host(out)
+
+
+def test_quantize_bitexact(pkg, g4lib, torch_gpu, ok):
+    g = rng(41)
+    x = (g.standard_normal((37, 2048)) * g.uniform(1e-3, 1e3, (37, 1))).astype(np.float32)
+    x[2] = 0
+    x[3, 5] = 3e4
+    q, s = gpu_quantize(pkg, g4lib, torch_gpu, x)
+    q0, s0 = ok.quantize(x)
+    assert np.array_equal(q, q0) and np.array_equal(s, s0)
+
+
+def test_quantize_golden(pkg, g4lib, torch_gpu):
+    gold = load_golden("ops.npz")
+    q, s = gpu_quantize(pkg, g4lib, torch_gpu, gold["quant_x"])
+    assert np.array_equal(q, gold["quant_q"]) and np.array_equal(s, gold["quant_s"])
+
+
+def test_matmul_golden(pkg, g4lib, torch_gpu):
+    gold = load_golden("ops.npz")
+    for name in ("mm_a", "mm_b"):
+        hw = HostWeight(pkg, gold[f"{name}_w"], gold[f"{name}_ws"])
+        y = gpu_matmul(pkg, g4lib, torch_gpu, DeviceWeight(pkg, torch_gpu, hw), gold[f"{name}_xq"], gold[f"{name}_xs"])
+        assert np.array_equal(y, gold[f"{name}_y"]), name
+
+
+# Every linear shape of a Gemma-4-E2B layer (N x K) plus the lm_head.
+DECODE_SHAPES = [(2048, 1536), (4096, 1536), (256, 1536), (512, 1536), (1536, 2048), (1536, 4096),
+                 (6144, 1536), (12288, 1536), (1536, 6144), (1536, 12288), (256, 1536), (1536, 256),
+                 (8960, 1536), (262144, 1536)]
+
+
+@pytest.mark.parametrize("n,k", DECODE_SHAPES)
+def test_matmul_decode_shapes_bitexact(pkg, g4lib, torch_gpu, ok, n, k):
+    g = rng(n + k)
+    w, s = random_weight(g, n, k)
+    hw = HostWeight(pkg, w, s)
+    dw = DeviceWeight(pkg, torch_gpu, hw)
+    xq, xs = ok.quantize(g.standard_normal((1, k)).astype(np.float32))
+    y = gpu_matmul(pkg, g4lib, torch_gpu, dw, xq, xs)
+    assert np.array_equal(y, ok.matmul(xq, xs, hw.record, n))
+    # a second call reuses the split-K counters, which must have been reset
+    assert np.array_equal(gpu_matmul(pkg, g4lib, torch_gpu, dw, xq, xs), y)
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 5, 8, 9, 17, 64, 100, 512])
+def test_matmul_row_counts_bitexact(pkg, g4lib, torch_gpu, ok, rows):
+    g = rng(rows)
+    n, k = 1536, 2048
+    w, s = random_weight(g, n, k)
+    hw = HostWeight(pkg, w, s)
+    xq, xs = ok.quantize(g.standard_normal((rows, k)).astype(np.float32))
+    y = gpu_matmul(pkg, g4lib, torch_gpu, DeviceWeight(pkg, torch_gpu, hw), xq, xs)
+    assert np.array_equal(y, ok.matmul(xq, xs, hw.record, n))
+
+
+def test_matmul_prefill_config_bitexact(pkg, g4lib, torch_gpu, ok):
+    """The prefill GEMM workload: X [512 x 1536] N(0,1), W [6144 x 1536]."""
+    g = rng(2026)
+    w, s = random_weight(g, 6144, 1536)
+    hw = HostWeight(pkg, w, s)
+    xq, xs = ok.quantize(g.standard_normal((512, 1536)).astype(np.float32))
+    y = gpu_matmul(pkg, g4lib, torch_gpu, DeviceWeight(pkg, torch_gpu, hw), xq, xs)
+    assert np.array_equal(y, ok.matmul(xq, xs, hw.record, 6144))
+
+
+def test_rmsnorm(pkg, g4lib, torch_gpu, ok):
+    g = rng(43)
+    for width, rows, weighted in ((1536, 33, True), (256, 280, True), (512, 9, False)):
+        x = (g.standard_normal((rows, width)) * 4).astype(np.float32)
+        w = g.uniform(0.5, 1.5, width).astype(np.float32)
+        xd = dev(torch_gpu, x)
+        wd = dev(torch_gpu, w) if weighted else None
+        pkg.check(g4lib.g4_rmsnorm(None, xd.data_ptr(), xd.data_ptr(), wd.data_ptr() if weighted else None,
+                                   width, 1e-6, rows))
+        torch_gpu.cuda.synchronize()
+        ref = ok.rmsnorm(x, HostF32(pkg, w).record if weighted else None, width, 1e-6)
+        assert np.allclose(host(xd), ref, rtol=5e-7, atol=1e-7)
+
+
+def test_elementwise_golden_bitexact(pkg, g4lib, torch_gpu):
+    gold = load_golden("ops.npz")
+    torch = torch_gpu
+    # rope, both table widths
+    for name, hd in (("rope_s", 256), ("rope_g", 512)):
+        v = dev(torch, gold[f"{name}_v"])
+        c, s = dev(torch, gold[f"{name}_cos"]), dev(torch, gold[f"{name}_sin"])
+        pkg.check(g4lib.g4_apply_rope(None, c.data_ptr(), s.data_ptr(), gold[f"{name}_cos"].shape[1],
+                                      v.data_ptr(), 2, hd, 5, 3))
+        torch.cuda.synchronize()
+        assert np.array_equal(host(v), gold[f"{name}_out"]), name
+    # geglu
+    gate, up, table = gold["geglu_gate"], gold["geglu_up"], gold["geglu_table"]
+    gd, ud, td = dev(torch, gate), dev(torch, up), dev(torch, table)
+    pkg.check(g4lib.g4_geglu(None, gd.data_ptr(), ud.data_ptr(), gate.shape[0], gate.shape[1], up.shape[1],
+                             td.data_ptr(), 4096, -8.0, 8.0))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(gd), gold["geglu_out"])
+    # embedding
+    hw = HostWeight(pkg, gold["emb_w"], gold["emb_ws"])
+    dw = DeviceWeight(pkg, torch, hw)
+    toks = dev(torch, gold["emb_tokens"])
+    out = torch.empty(gold["emb_out"].shape, dtype=torch.float32, device="cuda")
+    pkg.check(g4lib.g4_embedding(None, out.data_ptr(), dw.record, toks.data_ptr(), toks.numel(),
+                                 float(np.sqrt(np.float32(1536)))))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out), gold["emb_out"])
+    # add_and_scale
+    a, b = dev(torch, gold["add_a"]), dev(torch, gold["add_b"])
+    pkg.check(g4lib.g4_add_and_scale(None, a.data_ptr(), b.data_ptr(), a.numel(), 0.7071067))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(a), gold["add_out"])
+
+
+def test_model_tables_bitexact(pkg, g4lib, torch_gpu, image, ok):
+    """geglu with the image's GELU table; embeddings and RoPE from the image."""
+    torch = torch_gpu
+    g = rng(47)
+    gate = (g.standard_normal((7, 12288)) * 3).astype(np.float32)
+    up = g.standard_normal((7, 12288)).astype(np.float32)
+    table = image.array(pkg.GELU_TABLE)
+    gd, ud, td = dev(torch, gate), dev(torch, up), dev(torch, table)
+    pkg.check(g4lib.g4_geglu(None, gd.data_ptr(), ud.data_ptr(), 7, 12288, 12288, td.data_ptr(), 4096, -8.0, 8.0))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(gd), ok.geglu(gate, up, 12288, image.records[pkg.GELU_TABLE]))
+    cos = image.array(pkg.layer_record(4, "rope_cos"))
+    sin = image.array(pkg.layer_record(4, "rope_sin"))
+    v = g.standard_normal((5, 8, 512)).astype(np.float32)
+    vd = dev(torch, v)
+    cd, sd = dev(torch, cos[:200000 // 2]), dev(torch, sin[:200000 // 2])
+    pkg.check(g4lib.g4_apply_rope(None, cd.data_ptr(), sd.data_ptr(), 64, vd.data_ptr(), 8, 512, 99990, 5))
+    torch.cuda.synchronize()
+    ref = ok.rope(image.records[pkg.layer_record(4, "rope_cos")], image.records[pkg.layer_record(4, "rope_sin")],
+                  v, 8, 512, 99990)
+    assert np.array_equal(host(vd), ref)
+
+
+ATTN_CASES = [
+    # head_dim, ring, full, start_pos, n
+    (256, 1024, 0, 0, 8),
+    (256, 1024, 0, 1500, 1),      # window wraps the ring
+    (256, 1024, 0, 600, 300),     # a prefill chunk straddling the window edge
+    (512, 4096, 1, 0, 16),
+    (512, 4096, 1, 3000, 1),
+    (512, 4096, 1, 1000, 64),
+]
+
+
+@pytest.mark.parametrize("hd,ring,full,start,n", ATTN_CASES)
+def test_attention(pkg, g4lib, torch_gpu, oracle_lib, hd, ring, full, start, n):
+    torch = torch_gpu
+    g = rng(hd + start + n)
+    kc = g.standard_normal((ring, hd)).astype(np.float32)
+    vc = g.standard_normal((ring, hd)).astype(np.float32)
+    q = (g.standard_normal((n, 8, hd)) * 0.25).astype(np.float32)
+    ref = np.empty_like(q)
+    oracle_lib.oracle().orc_attend(ref.ctypes.data, q.ctypes.data, kc.ctypes.data, vc.ctypes.data,
+                                   ring, hd, 8, full, start, n)
+    out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    kd, vd, qd = dev(torch, kc), dev(torch, vc), dev(torch, q)
+    pkg.check(g4lib.g4_attend(None, out.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                              ring, hd, 8, full, start, n))
+    torch.cuda.synchronize()
+    o = host(out)
+    scale = np.abs(ref).max()
+    assert np.abs(o - ref).max() <= 2e-5 * scale, float(np.abs(o - ref).max() / scale)

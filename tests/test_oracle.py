@@ -1,0 +1,271 @@
+"""Pins the oracle (oracle/oracle.c, the CPU restatement of gemma4.c:178-522):
+
+1. against the golden vectors written by the reference's own compiled
+   gemma4.c (tests/golden/*.npz), bit for bit -- this holds anywhere;
+2. against the compiled reference itself (oracle/_ref) on fresh inputs,
+   bit for bit -- where the reference checkout exists;
+3. against closed forms computed independently in float64 (integer dot
+   products, the GELU and rotation formulas, a float64 softmax), so a dropped
+   term, wrong index or transposed operand fails even if both 1 and 2 were
+   wrong the same way.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import HostF32, HostWeight, load_golden
+
+from conftest import random_weight, rng
+
+
+@pytest.fixture(scope="module")
+def gold():
+    return load_golden("ops.npz")
+
+
+@pytest.fixture(scope="module", params=["fast", "scalar"])
+def ok(request, oracle_lib):
+    """Oracle kernels with the VNNI matmul on and off."""
+    lib = oracle_lib.oracle()
+    lib.orc_set_fast(1 if request.param == "fast" else 0)
+    yield oracle_lib.Kernels()
+    lib.orc_set_fast(1)
+
+
+def _ref_or_skip(oracle_lib):
+    if not oracle_lib.ref_available():
+        pytest.skip("reference library not built here")
+    return oracle_lib.Kernels(use_ref=True)
+
+
+# --- 1. golden vectors ------------------------------------------------------
+
+def test_golden_quantize(ok, gold):
+    q, s = ok.quantize(gold["quant_x"])
+    assert np.array_equal(q, gold["quant_q"]) and np.array_equal(s, gold["quant_s"])
+
+
+def test_golden_matmul(pkg, ok, gold):
+    for name in ("mm_a", "mm_b"):
+        hw = HostWeight(pkg, gold[f"{name}_w"], gold[f"{name}_ws"])
+        y = ok.matmul(gold[f"{name}_xq"], gold[f"{name}_xs"], hw.record, hw.n)
+        assert np.array_equal(y, gold[f"{name}_y"]), name
+
+
+def test_golden_attention_primitives(ok, gold):
+    ring = gold["att_k"].shape[0]
+    hd = gold["att_q"].size
+    first, num = int(gold["att_first"]), int(gold["att_num"])
+    sc = ok.scores(gold["att_q"], gold["att_k"], first, num, ring - 1, hd)
+    assert np.array_equal(sc, gold["att_scores"])
+    p = ok.softmax(sc)
+    assert np.array_equal(p, gold["att_p"])
+    o = ok.value_sum(p, gold["att_v"], first, num, ring - 1, hd)
+    assert np.array_equal(o, gold["att_o"])
+
+
+def test_golden_elementwise(pkg, ok, gold):
+    tab = HostF32(pkg, gold["geglu_table"], shape=(4096, -8, 8))
+    assert np.array_equal(ok.geglu(gold["geglu_gate"], gold["geglu_up"], 320, tab.record), gold["geglu_out"])
+    hw = HostWeight(pkg, gold["emb_w"], gold["emb_ws"])
+    emb = ok.embedding(hw.record, gold["emb_tokens"], float(np.sqrt(np.float32(1536))))
+    assert np.array_equal(emb, gold["emb_out"])
+    rw = ok.rmsnorm(gold["rms_x"], HostF32(pkg, gold["rms_w"]).record, 1536, 1e-6)
+    assert np.array_equal(rw, gold["rms_out"])
+    assert np.array_equal(ok.rmsnorm(gold["rms_xh"], None, 256, 1e-6), gold["rms_outh"])
+    assert np.array_equal(ok.add_and_scale(gold["add_a"], gold["add_b"], 0.7071067), gold["add_out"])
+    for name, hd in (("rope_s", 256), ("rope_g", 512)):
+        r = ok.rope(HostF32(pkg, gold[f"{name}_cos"]).record, HostF32(pkg, gold[f"{name}_sin"]).record,
+                    gold[f"{name}_v"], 2, hd, 5)
+        assert np.array_equal(r, gold[f"{name}_out"]), name
+
+
+# --- 2. the compiled reference on fresh inputs --------------------------------
+
+@pytest.mark.parametrize("n,k,rows", [(16, 64, 1), (256, 1536, 3), (96, 2048, 8), (64, 12288, 13), (6144, 1536, 17)])
+def test_reference_matmul(pkg, ok, oracle_lib, n, k, rows):
+    ref = _ref_or_skip(oracle_lib)
+    g = rng(n * 7 + k + rows)
+    w, s = random_weight(g, n, k)
+    hw = HostWeight(pkg, w, s)
+    xq, xs = ref.quantize(g.standard_normal((rows, k)).astype(np.float32))
+    assert np.array_equal(ok.matmul(xq, xs, hw.record, n), ref.matmul(xq, xs, hw.record, n))
+
+
+def test_reference_kernels_fresh(pkg, ok, oracle_lib):
+    ref = _ref_or_skip(oracle_lib)
+    g = rng(5)
+    x = (g.standard_normal((33, 2048)) * g.uniform(0.01, 100, (33, 1))).astype(np.float32)
+    q1, s1 = ok.quantize(x)
+    q2, s2 = ref.quantize(x)
+    assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+    for hd in (256, 512):
+        ring = 1024
+        kc = g.standard_normal((ring, hd)).astype(np.float32)
+        qv = g.standard_normal(hd).astype(np.float32)
+        a = ok.scores(qv, kc, 900, 400, ring - 1, hd)
+        assert np.array_equal(a, ref.scores(qv, kc, 900, 400, ring - 1, hd))
+        assert np.array_equal(ok.softmax(a * 3), ref.softmax(a * 3))
+        vc = g.standard_normal((ring, hd)).astype(np.float32)
+        p = ref.softmax(a)
+        assert np.array_equal(ok.value_sum(p, vc, 900, 400, ring - 1, hd),
+                              ref.value_sum(p, vc, 900, 400, ring - 1, hd))
+    w = g.uniform(0.5, 1.5, 512).astype(np.float32)
+    xr = g.standard_normal((9, 512)).astype(np.float32)
+    assert np.array_equal(ok.rmsnorm(xr, HostF32(pkg, w).record, 512, 1e-6),
+                          ref.rmsnorm(xr, HostF32(pkg, w).record, 512, 1e-6))
+
+
+def test_reference_model_tables(pkg, image, ok, oracle_lib):
+    """Kernels that read the image's own tables (GELU, RoPE, embeddings)."""
+    ref = _ref_or_skip(oracle_lib)
+    g = rng(11)
+    gate = (g.standard_normal((5, 6144)) * 3).astype(np.float32)
+    up = g.standard_normal((5, 6144)).astype(np.float32)
+    t = image.records[pkg.GELU_TABLE]
+    assert np.array_equal(ok.geglu(gate, up, 6144, t), ref.geglu(gate, up, 6144, t))
+    toks = g.integers(0, 262144, 7).astype(np.int32)
+    e = image.records[pkg.EMBED_PER_LAYER]
+    assert np.array_equal(ok.embedding(e, toks, 16.0), ref.embedding(e, toks, 16.0))
+    c, s = image.records[pkg.layer_record(4, "rope_cos")], image.records[pkg.layer_record(4, "rope_sin")]
+    v = g.standard_normal((3, 8, 512)).astype(np.float32)
+    assert np.array_equal(ok.rope(c, s, v, 8, 512, 77777), ref.rope(c, s, v, 8, 512, 77777))
+
+
+# --- 3. closed forms ------------------------------------------------------------
+
+def test_quantize_invariants(ok):
+    g = rng(3)
+    x = (g.standard_normal((4, 640)) * 5).astype(np.float32)
+    x[1, 64:128] = 0
+    q, s = ok.quantize(x)
+    grp = x.reshape(4, 10, 64)
+    qg = q.reshape(4, 10, 64).astype(np.int32)
+    assert s[1, 1] == 0 and not qg[1, 1].any()  # zero group -> scale 0, q 0
+    amax = np.abs(grp).max(axis=2)
+    nz = amax > 0
+    assert np.array_equal(np.abs(qg).max(axis=2)[nz], np.full(nz.sum(), 127))  # the max maps to +-127
+    assert np.allclose(s, amax / 127, rtol=1e-7)
+    err = np.abs(qg * s[:, :, None].astype(np.float64) - grp)
+    assert (err <= s[:, :, None] * 0.5001 + 1e-30).all()  # round to nearest
+
+
+def test_matmul_integer_closed_form(pkg, ok):
+    """Y = sum_g ws[n,g] xs[m,g] sum_{k in g} xq[m,k] w[n,k], brute force in
+    exact integers then float64 (no packing, no fold order)."""
+    g = rng(17)
+    n, k, rows = 32, 512, 3
+    w, s = random_weight(g, n, k)
+    hw = HostWeight(pkg, w, s)
+    xq, xs = ok.quantize(g.standard_normal((rows, k)).astype(np.float32))
+    y = ok.matmul(xq, xs, hw.record, n)
+    dots = np.einsum("mgk,ngk->mng", xq.reshape(rows, k // 64, 64).astype(np.int64),
+                     w.reshape(n, k // 64, 64).astype(np.int64))
+    expect = (dots * xs[:, None, :].astype(np.float64) * s[None, :, :].astype(np.float64)).sum(axis=2)
+    assert np.allclose(y, expect, rtol=2e-6, atol=1e-6 * np.abs(expect).max())
+
+
+def test_attention_closed_form(ok):
+    g = rng(19)
+    hd, ring = 512, 1024
+    kc = g.standard_normal((ring, hd)).astype(np.float32)
+    vc = g.standard_normal((ring, hd)).astype(np.float32)
+    qv = (g.standard_normal(hd) * 0.1).astype(np.float32)
+    first, num = 1000, 50  # wraps past the ring end
+    rows = (first + np.arange(num)) & (ring - 1)
+    sc = ok.scores(qv, kc, first, num, ring - 1, hd)
+    exact = kc[rows].astype(np.float64) @ qv.astype(np.float64)
+    assert np.allclose(sc, exact, rtol=1e-5, atol=1e-5)
+    p = ok.softmax(sc)
+    e = np.exp(sc.astype(np.float64) - sc.max())
+    assert np.allclose(p, e / e.sum(), rtol=1e-5)
+    o = ok.value_sum(p, vc, first, num, ring - 1, hd)
+    assert np.allclose(o, p.astype(np.float64) @ vc[rows].astype(np.float64), rtol=1e-4, atol=1e-5)
+
+
+def test_elementwise_closed_forms(pkg, ok):
+    g = rng(23)
+    # rmsnorm: w * x / sqrt(mean(x^2) + eps)
+    x = g.standard_normal((3, 1536)).astype(np.float32)
+    w = g.uniform(0.5, 1.5, 1536).astype(np.float32)
+    y = ok.rmsnorm(x, HostF32(pkg, w).record, 1536, 1e-6)
+    x64 = x.astype(np.float64)
+    assert np.allclose(y, w * x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6), rtol=1e-5)
+    # rope: rotation of (x_j, x_{j+hd/2}) by the table angle, untouched beyond pairs
+    ang = g.uniform(-3, 3, (8, 64))
+    c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    v = g.standard_normal((2, 1, 512)).astype(np.float32)
+    r = ok.rope(HostF32(pkg, c).record, HostF32(pkg, s).record, v, 1, 512, 3)
+    a, b = v[:, 0, :64].astype(np.float64), v[:, 0, 256:320].astype(np.float64)
+    cc, ss = c[3:5].astype(np.float64), s[3:5].astype(np.float64)
+    assert np.allclose(r[:, 0, :64], a * cc - b * ss, atol=1e-6)
+    assert np.allclose(r[:, 0, 256:320], b * cc + a * ss, atol=1e-6)
+    assert np.array_equal(r[:, 0, 64:256], v[:, 0, 64:256])
+    # geglu: tanh-GELU(x) * up within the table's interpolation error
+    table = (lambda t: (0.5 * t * (1 + np.tanh(0.7978845608 * (t + 0.044715 * t ** 3)))).astype(np.float32))(
+        np.linspace(-8, 8, 4096, dtype=np.float32))
+    tab = HostF32(pkg, table, shape=(4096, -8, 8))
+    gate = np.concatenate([g.uniform(-9, 9, 1000), [-8.0, 8.0, 20.0, -20.0]]).astype(np.float32)[None]
+    up = g.uniform(-2, 2, gate.shape).astype(np.float32)
+    out = ok.geglu(gate, up, gate.shape[1], tab.record)
+    t = gate.astype(np.float64)
+    gelu = 0.5 * t * (1 + np.tanh(0.7978845608 * (t + 0.044715 * t ** 3)))
+    gelu = np.where(t <= -8, table[0], np.where(t >= 8, t, gelu))
+    assert np.allclose(out, gelu * up, atol=2e-4)
+
+
+def test_sliding_equals_global_inside_window(oracle_lib):
+    """While every query sees all keys (positions < 512), sliding and full
+    attention agree exactly (gemma4.c:448)."""
+    lib = oracle_lib.oracle()
+    g = rng(29)
+    hd, heads, n = 256, 8, 40
+    kc = g.standard_normal((1024, hd)).astype(np.float32)
+    vc = g.standard_normal((1024, hd)).astype(np.float32)
+    q = g.standard_normal((n, heads, hd)).astype(np.float32)
+    outs = []
+    for full in (0, 1):
+        o = np.empty_like(q)
+        lib.orc_attend(o.ctypes.data, q.ctypes.data, kc.ctypes.data, vc.ctypes.data, 1024, hd, heads, full, 300, n)
+        outs.append(o)
+    assert np.array_equal(outs[0], outs[1])
+
+
+# --- the whole step -------------------------------------------------------------
+
+def test_oracle_model_matches_golden(image, oracle_lib):
+    """forward()/logits() of the oracle reproduce the reference's logits rows
+    bit for bit (SHA-256 of all 262144 floats) and its greedy tokens."""
+    from helpers import load_golden
+    import hashlib
+    gold = load_golden("model.npz")
+    m = oracle_lib.Model(image)
+    m.forward(gold["tokens"], 0)
+    for r in (0, 7):
+        lg = m.logits(r)
+        assert hashlib.sha256(lg.tobytes()).digest() == bytes(gold[f"row{r}_sha"]), r
+    lg = m.logits(7)
+    pos = gold["tokens"].size
+    for step, tok in enumerate(gold["decode_tokens"]):
+        assert int(np.argmax(lg)) == int(tok)
+        m.forward(np.array([tok], np.int32), pos)
+        pos += 1
+        lg = m.logits(0)
+        assert hashlib.sha256(lg.tobytes()).digest() == bytes(gold["decode_sha"][step])
+    m.close()
+
+
+def test_oracle_thread_count_independent(image, oracle_lib):
+    lib = oracle_lib.oracle()
+    toks = np.array([5, 6, 7], np.int32)
+    rows = []
+    for threads in (1, 5):
+        lib.orc_set_threads(threads)
+        m = oracle_lib.Model(image)
+        m.forward(toks, 0)
+        rows.append(m.logits(2))
+        m.close()
+    lib.orc_set_threads(0)
+    assert np.array_equal(rows[0], rows[1])
