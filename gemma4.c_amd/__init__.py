@@ -37,6 +37,9 @@ RECORDS = 671
 FFN_6144 = 1
 UNIT_NORMS = 2
 
+ORDER_REFERENCE = 0
+ORDER_PARALLEL = 1
+
 # Record indices (field order of gemma4.c:125-155).
 EMBED, EMBED_PER_LAYER = 0, 1
 NORM, PER_LAYER_MODEL_PROJECTION, PER_LAYER_PROJECTION_NORM, GELU_TABLE = 667, 668, 669, 670
@@ -78,6 +81,8 @@ _G4_SIGNATURES = {
     "g4_argmax": (_c_i, [_c_sz, ctypes.POINTER(_c_i)]),
     "g4_shutdown": (None, []),
     "g4_stream": (_c_p, []),
+    "g4_set_order": (_c_i, [_c_i]),
+    "g4_softmax": (_c_i, [_c_p, _c_p, _c_i, _c_sz]),
     "g4_quantize": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_sz, _c_sz]),
     "g4_matmul_int8": (_c_i, [_c_p, _c_p, _c_p, _c_p, ctypes.POINTER(Tensor), _c_sz]),
     "g4_rmsnorm": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i, _c_f, _c_sz]),

@@ -43,7 +43,7 @@ struct Scratch {
     size_t dots_bytes = 0;
     unsigned *counters = nullptr;  // per 16-row block arrival counters (kept zero)
     size_t counters_count = 0;
-    float *attn = nullptr;         // attention partials (m, l, o per chunk)
+    float *attn = nullptr;         // attention partials (m, l, o per chunk) or scores
     size_t attn_bytes = 0;
 };
 Scratch &scratch();
@@ -60,9 +60,16 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
                   const float *xs, const int8_t *w, const uint16_t *ws, int n_out, int k,
                   int rows);
 
-// gemma4.c:360-373 (weight may be null)
+// Reduction order of rmsnorm and attention (g4_set_order).
+int order();
+
+// gemma4.c:360-373 (weight may be null); dispatches on order().
 void launch_rmsnorm(hipStream_t s, float *out, const float *in, const float *weight, int width,
                     float eps, size_t rows);
+void launch_rmsnorm_parallel(hipStream_t s, float *out, const float *in, const float *weight,
+                             int width, float eps, size_t rows);
+void launch_rmsnorm_reference(hipStream_t s, float *out, const float *in, const float *weight,
+                              int width, float eps, size_t rows);
 // gemma4.c:375-378
 void launch_add_and_scale(hipStream_t s, float *out, const float *add, size_t n, float scale);
 // gemma4.c:381-398 (rows of v are heads*head_dim wide)
@@ -75,10 +82,16 @@ void launch_geglu(hipStream_t s, float *gate, const float *up, int rows, int wid
 // Tokens outside [0, table_rows) produce NaN rows instead of reading outside.
 void launch_embedding(hipStream_t s, float *out, const int8_t *table, const uint16_t *scales,
                       int width, int table_rows, const int *tokens, size_t n, float multiplier);
-// gemma4.c:443-456: attention over a ring cache.
+// gemma4.c:443-456: attention over a ring cache; dispatches on order().
 int launch_attend(hipStream_t s, float *out, const float *q, const float *key_cache,
                   const float *value_cache, int cache_len, int head_dim, int heads, int full,
                   int start_pos, size_t n);
+int launch_attend_parallel(hipStream_t s, float *out, const float *q, const float *key_cache,
+                           const float *value_cache, int cache_len, int head_dim, int heads,
+                           int full, int start_pos, size_t n);
+int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
+                            const float *value_cache, int cache_len, int head_dim, int heads,
+                            int full, int start_pos, size_t n);
 // Fused tail of the K/V projections (gemma4.c:437-440): rmsnorm+rope of the n
 // new keys and rmsnorm of the new values, written into the rings at
 // (start_pos + t) & (cache_len - 1).

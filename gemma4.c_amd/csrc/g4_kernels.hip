@@ -371,8 +371,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm(float *out, const float *in,
         y[i] = (weight ? weight[i] : 1.0f) * (inverse * x[i]);
 }
 
-void launch_rmsnorm(hipStream_t s, float *out, const float *in, const float *weight, int width,
-                    float eps, size_t rows) {
+void launch_rmsnorm_parallel(hipStream_t s, float *out, const float *in, const float *weight,
+                             int width, float eps, size_t rows) {
     if (!rows) return;
     hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, s, out, in, weight, width, eps);
 }
@@ -485,15 +485,30 @@ __global__ __launch_bounds__(256) void k_kv_finish(float *key_cache, float *valu
                                                    const float *__restrict__ k_norm,
                                                    const float *__restrict__ cosines,
                                                    const float *__restrict__ sines, int pairs,
-                                                   int head_dim, int cache_len, int start_pos) {
+                                                   int head_dim, int cache_len, int start_pos,
+                                                   int reference_order) {
     __shared__ float red[4];
     __shared__ float row[512];
     const int t = blockIdx.x, is_value = blockIdx.y;
     const float *x = (is_value ? v_new : k_new) + (size_t)t * head_dim;
     const float *weight = is_value ? nullptr : k_norm;
     float s = 0.0f;
-    for (int i = threadIdx.x; i < head_dim; i += 256) s += x[i] * x[i];
-    s = block_sum256(s, red);
+    if (reference_order) {
+        // the reference's sequential sum (gemma4.c:367-368): squares in
+        // parallel, one lane adds them in index order
+        for (int i = threadIdx.x; i < head_dim; i += 256) row[i] = x[i] * x[i];
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int i = 0; i < head_dim; i++) s += row[i];
+            red[0] = s;
+        }
+        __syncthreads();
+        s = red[0];
+        __syncthreads();
+    } else {
+        for (int i = threadIdx.x; i < head_dim; i += 256) s += x[i] * x[i];
+        s = block_sum256(s, red);
+    }
     const float inverse = 1.0f / sqrtf(s / (float)head_dim + 1e-6f);
     for (int i = threadIdx.x; i < head_dim; i += 256)
         row[i] = (weight ? weight[i] : 1.0f) * (inverse * x[i]);
@@ -524,7 +539,8 @@ void launch_kv_finish(hipStream_t s, float *key_cache, float *value_cache, const
                       size_t n) {
     if (!n) return;
     hipLaunchKernelGGL(k_kv_finish, dim3((unsigned)n, 2), dim3(256), 0, s, key_cache, value_cache,
-                       k_new, v_new, k_norm, cosines, sines, pairs, head_dim, cache_len, start_pos);
+                       k_new, v_new, k_norm, cosines, sines, pairs, head_dim, cache_len, start_pos,
+                       order() == G4_ORDER_REFERENCE ? 1 : 0);
 }
 
 __global__ __launch_bounds__(256) void k_softcap(float *x, size_t n) {
@@ -722,9 +738,9 @@ __global__ __launch_bounds__(256) void k_attn_combine(float *__restrict__ out,
     }
 }
 
-int launch_attend(hipStream_t s, float *out, const float *q, const float *key_cache,
-                  const float *value_cache, int cache_len, int head_dim, int heads, int full,
-                  int start_pos, size_t n) {
+int launch_attend_parallel(hipStream_t s, float *out, const float *q, const float *key_cache,
+                           const float *value_cache, int cache_len, int head_dim, int heads,
+                           int full, int start_pos, size_t n) {
     if (!n) return G4_OK;
     const int last_pos = start_pos + (int)n - 1;
     const int max_keys = full ? last_pos + 1 : (last_pos + 1 < G4_WINDOW ? last_pos + 1 : G4_WINDOW);

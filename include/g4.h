@@ -94,6 +94,16 @@ void g4_shutdown(void);
 /* The library's HIP stream (a hipStream_t) for timing with HIP events. */
 void *g4_stream(void);
 
+/* Summation order of rmsnorm and attention, for every later call (model and
+ * per-op).  G4_ORDER_REFERENCE (the default) reproduces the reference's
+ * sequential fp32 sums (gemma4.c:366-368, 400-408, 296-307) and its libm expf
+ * bit for bit, so the whole step is bit-identical to gemma4.c up to the final
+ * tanhf.  G4_ORDER_PARALLEL uses tree sums and split-KV flash decoding:
+ * faster, equal to within fp32 rounding per op.  Returns the previous order. */
+#define G4_ORDER_REFERENCE 0
+#define G4_ORDER_PARALLEL 1
+int g4_set_order(int order);
+
 /* ---- Per-op entry points (device pointers) ------------------------------ */
 
 /* gemma4.c:265-279: per 64-value group, scale = max|x|/127, q = rint(x/scale). */
@@ -125,6 +135,10 @@ int g4_geglu(void *stream, float *gate, const float *up, int rows, int width, in
 /* gemma4.c:337-358: gather and dequantize packed rows; tokens is a device array. */
 int g4_embedding(void *stream, float *out, const g4_tensor *table, const int *tokens,
                  size_t n, float multiplier);
+
+/* gemma4.c:400-408: softmax of `rows` independent rows of `count` values in
+ * place, in the reference's order with its libm expf (bit-identical). */
+int g4_softmax(void *stream, float *values, int count, size_t rows);
 
 /* gemma4.c:443-456: causal attention of n query tokens (heads x head_dim each,
  * row-major) at positions start_pos.. over a ring KV cache of cache_len rows;
