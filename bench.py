@@ -1,0 +1,326 @@
+"""Benchmark of the MI355X W8A8 forward path on the synthetic Gemma-4-E2B model.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--order reference|parallel]
+
+Prints one JSON line.  A step is one 512-token prefill (g4_forward over 512
+uniform-random token ids at position 0) followed by the logits of its last row,
+the unit gemma4.c's --bench prefill times (gemma4.c:627-634); `value` is
+prefill tokens per second over K such steps, with the model already resident
+in HBM.  Also reported: prefill of 8192 tokens in 512-token chunks, 128 greedy
+decode steps at 16384 tokens of context (forward + logits each, gemma4.c:636-643),
+the int8-MFMA roofline of the prefill GEMM (X[512x1536] x W[6144x1536]) and the
+HBM roofline of the decode GEMV sweep (every E2B linear shape at one token,
+weighted by bytes), each timed with HIP events on the stream they run on, and
+the oracle (the CPU restatement of the same path) timed on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MODEL_SEED = 20261201
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
+INT8_MFMA_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
+
+# (N, K, count per decoded token) for every linear of a Gemma-4-E2B step.
+GEMV_SWEEP = [
+    (2048, 1536, 28), (4096, 1536, 7), (256, 1536, 24), (512, 1536, 6),
+    (1536, 2048, 28), (1536, 4096, 7), (6144, 1536, 30), (1536, 6144, 15),
+    (12288, 1536, 40), (1536, 12288, 20), (256, 1536, 35), (1536, 256, 35),
+    (8960, 1536, 1), (262144, 1536, 1),
+]
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gemv_bytes(n: int, k: int) -> int:
+    """Algorithmic bytes of one W8A8 product at one token: int8 weights, fp16
+    scales per 64, int8 activations + fp32 scales per 64, fp32 outputs."""
+    return n * k + n * k // 32 + k + k // 16 + 4 * n
+
+
+def random_weight(torch, n: int, k: int, gen):
+    """int8 U[-127, 127] packed weights, fp16 scales log-uniform in [1e-3, 1e-2]."""
+    w = torch.randint(-127, 128, (n * k,), dtype=torch.int8, device="cuda", generator=gen)
+    u = torch.rand((n * k // 64,), device="cuda", generator=gen)
+    s = torch.exp(math.log(1e-3) + u * (math.log(1e-2) - math.log(1e-3)))
+    return w, s.to(torch.float16)
+
+
+def timed_launches(torch, fn, launches: int) -> float:
+    """Average milliseconds per launch between HIP events on torch's stream.
+    The stream is first parked on a spin kernel long enough for the host to
+    enqueue every launch, so the events see back-to-back kernels rather than
+    the host's launch rate."""
+    fn(0)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(2.5e6 * (0.5 + launches * 0.02)))  # ~(0.5 + 0.02 * launches) ms
+    start.record()
+    for i in range(launches):
+        fn(i)
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / launches
+
+
+def gemm_roofline(pkg, lib, torch) -> dict:
+    """The prefill GEMM: X [512 x 1536] N(0,1) quantized per 64, W [6144 x 1536]
+    U[-127,127] with log-uniform fp16 scales; 2*512*6144*1536 int8 ops."""
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    m, n, k = 512, 6144, 1536
+    x = torch.randn((m, k), device="cuda", generator=gen)
+    xq = torch.empty((m, k), dtype=torch.int8, device="cuda")
+    xs = torch.empty((m, k // 64), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    pkg.check(lib.g4_quantize(stream, xq.data_ptr(), xs.data_ptr(), x.data_ptr(), m, k))
+    copies = 8  # 8 x 9.7 MB of weights: repeats are not served from one L2 alone
+    ws = [random_weight(torch, n, k, gen) for _ in range(copies)]
+    recs = []
+    for w, s in ws:
+        rec = pkg.Tensor()
+        rec.data, rec.scales = w.data_ptr(), s.data_ptr()
+        rec.shape[0], rec.shape[1] = n, k
+        recs.append(rec)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+
+    def launch(i):
+        pkg.check(lib.g4_matmul_int8(stream, out.data_ptr(), xq.data_ptr(), xs.data_ptr(), recs[i % copies], m))
+
+    ms = timed_launches(torch, launch, 200)
+    ops = 2.0 * m * n * k
+    tops = ops / (ms * 1e-3) / 1e12
+    moved = n * k + n * k // 32 + m * k + m * k // 16 + 4 * m * n
+    return {"kernel": "k_gemm", "ms_per_launch": ms, "tops": tops, "bytes": moved, "ops": ops}
+
+
+def gemv_sweep(pkg, lib, torch) -> dict:
+    """Every decode GEMV shape at one token, rotated over >= 512 MB of weight
+    copies per shape so repeats come from HBM, not the 256 MB Infinity Cache."""
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    stream = torch.cuda.current_stream().cuda_stream
+    per_shape = {}
+    total_bytes = total_time = 0.0
+    for n, k, count in GEMV_SWEEP:
+        key = f"{n}x{k}"
+        if key in per_shape:
+            rec = per_shape[key]
+        else:
+            copies = max(2, (512 << 20) // (n * k))
+            pool_w = torch.randint(-127, 128, (copies, n * k), dtype=torch.int8, device="cuda", generator=gen)
+            pool_s = (torch.rand((copies, n * k // 64), device="cuda", generator=gen) * 9e-3 + 1e-3).to(torch.float16)
+            x = torch.randn((1, k), device="cuda", generator=gen)
+            xq = torch.empty((1, k), dtype=torch.int8, device="cuda")
+            xs = torch.empty((1, k // 64), dtype=torch.float32, device="cuda")
+            pkg.check(lib.g4_quantize(stream, xq.data_ptr(), xs.data_ptr(), x.data_ptr(), 1, k))
+            out = torch.empty((1, n), dtype=torch.float32, device="cuda")
+            recs = []
+            for c in range(copies):
+                r = pkg.Tensor()
+                r.data, r.scales = pool_w[c].data_ptr(), pool_s[c].data_ptr()
+                r.shape[0], r.shape[1] = n, k
+                recs.append(r)
+
+            def launch(i, recs=recs, out=out, xq=xq, xs=xs):
+                pkg.check(lib.g4_matmul_int8(stream, out.data_ptr(), xq.data_ptr(), xs.data_ptr(),
+                                             recs[i % len(recs)], 1))
+
+            launches = max(50, min(2000, copies * 4))
+            ms = timed_launches(torch, launch, launches)
+            b = gemv_bytes(n, k)
+            rec = {"ms": ms, "gbs": b / (ms * 1e-3) / 1e9, "bytes": b}
+            per_shape[key] = rec
+            del pool_w, pool_s
+            torch.cuda.empty_cache()
+        total_bytes += count * rec["bytes"]
+        total_time += count * rec["ms"]
+    return {
+        "byte_weighted_gbs": total_bytes / (total_time * 1e-3) / 1e9,
+        "bytes_per_token": total_bytes,
+        "gemv_ms_per_token": total_time,
+        "per_shape": {k: round(v["gbs"], 1) for k, v in per_shape.items()},
+    }
+
+
+def model_benchmarks(pkg, lib, np, steps: int, warmup: int) -> dict:
+    rng = np.random.default_rng(3)
+    out = np.empty(pkg.VOCAB, np.float32)
+
+    def forward(tokens, pos):
+        pkg.check(lib.g4_forward(tokens.ctypes.data, tokens.size, pos))
+
+    def prefill(tokens):
+        for pos in range(0, tokens.size, 512):
+            forward(tokens[pos:pos + 512], pos)
+        pkg.check(lib.g4_logits((tokens.size - 1) % 512, out.ctypes.data))
+
+    # headline: K timed 512-token prefill steps
+    t512 = rng.integers(0, pkg.VOCAB, 512).astype(np.int32)
+    for _ in range(warmup):
+        prefill(t512)
+    start = time.perf_counter()
+    for _ in range(steps):
+        prefill(t512)
+    elapsed = time.perf_counter() - start
+    res = {"prefill512_s": elapsed, "prefill512_tok_s": 512 * steps / elapsed}
+    log(f"prefill 512: {res['prefill512_tok_s']:.0f} tok/s ({elapsed / steps * 1e3:.2f} ms/step)")
+
+    # prefill 8192 in 512-token chunks: 1 warmup + mean of 3
+    t8k = rng.integers(0, pkg.VOCAB, 8192).astype(np.int32)
+    prefill(t8k)
+    times = []
+    for _ in range(3):
+        s = time.perf_counter()
+        prefill(t8k)
+        times.append(time.perf_counter() - s)
+    res["prefill8192_tok_s"] = 8192 / (sum(times) / len(times))
+    log(f"prefill 8192: {res['prefill8192_tok_s']:.0f} tok/s")
+
+    # decode at 16384 tokens of context: fill, then 128 steps of forward + logits
+    t16k = rng.integers(0, pkg.VOCAB, 16384).astype(np.int32)
+    prefill(t16k)
+    token = np.array([2], np.int32)  # gemma4.c:637 decodes token 2
+    s = time.perf_counter()
+    for i in range(128):
+        forward(token, 16384 + i)
+        pkg.check(lib.g4_logits(0, out.ctypes.data))
+    res["decode16k_tok_s"] = 128 / (time.perf_counter() - s)
+    log(f"decode @16K: {res['decode16k_tok_s']:.1f} tok/s")
+    return res
+
+
+def cpu_baseline(pkg, image, np) -> dict:
+    """The oracle (CPU restatement of the same path, bit-identical to the
+    reference) on this host: 512-token prefill + logits, 1 warmup + 2 timed."""
+    from oracle import binding
+    lib = binding.oracle()
+    threads = min(lib.orc_threads(), 16)
+    lib.orc_set_threads(threads)
+    model = binding.Model(image)
+    tokens = np.random.default_rng(3).integers(0, pkg.VOCAB, 512).astype(np.int32)
+    model.forward(tokens, 0)
+    model.logits(511)
+    times = []
+    for _ in range(2):
+        s = time.perf_counter()
+        model.forward(tokens, 0)
+        model.logits(511)
+        times.append(time.perf_counter() - s)
+    prefill = 512 / (sum(times) / len(times))
+    # decode at 512 tokens of context: 4 steps of forward + logits
+    s = time.perf_counter()
+    for i in range(4):
+        model.forward(np.array([2], np.int32), 512 + i)
+        model.logits(0)
+    decode = 4 / (time.perf_counter() - s)
+    model.close()
+    log(f"cpu oracle ({threads} threads): prefill 512 {prefill:.1f} tok/s, decode@512 {decode:.2f} tok/s")
+    return {"value": prefill, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": "512-token prefill + logits of the same synthetic model, 1 warmup + mean of 2; "
+                      f"decode@512 ctx {decode:.2f} tok/s over 4 steps",
+            "decode512_tok_s": decode}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--order", choices=["reference", "parallel"], default="reference")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(this path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch  # before libg4.so: one HIP runtime in the process
+
+    import __graft_entry__
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    pkg = __graft_entry__.load_package()
+    lib = pkg.lib()
+    lib.g4_set_order(pkg.ORDER_REFERENCE if args.order == "reference" else pkg.ORDER_PARALLEL)
+
+    t = time.perf_counter()
+    image = pkg.Image.synthetic(seed=MODEL_SEED)
+    log(f"synthetic E2B image {image.size / 1e9:.2f} GB in {time.perf_counter() - t:.1f} s")
+
+    gemm = gemm_roofline(pkg, lib, torch)
+    log(f"prefill GEMM 512x6144x1536: {gemm['ms_per_launch'] * 1e3:.1f} us, {gemm['tops']:.0f} TOPS")
+    sweep = gemv_sweep(pkg, lib, torch)
+    log(f"decode GEMV sweep: {sweep['byte_weighted_gbs']:.0f} GB/s byte-weighted; {sweep['per_shape']}")
+    torch.cuda.empty_cache()
+
+    t = time.perf_counter()
+    pkg.check(lib.g4_init(image.records, 0))
+    log(f"g4_init (upload + KV allocation) {time.perf_counter() - t:.1f} s")
+    try:
+        res = model_benchmarks(pkg, lib, np, args.steps, args.warmup)
+    finally:
+        lib.g4_shutdown()
+
+    cpu = None if args.no_cpu else cpu_baseline(pkg, image, np)
+    steps_ms = res["prefill512_s"] / args.steps * 1e3
+    line = {
+        "metric": "prefill tok/s @512 & 8192 tok; decode tok/s @16K ctx; %HBM/%MFMA peak, 1 GPU",
+        "value": round(res["prefill512_tok_s"], 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(steps_ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "Gemma-4-E2B-shaped random-init model in the exporter .bin layout "
+                        "(N(0,0.02) int8 matrices, seed 20261201); step = 512-token prefill + logits",
+            "prefill_tokens": 512,
+            "summation_order": args.order,
+        },
+        "prefill8192_tok_s": round(res["prefill8192_tok_s"], 1),
+        "decode16k_tok_s": round(res["decode16k_tok_s"], 2),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "k_gemm (prefill W8A8 GEMM, X[512x1536] x W[6144x1536])",
+            "achieved": round(gemm["tops"], 1),
+            "peak": INT8_MFMA_PEAK_TOPS,
+            "unit": "TOPS",
+            "frac": round(gemm["tops"] / INT8_MFMA_PEAK_TOPS, 4),
+            "traffic": None,
+        },
+        "roofline_decode": {
+            "bound": "hbm",
+            "kernel": "k_gemv (decode W8A8 GEMV sweep, byte-weighted over one token's linears)",
+            "achieved": round(sweep["byte_weighted_gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(sweep["byte_weighted_gbs"] / HBM_PEAK_GBS, 4),
+            "bytes_per_token": sweep["bytes_per_token"],
+            "per_shape_gbs": sweep["per_shape"],
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

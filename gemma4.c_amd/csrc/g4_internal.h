@@ -35,19 +35,17 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
 
 // ---- scratch owned by the library ------------------------------------------
 
-// Device scratch for split-K matmul dot products, their arrival counters and
-// attention partials.  Grows on demand (allocation happens outside any kernel
-// sequence that a caller might capture).
+// Device scratch for split-K matmul dot products and attention partials or
+// scores.  Grows on demand (allocation happens outside any kernel sequence
+// that a caller might capture).
 struct Scratch {
-    int32_t *dots = nullptr;       // split-K exact group dot products
+    int32_t *dots = nullptr;  // split-K exact group dot products
     size_t dots_bytes = 0;
-    unsigned *counters = nullptr;  // per 16-row block arrival counters (kept zero)
-    size_t counters_count = 0;
-    float *attn = nullptr;         // attention partials (m, l, o per chunk) or scores
+    float *attn = nullptr;    // attention partials (m, l, o per chunk) or scores
     size_t attn_bytes = 0;
 };
 Scratch &scratch();
-int scratch_reserve(size_t dots_bytes, size_t counters, size_t attn_bytes);
+int scratch_reserve(size_t dots_bytes, size_t attn_bytes);
 
 // ---- launchers (asynchronous on `stream`; shapes validated by callers) -------
 

@@ -23,7 +23,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 static Scratch g_scratch;
 Scratch &scratch() { return g_scratch; }
 
-int scratch_reserve(size_t dots_bytes, size_t counters, size_t attn_bytes) {
+int scratch_reserve(size_t dots_bytes, size_t attn_bytes) {
     Scratch &s = g_scratch;
     if (dots_bytes > s.dots_bytes) {
         if (s.dots) G4_HIP(hipFree(s.dots));
@@ -31,15 +31,6 @@ int scratch_reserve(size_t dots_bytes, size_t counters, size_t attn_bytes) {
         s.dots_bytes = 0;
         G4_HIP(hipMalloc(&s.dots, dots_bytes));
         s.dots_bytes = dots_bytes;
-    }
-    if (counters > s.counters_count) {
-        if (s.counters) G4_HIP(hipFree(s.counters));
-        s.counters = nullptr;
-        s.counters_count = 0;
-        G4_HIP(hipMalloc(&s.counters, counters * sizeof(unsigned)));
-        G4_HIP(hipMemset(s.counters, 0, counters * sizeof(unsigned)));
-        G4_HIP(hipDeviceSynchronize());
-        s.counters_count = counters;
     }
     if (attn_bytes > s.attn_bytes) {
         if (s.attn) G4_HIP(hipFree(s.attn));
@@ -113,20 +104,47 @@ void launch_quantize(hipStream_t s, int8_t *q, float *scales, const float *x, si
 // lane l holds chunk c = l/4 (k = 4c..4c+3) of rows 4(l%4)..4(l%4)+3.  Four
 // v_dot4_i32_i8 give the lane's partial dots; a transposing butterfly over the
 // 16 lanes that share l%4 leaves the exact int32 group dot of row
-// 4(l%4) + 2 b2 + b3 (b2, b3 = bits 2, 3 of l) in lanes 0..15.  The fold
-// acc = fma((float)dot, f32(ws) * xs, acc) runs over groups in ascending
-// order as in gemma4.c:216-218, so results are bit-identical.  With several
-// splits per block, each wave stores its exact dots and the last wave to
-// arrive on the block's counter folds all groups in order.
+// 4(l%4) + 2 b2 + b3 (b2, b3 = bits 2, 3 of l) in lanes 0..15.
+//
+// Memory-level parallelism: a wave issues a batch of U tiles (U KB) with the
+// activation dwords and weight scales interleaved in the order they are
+// consumed, so each group waits only for its own loads.
+//
+// Fold: acc = fma((float)dot, f32(ws) * xs, acc) over groups in ascending
+// order (gemma4.c:216-218), so results are bit-identical.  With one split per
+// block the wave folds as it goes; with several, each wave stores its exact
+// dots and k_gemv_fold (the next launch on the stream) folds all groups in
+// order -- the kernel boundary orders the two, no device-scope fences needed.
 
 template <int M>
+__device__ __forceinline__ void gemv_group_dots(const uint4 t, const int (&x4)[M], int b2, int b3,
+                                                int (&d)[M]) {
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        const int p0 = __builtin_amdgcn_sdot4((int)t.x, x4[m], 0, false);
+        const int p1 = __builtin_amdgcn_sdot4((int)t.y, x4[m], 0, false);
+        const int p2 = __builtin_amdgcn_sdot4((int)t.z, x4[m], 0, false);
+        const int p3 = __builtin_amdgcn_sdot4((int)t.w, x4[m], 0, false);
+        int k0 = b2 ? p2 : p0, k1 = b2 ? p3 : p1;
+        const int s0 = b2 ? p0 : p2, s1 = b2 ? p1 : p3;
+        k0 += __shfl_xor(s0, 4);
+        k1 += __shfl_xor(s1, 4);
+        int kk = b3 ? k1 : k0;
+        const int ss = b3 ? k0 : k1;
+        kk += __shfl_xor(ss, 8);
+        kk += __shfl_xor(kk, 16);
+        kk += __shfl_xor(kk, 32);
+        d[m] = kk;
+    }
+}
+
+template <int M, int U>
 __global__ __launch_bounds__(64) void k_gemv(float *__restrict__ out, size_t out_stride,
                                              const int8_t *__restrict__ xq,
                                              const float *__restrict__ xs,
                                              const int8_t *__restrict__ w,
                                              const uint16_t *__restrict__ ws, int k, int splits,
-                                             int rows, int32_t *__restrict__ dots,
-                                             unsigned *__restrict__ counters) {
+                                             int rows, int32_t *__restrict__ dots) {
     const int groups = k >> 6;
     const int block = blockIdx.x / splits, split = blockIdx.x % splits;
     const int g_begin = (int)((long)split * groups / splits);
@@ -134,87 +152,106 @@ __global__ __launch_bounds__(64) void k_gemv(float *__restrict__ out, size_t out
     const int lane = threadIdx.x;
     const int chunk = lane >> 2, b2 = (lane >> 2) & 1, b3 = (lane >> 3) & 1;
     const int row = 4 * (lane & 3) + 2 * b2 + b3;
-    const uint4 *tiles = reinterpret_cast<const uint4 *>(w + (size_t)block * 16 * k);
-    const uint16_t *wscale = ws + (size_t)block * groups * 16;
+    const uint4 *tiles = reinterpret_cast<const uint4 *>(w + (size_t)block * 16 * k) + lane;
+    const uint16_t *wscale = ws + (size_t)block * groups * 16 + row;
+    const int *xrow = reinterpret_cast<const int *>(xq) + chunk;
+    const bool fold = splits == 1;
 
     float acc[M];
 #pragma unroll
     for (int m = 0; m < M; m++) acc[m] = 0.0f;
 
-    constexpr int U = 4;
-    for (int g = g_begin; g < g_end; g += U) {
+    auto consume = [&](int gg, const uint4 &t, const int (&x4)[M], uint16_t wsr) {
+        int d[M];
+        gemv_group_dots<M>(t, x4, b2, b3, d);
+        if (fold) {
+            const float wsf = half_bits_to_float(wsr);
+#pragma unroll
+            for (int m = 0; m < M; m++)
+                if (m < rows) acc[m] = fmaf((float)d[m], wsf * xs[(size_t)m * groups + gg], acc[m]);
+        } else if (lane < 16) {
+#pragma unroll
+            for (int m = 0; m < M; m++)
+                dots[(((size_t)block * groups + gg) * M + m) * 16 + row] = d[m];
+        }
+    };
+
+    int g = g_begin;
+    for (; g + U <= g_end; g += U) {
         uint4 t[U];
         int x4[U][M];
+        uint16_t wsr[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            if (g + u < g_end) {
-                t[u] = tiles[(size_t)(g + u) * 64 + lane];
+            t[u] = tiles[(size_t)(g + u) * 64];
 #pragma unroll
-                for (int m = 0; m < M; m++)
-                    x4[u][m] = m < rows ? *reinterpret_cast<const int *>(xq + (size_t)m * k +
-                                                                         (g + u) * 64 + 4 * chunk)
-                                        : 0;
-            }
+            for (int m = 0; m < M; m++)
+                x4[u][m] = m < rows ? xrow[((size_t)m * k + (size_t)(g + u) * 64) >> 2] : 0;
+            wsr[u] = fold ? wscale[(g + u) * 16] : 0;
         }
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (g + u >= g_end) break;
-            const int gg = g + u;
-            int d[M];
-#pragma unroll
-            for (int m = 0; m < M; m++) {
-                const int p0 = __builtin_amdgcn_sdot4((int)t[u].x, x4[u][m], 0, false);
-                const int p1 = __builtin_amdgcn_sdot4((int)t[u].y, x4[u][m], 0, false);
-                const int p2 = __builtin_amdgcn_sdot4((int)t[u].z, x4[u][m], 0, false);
-                const int p3 = __builtin_amdgcn_sdot4((int)t[u].w, x4[u][m], 0, false);
-                int k0 = b2 ? p2 : p0, k1 = b2 ? p3 : p1;
-                const int s0 = b2 ? p0 : p2, s1 = b2 ? p1 : p3;
-                k0 += __shfl_xor(s0, 4);
-                k1 += __shfl_xor(s1, 4);
-                int kk = b3 ? k1 : k0;
-                const int ss = b3 ? k0 : k1;
-                kk += __shfl_xor(ss, 8);
-                kk += __shfl_xor(kk, 16);
-                kk += __shfl_xor(kk, 32);
-                d[m] = kk;
-            }
-            if (splits == 1) {
-                const float wsf = half_bits_to_float(wscale[gg * 16 + row]);
-#pragma unroll
-                for (int m = 0; m < M; m++)
-                    if (m < rows) acc[m] = fmaf((float)d[m], wsf * xs[(size_t)m * groups + gg], acc[m]);
-            } else if (lane < 16) {
-#pragma unroll
-                for (int m = 0; m < M; m++)
-                    dots[(((size_t)block * groups + gg) * M + m) * 16 + row] = d[m];
-            }
-        }
+        for (int u = 0; u < U; u++) consume(g + u, t[u], x4[u], wsr[u]);
     }
-
-    if (splits > 1) {
-        __threadfence();
-        unsigned previous = 0;
-        if (lane == 0) previous = atomicAdd(&counters[block], 1u);
-        previous = __shfl(previous, 0);
-        if (previous != (unsigned)(splits - 1)) return;
-        __threadfence();
-        if (lane < 16) {
-            for (int g = 0; g < groups; g++) {
-                const float wsf = half_bits_to_float(wscale[g * 16 + row]);
+    for (; g < g_end; g++) {
+        const uint4 t = tiles[(size_t)g * 64];
+        int x4[M];
 #pragma unroll
-                for (int m = 0; m < M; m++)
-                    if (m < rows)
-                        acc[m] = fmaf((float)dots[(((size_t)block * groups + g) * M + m) * 16 + row],
-                                      wsf * xs[(size_t)m * groups + g], acc[m]);
-            }
-        }
-        if (lane == 0) atomicExch(&counters[block], 0u);
+        for (int m = 0; m < M; m++) x4[m] = m < rows ? xrow[((size_t)m * k + (size_t)g * 64) >> 2] : 0;
+        consume(g, t, x4, fold ? wscale[g * 16] : 0);
     }
-    if (lane < 16) {
+    if (fold && lane < 16) {
 #pragma unroll
         for (int m = 0; m < M; m++)
             if (m < rows) out[(size_t)m * out_stride + (size_t)block * 16 + row] = acc[m];
     }
+}
+
+// The group-ordered fold of split GEMV dots: one thread per output row.
+template <int M>
+__global__ __launch_bounds__(256) void k_gemv_fold(float *__restrict__ out, size_t out_stride,
+                                                   const int32_t *__restrict__ dots,
+                                                   const float *__restrict__ xs,
+                                                   const uint16_t *__restrict__ ws, int n_out,
+                                                   int groups, int rows) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= n_out) return;
+    const int block = n >> 4, r = n & 15;
+    const int32_t *d = dots + (size_t)block * groups * M * 16 + r;
+    const uint16_t *s = ws + (size_t)block * groups * 16 + r;
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) acc[m] = 0.0f;
+    // Loads for a batch of B groups are issued before the fma chain that
+    // consumes them, so the chain is not serialized on memory latency.
+    constexpr int B = 16;
+    int g = 0;
+    for (; g + B <= groups; g += B) {
+        int dv[B][M];
+        uint16_t sv[B];
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            sv[u] = s[(g + u) * 16];
+#pragma unroll
+            for (int m = 0; m < M; m++) dv[u][m] = m < rows ? d[((size_t)(g + u) * M + m) * 16] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            const float wsf = half_bits_to_float(sv[u]);
+#pragma unroll
+            for (int m = 0; m < M; m++)
+                if (m < rows) acc[m] = fmaf((float)dv[u][m], wsf * xs[(size_t)m * groups + g + u], acc[m]);
+        }
+    }
+    for (; g < groups; g++) {
+        const float wsf = half_bits_to_float(s[g * 16]);
+#pragma unroll
+        for (int m = 0; m < M; m++)
+            if (m < rows)
+                acc[m] = fmaf((float)d[((size_t)g * M + m) * 16], wsf * xs[(size_t)m * groups + g], acc[m]);
+    }
+#pragma unroll
+    for (int m = 0; m < M; m++)
+        if (m < rows) out[(size_t)m * out_stride + n] = acc[m];
 }
 
 // ---------------------------------------------------------------------------
@@ -323,32 +360,45 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
         return G4_OK;
     }
     const int m_pad = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+    // Enough waves to keep ~16 KB in flight on every CU: aim for >= 2048 waves,
+    // each covering at least 8 groups (8 KB of weights).
     int splits = 1;
-    if (blocks < 1024) {
-        splits = (1024 + blocks - 1) / blocks;
-        const int max_splits = groups / 4 > 0 ? groups / 4 : 1;
+    if (blocks < 2048) {
+        splits = (2048 + blocks - 1) / blocks;
+        const int max_splits = groups / 8 > 0 ? groups / 8 : 1;
         if (splits > max_splits) splits = max_splits;
     }
     int32_t *dots = nullptr;
-    unsigned *counters = nullptr;
     if (splits > 1) {
         const size_t need = (size_t)n_out * groups * m_pad * sizeof(int32_t);
-        int rc = scratch_reserve(need, (size_t)blocks, 0);
+        int rc = scratch_reserve(need, 0);
         if (rc) return rc;
         dots = scratch().dots;
-        counters = scratch().counters;
     }
     dim3 grid((unsigned)(blocks * splits));
-#define G4_GEMV(MM)                                                                            \
-    hipLaunchKernelGGL(k_gemv<MM>, grid, dim3(64), 0, s, out, out_stride, xq, xs, w, ws, k,    \
-                       splits, rows, dots, counters)
+#define G4_GEMV(MM, UU)                                                                        \
+    hipLaunchKernelGGL((k_gemv<MM, UU>), grid, dim3(64), 0, s, out, out_stride, xq, xs, w, ws, \
+                       k, splits, rows, dots)
     switch (m_pad) {
-    case 1: G4_GEMV(1); break;
-    case 2: G4_GEMV(2); break;
-    case 4: G4_GEMV(4); break;
-    default: G4_GEMV(8); break;
+    case 1: G4_GEMV(1, 16); break;
+    case 2: G4_GEMV(2, 8); break;
+    case 4: G4_GEMV(4, 4); break;
+    default: G4_GEMV(8, 4); break;
     }
 #undef G4_GEMV
+    if (splits > 1) {
+        dim3 fgrid((unsigned)((n_out + 255) / 256));
+#define G4_FOLD(MM)                                                                            \
+    hipLaunchKernelGGL((k_gemv_fold<MM>), fgrid, dim3(256), 0, s, out, out_stride, dots, xs, ws, \
+                       n_out, groups, rows)
+        switch (m_pad) {
+        case 1: G4_FOLD(1); break;
+        case 2: G4_FOLD(2); break;
+        case 4: G4_FOLD(4); break;
+        default: G4_FOLD(8); break;
+        }
+#undef G4_FOLD
+    }
     return G4_OK;
 }
 
@@ -747,7 +797,7 @@ int launch_attend_parallel(hipStream_t s, float *out, const float *q, const floa
     const int max_chunks = (max_keys + kAttnChunk - 1) / kAttnChunk;
     const size_t o_floats = n * (size_t)max_chunks * heads * head_dim;
     const size_t ml_floats = n * (size_t)max_chunks * heads * 2;
-    int rc = scratch_reserve(0, 0, (o_floats + ml_floats) * sizeof(float));
+    int rc = scratch_reserve(0, (o_floats + ml_floats) * sizeof(float));
     if (rc) return rc;
     float *part_o = scratch().attn, *part_ml = part_o + o_floats;
     dim3 grid1((unsigned)max_chunks, (unsigned)n);

@@ -284,9 +284,8 @@ static int init(const g4_tensor *records, int device) {
     G4_HIP(hipHostMalloc((void **)&c.tokens_pinned, G4_BATCH * sizeof(int), hipHostMallocDefault));
     // Split-K scratch for the widest few-row product (1536 x 12288) and the
     // decode attention partials for a full-length context.
-    G4_TRY(scratch_reserve((size_t)G4_HIDDEN * (8 * G4_HIDDEN / 64) * 8 * sizeof(int32_t),
-                           (size_t)G4_VOCAB / 16,
-                           (size_t)(G4_MAX_CONTEXT / 64) * 8 * (512 + 2) * sizeof(float)));
+    G4_TRY(scratch_reserve((size_t)G4_VOCAB * (G4_HIDDEN / 64) * sizeof(int32_t),
+                           (size_t)G4_MAX_CONTEXT * 8 * sizeof(float) * 2));
     G4_HIP(hipDeviceSynchronize());
     c.ready = true;
     return G4_OK;

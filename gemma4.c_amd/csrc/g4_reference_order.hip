@@ -91,15 +91,29 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reference(float *out, const flo
     float sum = 0.0f;
     if (valid && lane == 0) {
         if (staged) {
+            // Batches of 64 squares are read into registers ahead of the add
+            // chain that consumes them, so the chain never waits on LDS.
             const float4 *sq = reinterpret_cast<const float4 *>(s_sq[wave]);
-            for (int i = 0; i < width / 4; i++) {
-                const float4 q = sq[i];
-                sum += q.x;
-                sum += q.y;
-                sum += q.z;
-                sum += q.w;
+            const int batches = width / 64;
+            float4 cur[16], next[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) cur[j] = batches > 0 ? sq[j] : make_float4(0, 0, 0, 0);
+            for (int b = 0; b < batches; b++) {
+                if (b + 1 < batches) {
+#pragma unroll
+                    for (int j = 0; j < 16; j++) next[j] = sq[(b + 1) * 16 + j];
+                }
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    sum += cur[j].x;
+                    sum += cur[j].y;
+                    sum += cur[j].z;
+                    sum += cur[j].w;
+                }
+#pragma unroll
+                for (int j = 0; j < 16; j++) cur[j] = next[j];
             }
-            for (int i = width & ~3; i < width; i++) sum += s_sq[wave][i];
+            for (int i = batches * 64; i < width; i++) sum += s_sq[wave][i];
         } else {
             for (int i = 0; i < width; i++) sum += x[i] * x[i];
         }
@@ -133,44 +147,56 @@ __device__ __forceinline__ int first_visible(int pos, int full) {
 }
 
 // Scores of every (token, head, visible key), exact (gemma4.c:281-294): 16
-// lanes per key, lane m an fma chain over channels m, m+16, ..., then the fixed
-// tree.  scores[(t * heads + h) * stride + k], k relative to the first key.
-template <int HD>
+// lanes per key, lane m an fma chain over channels m, m+16, ... (s ascending),
+// then the fixed tree.  A block takes TQ tokens x 8 heads against 64 keys: each
+// 16-lane group keeps its key's channel slice in registers and reads the query
+// rows from LDS, stored [row][m][s] so a lane's chain is contiguous (16-byte
+// LDS loads).  scores[(t * 8 + h) * stride + (p - first(t))] for key position p.
+template <int HD, int TQ>
 __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q,
                                                      const float *__restrict__ key_cache,
-                                                     int cache_len, int heads, int full,
-                                                     int start_pos, size_t stride,
-                                                     float *__restrict__ scores) {
-    __shared__ float s_q[8][HD];
-    const int t = blockIdx.y;
-    const int pos = start_pos + t, first = first_visible(pos, full), keys = pos + 1 - first;
-    const int k0 = blockIdx.x * 64;
-    if (k0 >= keys) return;
-    const int kn = keys - k0 < 64 ? keys - k0 : 64;
+                                                     int cache_len, int full, int start_pos, int n,
+                                                     size_t stride, float *__restrict__ scores) {
+    constexpr int S = HD / 16;
+    __shared__ __attribute__((aligned(16))) float s_q[TQ * 8][16][S];
+    const int t0 = blockIdx.y * TQ;
+    const int tn = n - t0 < TQ ? n - t0 : TQ;
+    const int pos_last = start_pos + t0 + tn - 1;
+    const int kbase = first_visible(start_pos + t0, full) + blockIdx.x * 64;
+    if (kbase > pos_last) return;
     const int mask = cache_len - 1, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float *qt = q + (size_t)t * heads * HD;
-    for (int i = tid; i < heads * HD; i += 256) s_q[i / HD][i % HD] = qt[i];
+    const float *qt = q + (size_t)t0 * 8 * HD;
+    for (int i = tid; i < tn * 8 * HD; i += 256) {
+        const int row = i / HD, j = i % HD;
+        s_q[row][j & 15][j >> 4] = qt[i];
+    }
     __syncthreads();
-    const int m16 = lane & 15, kg = lane >> 4;
-    for (int kk = wave * 4 + kg; kk < kn; kk += 16) {
-        const float *kr = key_cache + (size_t)((first + k0 + kk) & mask) * HD;
-        float acc[8];
+    const int m = lane & 15, kg = lane >> 4;
+    for (int kk = wave * 4 + kg; kk < 64; kk += 16) {
+        const int p = kbase + kk;
+        if (p > pos_last) break;  // uniform within the 16-lane group
+        const float *kr = key_cache + (size_t)(p & mask) * HD + m;
+        float kv[S];
 #pragma unroll
-        for (int h = 0; h < 8; h++) acc[h] = 0.0f;
-        for (int j = m16; j < HD; j += 16) {
-            const float kv = kr[j];
+        for (int s = 0; s < S; s++) kv[s] = kr[16 * s];
+        for (int row = 0; row < tn * 8; row++) {
+            const int t = t0 + row / 8, pos = start_pos + t, first = first_visible(pos, full);
+            const float4 *qv = reinterpret_cast<const float4 *>(s_q[row][m]);
+            float acc = 0.0f;
 #pragma unroll
-            for (int h = 0; h < 8; h++)
-                if (h < heads) acc[h] = fmaf(s_q[h][j], kv, acc[h]);
-        }
-#pragma unroll
-        for (int h = 0; h < 8; h++) {
-            float v = acc[h];
-            v += __shfl_down(v, 8, 16);
-            v += __shfl_down(v, 4, 16);
-            v += __shfl_down(v, 2, 16);
-            v += __shfl_down(v, 1, 16);
-            if (m16 == 0 && h < heads) scores[((size_t)t * heads + h) * stride + k0 + kk] = v;
+            for (int s4 = 0; s4 < S / 4; s4++) {
+                const float4 qq = qv[s4];
+                acc = fmaf(qq.x, kv[4 * s4 + 0], acc);
+                acc = fmaf(qq.y, kv[4 * s4 + 1], acc);
+                acc = fmaf(qq.z, kv[4 * s4 + 2], acc);
+                acc = fmaf(qq.w, kv[4 * s4 + 3], acc);
+            }
+            acc += __shfl_down(acc, 8, 16);
+            acc += __shfl_down(acc, 4, 16);
+            acc += __shfl_down(acc, 2, 16);
+            acc += __shfl_down(acc, 1, 16);
+            if (m == 0 && p >= first && p <= pos)
+                scores[((size_t)t * 8 + (row & 7)) * stride + (p - first)] = acc;
         }
     }
 }
@@ -179,14 +205,18 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
 // 64 values: a prefix-max scan gives each value the maximum m seen before it;
 // a value above m contributes expf(m - v) as a rescale factor (the sum becomes
 // s * e + 1), any other value expf(v - m) as an addend.  Lane 0 applies the
-// recurrence in index order.  Then p = expf(v - max) / sum.
+// recurrence in index order, reading its operands from LDS in batches so the
+// chain never waits on memory; the next block's values are loaded meanwhile.
+// Then p = expf(v - max) / sum.
 __device__ void softmax_row_reference(float *v, int count, float *s_e, int *s_new) {
     const int lane = threadIdx.x & 63;
     float carry = v[0];  // max = values[0], sum = 1 (gemma4.c:401)
     float sum = 1.0f;
+    float x_next = 1 + lane < count ? v[1 + lane] : -INFINITY;
     for (int base = 1; base < count; base += 64) {
-        const int j = base + lane;
-        const float x = j < count ? v[j] : -INFINITY;
+        const float x = x_next;
+        const int j_next = base + 64 + lane;
+        x_next = j_next < count ? v[j_next] : -INFINITY;
         float incl = x;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -203,8 +233,18 @@ __device__ void softmax_row_reference(float *v, int count, float *s_e, int *s_ne
         __syncthreads();
         if (lane == 0) {
             const int n = count - base < 64 ? count - base : 64;
-            if (!any_new) {
-                for (int jj = 0; jj < n; jj++) sum += s_e[jj];
+            if (!any_new && n == 64) {
+                const float4 *e4 = reinterpret_cast<const float4 *>(s_e);
+                float4 e[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++) e[i] = e4[i];
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    sum += e[i].x;
+                    sum += e[i].y;
+                    sum += e[i].z;
+                    sum += e[i].w;
+                }
             } else {
                 for (int jj = 0; jj < n; jj++) {
                     if (s_new[jj])
@@ -241,55 +281,158 @@ __global__ __launch_bounds__(64) void k_softmax_rows(float *values, int count, s
 }
 
 // out[t][h][d] = fma chain over keys in order (gemma4.c:296-307): one lane
-// per output channel; the probabilities are wave-uniform.
-__global__ __launch_bounds__(64) void k_attn_values_reference(float *__restrict__ out,
-                                                              const float *__restrict__ probs,
-                                                              const float *__restrict__ value_cache,
-                                                              int cache_len, int head_dim, int heads,
-                                                              int full, int start_pos, size_t stride) {
-    const int d = blockIdx.x * 64 + threadIdx.x, h = blockIdx.y, t = blockIdx.z;
-    const int pos = start_pos + t, first = first_visible(pos, full), keys = pos + 1 - first;
+// per output channel and (token, head) chain.  A block takes a 64-channel
+// slice for WAVES waves; wave w runs the chains of token t0 + w / (8 / HPW)
+// for HPW heads.  V rows are staged in LDS 64 keys at a time, transposed to
+// [channel][key] so a lane reads four keys with one 16-byte load, and DEPTH
+// tiles are prefetched into registers ahead of the chains.  A key outside a
+// token's window is skipped by that token's chains (the order of the keys it
+// does see is unchanged).
+template <int HD, int WAVES, int HPW, int DEPTH>
+__global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ out,
+                                                            const float *__restrict__ probs,
+                                                            const float *__restrict__ value_cache,
+                                                            int cache_len, int full, int start_pos,
+                                                            int n, size_t stride) {
+    constexpr int THREADS = WAVES * 64;
+    constexpr int TOKENS = WAVES * HPW / 8;     // tokens per block
+    constexpr int F4 = 64 * 64 / 4 / THREADS;   // float4 per thread per tile
+    __shared__ __attribute__((aligned(16))) float s_v[64][64 + 4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int d0 = blockIdx.x * 64, t0 = blockIdx.y * TOKENS;
+    const int tn = n - t0 < TOKENS ? n - t0 : TOKENS;
     const int mask = cache_len - 1;
-    const float *p = probs + ((size_t)t * heads + h) * stride;
-    const float *vc = value_cache + d;
-    float o = 0.0f;
-    int k = 0;
-    for (; k + 4 <= keys; k += 4) {
-        const float v0 = vc[(size_t)((first + k) & mask) * head_dim];
-        const float v1 = vc[(size_t)((first + k + 1) & mask) * head_dim];
-        const float v2 = vc[(size_t)((first + k + 2) & mask) * head_dim];
-        const float v3 = vc[(size_t)((first + k + 3) & mask) * head_dim];
-        o = fmaf(p[k], v0, o);
-        o = fmaf(p[k + 1], v1, o);
-        o = fmaf(p[k + 2], v2, o);
-        o = fmaf(p[k + 3], v3, o);
+    const int pos_last = start_pos + t0 + tn - 1;
+    const int kfirst = first_visible(start_pos + t0, full);
+    const int tiles = (pos_last - kfirst + 64) / 64;
+
+    const int my_t = t0 + wave / (8 / HPW), h0 = (wave % (8 / HPW)) * HPW;
+    const bool active = my_t < t0 + tn;
+    const int my_pos = start_pos + my_t, my_first = first_visible(my_pos, full);
+    const float *prow = probs + ((size_t)my_t * 8 + h0) * stride;
+
+    // tile loader: thread covers float4 (key kr, channels 4 cc .. 4 cc + 3)
+    auto load_tile = [&](int tile, float4 (&r)[F4]) {
+#pragma unroll
+        for (int i = 0; i < F4; i++) {
+            const int idx = i * THREADS + tid, kr = idx >> 4, cc = idx & 15;
+            const int p = kfirst + tile * 64 + kr;
+            r[i] = p <= pos_last ? *reinterpret_cast<const float4 *>(
+                                       value_cache + (size_t)(p & mask) * HD + d0 + 4 * cc)
+                                 : make_float4(0, 0, 0, 0);
+        }
+    };
+    float4 ring[DEPTH][F4];
+#pragma unroll
+    for (int s = 0; s < DEPTH; s++)
+        if (s < tiles) load_tile(s, ring[s]);
+
+    float o[HPW];
+#pragma unroll
+    for (int e = 0; e < HPW; e++) o[e] = 0.0f;
+
+    for (int tile = 0; tile < tiles; tile++) {
+        const int slot = tile % DEPTH;
+        __syncthreads();  // previous tile fully consumed
+#pragma unroll
+        for (int s = 0; s < DEPTH; s++) {
+            if (s != slot) continue;
+#pragma unroll
+            for (int i = 0; i < F4; i++) {
+                const int idx = i * THREADS + tid, kr = idx >> 4, cc = idx & 15;
+                s_v[4 * cc + 0][kr] = ring[s][i].x;
+                s_v[4 * cc + 1][kr] = ring[s][i].y;
+                s_v[4 * cc + 2][kr] = ring[s][i].z;
+                s_v[4 * cc + 3][kr] = ring[s][i].w;
+            }
+            if (tile + DEPTH < tiles) load_tile(tile + DEPTH, ring[s]);
+        }
+        __syncthreads();
+        if (!active) continue;
+        const int p0 = kfirst + tile * 64;
+        int k_lo = my_first - p0, k_hi = my_pos - p0 + 1;  // this token's keys in the tile
+        if (k_lo < 0) k_lo = 0;
+        if (k_hi > 64) k_hi = 64;
+        if (k_lo == 0 && k_hi == 64) {
+            const float4 *vr = reinterpret_cast<const float4 *>(s_v[lane]);
+#pragma unroll 4
+            for (int k4 = 0; k4 < 16; k4++) {
+                const float4 v4 = vr[k4];
+                const int pk = p0 + 4 * k4 - my_first;
+#pragma unroll
+                for (int e = 0; e < HPW; e++) {
+                    const float *pe = prow + (size_t)e * stride + pk;
+                    o[e] = fmaf(pe[0], v4.x, o[e]);
+                    o[e] = fmaf(pe[1], v4.y, o[e]);
+                    o[e] = fmaf(pe[2], v4.z, o[e]);
+                    o[e] = fmaf(pe[3], v4.w, o[e]);
+                }
+            }
+        } else {
+            for (int k = k_lo; k < k_hi; k++) {
+                const float vv = s_v[lane][k];
+                const int pk = p0 + k - my_first;
+#pragma unroll
+                for (int e = 0; e < HPW; e++) o[e] = fmaf(prow[(size_t)e * stride + pk], vv, o[e]);
+            }
+        }
     }
-    for (; k < keys; k++) o = fmaf(p[k], vc[(size_t)((first + k) & mask) * head_dim], o);
-    out[((size_t)t * heads + h) * head_dim + d] = o;
+    if (active) {
+#pragma unroll
+        for (int e = 0; e < HPW; e++) out[((size_t)my_t * 8 + h0 + e) * HD + d0 + lane] = o[e];
+    }
 }
 
 int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
                             const float *value_cache, int cache_len, int head_dim, int heads,
                             int full, int start_pos, size_t n) {
     if (!n) return G4_OK;
+    if (heads != 8) return set_error(G4_ERR_ARG, "reference-order attention needs 8 query heads");
     const int last_pos = start_pos + (int)n - 1;
     const int max_keys = full ? last_pos + 1 : (last_pos + 1 < G4_WINDOW ? last_pos + 1 : G4_WINDOW);
     const size_t stride = ((size_t)max_keys + 63) & ~(size_t)63;
-    int rc = scratch_reserve(0, 0, n * heads * stride * sizeof(float));
+    int rc = scratch_reserve(0, n * heads * stride * sizeof(float));
     if (rc) return rc;
     float *scores = scratch().attn;
-    const dim3 grid1((unsigned)((max_keys + 63) / 64), (unsigned)n);
-    if (head_dim == 256)
-        hipLaunchKernelGGL(k_attn_scores<256>, grid1, dim3(256), 0, s, q, key_cache, cache_len,
-                           heads, full, start_pos, stride, scores);
-    else
-        hipLaunchKernelGGL(k_attn_scores<512>, grid1, dim3(256), 0, s, q, key_cache, cache_len,
-                           heads, full, start_pos, stride, scores);
-    hipLaunchKernelGGL(k_attn_softmax_reference, dim3((unsigned)heads, (unsigned)n), dim3(64), 0, s,
-                       scores, heads, full, start_pos, stride);
-    hipLaunchKernelGGL(k_attn_values_reference, dim3((unsigned)(head_dim / 64), (unsigned)heads, (unsigned)n),
-                       dim3(64), 0, s, out, scores, value_cache, cache_len, head_dim, heads, full,
-                       start_pos, stride);
+    // keys spanned by one block of tokens: its first token's window start to
+    // its last token
+    auto span = [&](int tq) {
+        const int tokens = (int)n < tq ? (int)n : tq;
+        const int widest = full ? last_pos + 1 : G4_WINDOW - 1 + tokens;
+        return widest < last_pos + 1 ? widest : last_pos + 1;
+    };
+    const unsigned nn = (unsigned)n;
+    if (head_dim == 256) {
+        constexpr int TQ = 8;
+        dim3 grid((unsigned)((span(TQ) + 63) / 64), (nn + TQ - 1) / TQ);
+        hipLaunchKernelGGL((k_attn_scores<256, TQ>), grid, dim3(256), 0, s, q, key_cache, cache_len,
+                           full, start_pos, (int)n, stride, scores);
+    } else {
+        constexpr int TQ = 4;
+        dim3 grid((unsigned)((span(TQ) + 63) / 64), (nn + TQ - 1) / TQ);
+        hipLaunchKernelGGL((k_attn_scores<512, TQ>), grid, dim3(256), 0, s, q, key_cache, cache_len,
+                           full, start_pos, (int)n, stride, scores);
+    }
+    hipLaunchKernelGGL(k_attn_softmax_reference, dim3((unsigned)heads, nn), dim3(64), 0, s, scores,
+                       heads, full, start_pos, stride);
+    const unsigned slices = (unsigned)(head_dim / 64);
+    if (n <= 4) {  // decode: one token per block, 2 heads per lane, deep prefetch
+        dim3 grid(slices, nn);
+        if (head_dim == 256)
+            hipLaunchKernelGGL((k_attn_values<256, 4, 2, 8>), grid, dim3(256), 0, s, out, scores,
+                               value_cache, cache_len, full, start_pos, (int)n, stride);
+        else
+            hipLaunchKernelGGL((k_attn_values<512, 4, 2, 8>), grid, dim3(256), 0, s, out, scores,
+                               value_cache, cache_len, full, start_pos, (int)n, stride);
+    } else {  // prefill: 16 tokens x 8 heads per block share each V tile
+        dim3 grid(slices, (nn + 15) / 16);
+        if (head_dim == 256)
+            hipLaunchKernelGGL((k_attn_values<256, 16, 8, 2>), grid, dim3(1024), 0, s, out, scores,
+                               value_cache, cache_len, full, start_pos, (int)n, stride);
+        else
+            hipLaunchKernelGGL((k_attn_values<512, 16, 8, 2>), grid, dim3(1024), 0, s, out, scores,
+                               value_cache, cache_len, full, start_pos, (int)n, stride);
+    }
     return G4_OK;
 }
 
