@@ -185,9 +185,9 @@ __global__ __launch_bounds__(64) void k_gemv(float *__restrict__ out, size_t out
         for (int u = 0; u < U; u++) {
             t[u] = tiles[(size_t)(g + u) * 64];
 #pragma unroll
-            for (int m = 0; m < M; m++)
-                x4[u][m] = m < rows ? xrow[((size_t)m * k + (size_t)(g + u) * 64) >> 2] : 0;
-            wsr[u] = fold ? wscale[(g + u) * 16] : 0;
+            for (int m = 0; m < M; m++)  // rows past `rows` reread the last row (unused)
+                x4[u][m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)(g + u) * 64) >> 2];
+            wsr[u] = wscale[(g + u) * 16];
         }
 #pragma unroll
         for (int u = 0; u < U; u++) consume(g + u, t[u], x4[u], wsr[u]);
@@ -196,8 +196,8 @@ __global__ __launch_bounds__(64) void k_gemv(float *__restrict__ out, size_t out
         const uint4 t = tiles[(size_t)g * 64];
         int x4[M];
 #pragma unroll
-        for (int m = 0; m < M; m++) x4[m] = m < rows ? xrow[((size_t)m * k + (size_t)g * 64) >> 2] : 0;
-        consume(g, t, x4, fold ? wscale[g * 16] : 0);
+        for (int m = 0; m < M; m++) x4[m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)g * 64) >> 2];
+        consume(g, t, x4, wscale[g * 16]);
     }
     if (fold && lane < 16) {
 #pragma unroll
@@ -227,19 +227,24 @@ __global__ __launch_bounds__(256) void k_gemv_fold(float *__restrict__ out, size
     int g = 0;
     for (; g + B <= groups; g += B) {
         int dv[B][M];
+        float xv[B][M];
         uint16_t sv[B];
 #pragma unroll
         for (int u = 0; u < B; u++) {
             sv[u] = s[(g + u) * 16];
 #pragma unroll
-            for (int m = 0; m < M; m++) dv[u][m] = m < rows ? d[((size_t)(g + u) * M + m) * 16] : 0;
+            for (int m = 0; m < M; m++) {
+                const int mm = min(m, rows - 1);
+                dv[u][m] = d[((size_t)(g + u) * M + mm) * 16];
+                xv[u][m] = xs[(size_t)mm * groups + g + u];
+            }
         }
 #pragma unroll
         for (int u = 0; u < B; u++) {
             const float wsf = half_bits_to_float(sv[u]);
 #pragma unroll
             for (int m = 0; m < M; m++)
-                if (m < rows) acc[m] = fmaf((float)dv[u][m], wsf * xs[(size_t)m * groups + g + u], acc[m]);
+                if (m < rows) acc[m] = fmaf((float)dv[u][m], wsf * xv[u][m], acc[m]);
         }
     }
     for (; g < groups; g++) {
@@ -255,92 +260,177 @@ __global__ __launch_bounds__(256) void k_gemv_fold(float *__restrict__ out, size
 }
 
 // ---------------------------------------------------------------------------
-// W8A8 matmul, many rows (prefill): int8 MFMA GEMM, 64x64 output tile per
-// 256-thread block, one 64-deep K step per quantization group.
+// W8A8 matmul, many rows (prefill): int8 MFMA GEMM, 64 x BN output tile per
+// 256-thread block (2 x 2 waves of 32 x BN/2), one 64-deep K step per
+// quantization group.
 //
 // v_mfma_i32_16x16x64_i8: lane l supplies 16 bytes of A row (l%16) and of B
-// column (l%16), both for k-slots 16(l/16)..16(l/16)+15; the output element
-// (i, j) = (4(l/16)+v, l%16) comes back in lane l, register v.  B comes straight
-// from the packed tiles: column n, k = 16q + b lives at chunk 4q + b/4, so a
-// lane gathers 4 dwords from the staged tile.  Every MFMA covers exactly one
-// group, so the group-ordered fp32 fold is the reference's.
+// column (l%16), both for k-slots 16(l/16)..16(l/16)+15; output element
+// (i, j) = (4(l/16)+v, l%16) comes back in lane l, register v.  Every MFMA
+// covers exactly one group, so the group-ordered fp32 fold is the reference's
+// (bit-identical).
+//
+// Pipeline (one barrier per group): at the top of iteration g, LDS buffer
+// (g+1)&1 holds group g+1 and registers hold group g+2, loaded from global
+// memory during iteration g-1.  Each wave then
+//   1. reads its A/B fragments and scales of group g+1 from LDS,
+//   2. folds group g's int32 dots (computed by the MFMAs of iteration g-1),
+//   3. issues the MFMAs of group g+1 (they run on the matrix core while the
+//      next iteration's barrier, reads and fold proceed),
+//   4. stores group g+2 into buffer g&1 (read during iteration g-1) and
+//      issues the global loads of group g+3.
+// So the VALU fold of one group overlaps the MFMAs of the next.  The B tiles
+// are reordered on the way into LDS from the packed [chunk][row][4] layout to
+// row-major rows of 64 bytes, so each lane reads its B operand with one
+// 16-byte load; rows are padded to 80 bytes.
 
+template <int BN>
 __global__ __launch_bounds__(256) void k_gemm(float *__restrict__ out, size_t out_stride,
                                               const int8_t *__restrict__ xq,
                                               const float *__restrict__ xs,
                                               const int8_t *__restrict__ w,
                                               const uint16_t *__restrict__ ws, int rows,
                                               int n_out, int k) {
-    const int groups = k >> 6;
-    const int m0 = blockIdx.y * 64, nb0 = blockIdx.x * 4, n_blocks = n_out >> 4;
-    __shared__ __attribute__((aligned(16))) int8_t s_a[64 * 64];
-    __shared__ __attribute__((aligned(16))) int8_t s_b[4 * 1024];
-    __shared__ float s_xs[64], s_ws[64];
+    constexpr int BM = 64, NT = BN / 16, WN = BN / 2, NI = WN / 16, RS = 80;
+    constexpr int BV = NT / 4;  // 16-byte B loads per thread per group
+    __shared__ __attribute__((aligned(16))) int8_t s_a[2][BM * RS];
+    __shared__ __attribute__((aligned(16))) int8_t s_b[2][BN * RS];
+    __shared__ __attribute__((aligned(16))) float s_xs[2][BM];
+    __shared__ __attribute__((aligned(16))) float s_ws[2][BN];
+    const int groups = k >> 6, m0 = blockIdx.y * BM, nb0 = blockIdx.x * NT, n_blocks = n_out >> 4;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1, q = lane >> 4, l16 = lane & 15;
-    float acc[2][2][4];
+    const v4i zero = {0, 0, 0, 0};
+
+    // Rows past `rows`, tiles past n_out and groups past the last are loaded
+    // from the last valid one instead (their results are never used), so
+    // every load is unconditional.
+    const int a_row = tid >> 2, a_part = tid & 3;
+    const int8_t *a_src = xq + (size_t)min(m0 + a_row, rows - 1) * k + a_part * 16;
+    const float *x_src = xs + (size_t)min(m0 + (tid & (BM - 1)), rows - 1) * groups;
+    const int w_n = (tid - BM) & (BN - 1);
+    const uint16_t *w_src = ws + (size_t)min(nb0 + (w_n >> 4), n_blocks - 1) * groups * 16 + (w_n & 15);
+
+    struct Stage {
+        v4i a, b[BV];
+        float x;
+        uint16_t w;
+    };
+    auto gload = [&](int g, Stage &st) {
+        g = min(g, groups - 1);
+        st.a = *reinterpret_cast<const v4i *>(a_src + g * 64);
+#pragma unroll
+        for (int j = 0; j < BV; j++) {
+            const int idx = j * 256 + tid, t = min(nb0 + (idx >> 6), n_blocks - 1);
+            st.b[j] = *reinterpret_cast<const v4i *>(w + ((size_t)t * groups + g) * 1024 + (idx & 63) * 16);
+        }
+        st.x = x_src[g];  // every thread loads a scale; threads < BM + BN keep theirs
+        st.w = w_src[g * 16];
+    };
+    auto sstore = [&](int buf, const Stage &st) {
+        *reinterpret_cast<v4i *>(s_a[buf] + a_row * RS + a_part * 16) = st.a;
+#pragma unroll
+        for (int j = 0; j < BV; j++) {
+            const int idx = j * 256 + tid, t = idx >> 6, i = idx & 63, c = i >> 2, rq = i & 3;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+                *reinterpret_cast<int *>(s_b[buf] + (t * 16 + rq * 4 + jj) * RS + c * 4) = st.b[j][jj];
+        }
+        if (tid < BM)
+            s_xs[buf][tid] = st.x;
+        else if (tid < BM + BN)
+            s_ws[buf][tid - BM] = half_bits_to_float(st.w);
+    };
+
+    struct Frag {
+        v4i a[2], b[NI];
+        float4 x[2];
+        float w[NI];
+    };
+    auto fread = [&](int buf, Frag &f) {
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+            const int r = wm * 32 + mi * 16;
+            f.a[mi] = *reinterpret_cast<const v4i *>(s_a[buf] + (r + l16) * RS + q * 16);
+            f.x[mi] = *reinterpret_cast<const float4 *>(&s_xs[buf][r + 4 * q]);
+        }
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++) {
+            const int c = wn * WN + ni * 16 + l16;
+            f.b[ni] = *reinterpret_cast<const v4i *>(s_b[buf] + c * RS + q * 16);
+            f.w[ni] = s_ws[buf][c];
+        }
+    };
+    struct Dots {
+        v4i d[2][NI];
+        float4 x[2];
+        float w[NI];
+    };
+    auto mfma = [&](const Frag &f, Dots &o) {
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+                o.d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[mi], f.b[ni], zero, 0, 0, 0);
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) o.x[mi] = f.x[mi];
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++) o.w[ni] = f.w[ni];
+    };
+
+    float acc[2][NI][4];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < NI; j++)
 #pragma unroll
             for (int v = 0; v < 4; v++) acc[i][j][v] = 0.0f;
-    const v4i zero = {0, 0, 0, 0};
-
-    for (int g = 0; g < groups; g++) {
-        {
-            const int r = tid >> 2, part = tid & 3;
-            v4i v = zero;
-            if (m0 + r < rows)
-                v = *reinterpret_cast<const v4i *>(xq + (size_t)(m0 + r) * k + g * 64 + part * 16);
-            *reinterpret_cast<v4i *>(s_a + r * 64 + part * 16) = v;
-        }
-        {
-            const int t = tid >> 6;
-            v4i v = zero;
-            if (nb0 + t < n_blocks)
-                v = *reinterpret_cast<const v4i *>(w + ((size_t)(nb0 + t) * groups + g) * 1024 +
-                                                   lane * 16);
-            *reinterpret_cast<v4i *>(s_b + t * 1024 + lane * 16) = v;
-        }
-        if (tid < 64) {
-            s_xs[tid] = m0 + tid < rows ? xs[(size_t)(m0 + tid) * groups + g] : 0.0f;
-        } else if (tid < 128) {
-            const int n = tid - 64, t = n >> 4;
-            s_ws[n] = nb0 + t < n_blocks
-                          ? half_bits_to_float(ws[((size_t)(nb0 + t) * groups + g) * 16 + (n & 15)])
-                          : 0.0f;
-        }
-        __syncthreads();
+    auto fold = [&](const Dots &o) {
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++) {
-            const v4i a = *reinterpret_cast<const v4i *>(s_a + (wm * 32 + mi * 16 + l16) * 64 + q * 16);
+        for (int ni = 0; ni < NI; ni++)
 #pragma unroll
-            for (int ni = 0; ni < 2; ni++) {
-                const int t = wn * 2 + ni;
-                const int *bt = reinterpret_cast<const int *>(s_b + t * 1024);
-                v4i b;
-                b.x = bt[(4 * q + 0) * 16 + l16];
-                b.y = bt[(4 * q + 1) * 16 + l16];
-                b.z = bt[(4 * q + 2) * 16 + l16];
-                b.w = bt[(4 * q + 3) * 16 + l16];
-                const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, zero, 0, 0, 0);
-                const float wsf = s_ws[t * 16 + l16];
-#pragma unroll
-                for (int v = 0; v < 4; v++)
-                    acc[mi][ni][v] = fmaf((float)d[v], wsf * s_xs[wm * 32 + mi * 16 + 4 * q + v],
-                                          acc[mi][ni][v]);
+            for (int mi = 0; mi < 2; mi++) {
+                acc[mi][ni][0] = fmaf((float)o.d[mi][ni][0], o.w[ni] * o.x[mi].x, acc[mi][ni][0]);
+                acc[mi][ni][1] = fmaf((float)o.d[mi][ni][1], o.w[ni] * o.x[mi].y, acc[mi][ni][1]);
+                acc[mi][ni][2] = fmaf((float)o.d[mi][ni][2], o.w[ni] * o.x[mi].z, acc[mi][ni][2]);
+                acc[mi][ni][3] = fmaf((float)o.d[mi][ni][3], o.w[ni] * o.x[mi].w, acc[mi][ni][3]);
             }
-        }
+    };
+
+    Stage st;
+    Frag fr;
+    Dots dots[2];
+    gload(0, st);
+    sstore(0, st);
+    gload(1, st);
+    sstore(1, st);
+    gload(2, st);
+    __syncthreads();
+    fread(0, fr);
+    mfma(fr, dots[0]);
+    // One iteration per group; unrolled by two so the dots slot is static.
+    auto step = [&](int g, Dots &cur, Dots &next) {
         __syncthreads();
+        const bool more = g + 1 < groups;  // uniform across the block
+        if (more) fread((g + 1) & 1, fr);
+        fold(cur);
+        if (more) {
+            mfma(fr, next);
+            sstore(g & 1, st);
+            gload(g + 3, st);
+        }
+    };
+    for (int g = 0; g < groups; g += 2) {
+        step(g, dots[0], dots[1]);
+        if (g + 1 < groups) step(g + 1, dots[1], dots[0]);
     }
 #pragma unroll
     for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-        for (int ni = 0; ni < 2; ni++) {
-            const int t = wn * 2 + ni;
-            if (nb0 + t >= n_blocks) continue;
-            const size_t n = (size_t)(nb0 + t) * 16 + l16;
+        for (int ni = 0; ni < NI; ni++) {
+            const int col = wn * WN + ni * 16;
+            if (nb0 + (col >> 4) >= n_blocks) continue;
+            const size_t n = (size_t)nb0 * 16 + col + l16;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int m = m0 + wm * 32 + mi * 16 + 4 * q + v;
@@ -354,9 +444,9 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
     if (rows <= 0) return G4_OK;
     const int blocks = n_out / 16, groups = k / 64;
     if (rows > 8) {
-        dim3 grid((unsigned)((blocks + 3) / 4), (unsigned)((rows + 63) / 64));
-        hipLaunchKernelGGL(k_gemm, grid, dim3(256), 0, s, out, out_stride, xq, xs, w, ws, rows,
-                           n_out, k);
+        const unsigned mb = (unsigned)((rows + 63) / 64);
+        hipLaunchKernelGGL((k_gemm<64>), dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
+                           out, out_stride, xq, xs, w, ws, rows, n_out, k);
         return G4_OK;
     }
     const int m_pad = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;

@@ -92,26 +92,40 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reference(float *out, const flo
     if (valid && lane == 0) {
         if (staged) {
             // Batches of 64 squares are read into registers ahead of the add
-            // chain that consumes them, so the chain never waits on LDS.
+            // chain that consumes them (two alternating buffers), so the chain
+            // never waits on LDS.
             const float4 *sq = reinterpret_cast<const float4 *>(s_sq[wave]);
             const int batches = width / 64;
-            float4 cur[16], next[16];
+            float4 ba[16], bb[16];
+            if (batches > 0) {
 #pragma unroll
-            for (int j = 0; j < 16; j++) cur[j] = batches > 0 ? sq[j] : make_float4(0, 0, 0, 0);
-            for (int b = 0; b < batches; b++) {
+                for (int j = 0; j < 16; j++) ba[j] = sq[j];
+            }
+            for (int b = 0; b < batches; b += 2) {
                 if (b + 1 < batches) {
 #pragma unroll
-                    for (int j = 0; j < 16; j++) next[j] = sq[(b + 1) * 16 + j];
+                    for (int j = 0; j < 16; j++) bb[j] = sq[(b + 1) * 16 + j];
                 }
 #pragma unroll
                 for (int j = 0; j < 16; j++) {
-                    sum += cur[j].x;
-                    sum += cur[j].y;
-                    sum += cur[j].z;
-                    sum += cur[j].w;
+                    sum += ba[j].x;
+                    sum += ba[j].y;
+                    sum += ba[j].z;
+                    sum += ba[j].w;
                 }
+                if (b + 2 < batches) {
 #pragma unroll
-                for (int j = 0; j < 16; j++) cur[j] = next[j];
+                    for (int j = 0; j < 16; j++) ba[j] = sq[(b + 2) * 16 + j];
+                }
+                if (b + 1 < batches) {
+#pragma unroll
+                    for (int j = 0; j < 16; j++) {
+                        sum += bb[j].x;
+                        sum += bb[j].y;
+                        sum += bb[j].z;
+                        sum += bb[j].w;
+                    }
+                }
             }
             for (int i = batches * 64; i < width; i++) sum += s_sq[wave][i];
         } else {
@@ -150,15 +164,15 @@ __device__ __forceinline__ int first_visible(int pos, int full) {
 // lanes per key, lane m an fma chain over channels m, m+16, ... (s ascending),
 // then the fixed tree.  A block takes TQ tokens x 8 heads against 64 keys: each
 // 16-lane group keeps its key's channel slice in registers and reads the query
-// rows from LDS, stored [row][m][s] so a lane's chain is contiguous (16-byte
-// LDS loads).  scores[(t * 8 + h) * stride + (p - first(t))] for key position p.
+// rows from LDS, stored [row][m][s] (padded) so a lane's chain is contiguous
+// (16-byte LDS loads, bank-conflict free).  scores[(t * 8 + h) * stride + (p - first(t))] for key position p.
 template <int HD, int TQ>
 __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q,
                                                      const float *__restrict__ key_cache,
                                                      int cache_len, int full, int start_pos, int n,
                                                      size_t stride, float *__restrict__ scores) {
-    constexpr int S = HD / 16;
-    __shared__ __attribute__((aligned(16))) float s_q[TQ * 8][16][S];
+    constexpr int S = HD / 16, SP = S + 4;  // +4 floats: the 16 lanes' 16-byte reads hit distinct banks
+    __shared__ __attribute__((aligned(16))) float s_q[TQ * 8][16][SP];
     const int t0 = blockIdx.y * TQ;
     const int tn = n - t0 < TQ ? n - t0 : TQ;
     const int pos_last = start_pos + t0 + tn - 1;
@@ -298,7 +312,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
     constexpr int TOKENS = WAVES * HPW / 8;     // tokens per block
     constexpr int F4 = 64 * 64 / 4 / THREADS;   // float4 per thread per tile
     __shared__ __attribute__((aligned(16))) float s_v[64][64 + 4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave is made provably uniform so the probability loads below are scalar
+    // loads: vector loads would retire in order behind the V prefetch ring.
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int d0 = blockIdx.x * 64, t0 = blockIdx.y * TOKENS;
     const int tn = n - t0 < TOKENS ? n - t0 : TOKENS;
     const int mask = cache_len - 1;
@@ -316,39 +333,36 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
 #pragma unroll
         for (int i = 0; i < F4; i++) {
             const int idx = i * THREADS + tid, kr = idx >> 4, cc = idx & 15;
-            const int p = kfirst + tile * 64 + kr;
-            r[i] = p <= pos_last ? *reinterpret_cast<const float4 *>(
-                                       value_cache + (size_t)(p & mask) * HD + d0 + 4 * cc)
-                                 : make_float4(0, 0, 0, 0);
+            // keys past the block's last position are never consumed; loading a
+            // valid row instead keeps the loads unconditional (no drain)
+            const int p = min(kfirst + tile * 64 + kr, pos_last);
+            r[i] = *reinterpret_cast<const float4 *>(value_cache + (size_t)(p & mask) * HD + d0 + 4 * cc);
         }
     };
     float4 ring[DEPTH][F4];
 #pragma unroll
-    for (int s = 0; s < DEPTH; s++)
-        if (s < tiles) load_tile(s, ring[s]);
+    for (int s = 0; s < DEPTH; s++) load_tile(min(s, tiles - 1), ring[s]);
 
     float o[HPW];
 #pragma unroll
     for (int e = 0; e < HPW; e++) o[e] = 0.0f;
 
-    for (int tile = 0; tile < tiles; tile++) {
-        const int slot = tile % DEPTH;
+    // One tile: stage ring slot `s` in LDS, refill the slot DEPTH tiles ahead,
+    // then run this wave's chains over the tile.  The loop below is unrolled by
+    // DEPTH so every slot index is a compile-time constant (precise waits).
+    auto step = [&](int tile, float4 (&slot)[F4]) {
         __syncthreads();  // previous tile fully consumed
 #pragma unroll
-        for (int s = 0; s < DEPTH; s++) {
-            if (s != slot) continue;
-#pragma unroll
-            for (int i = 0; i < F4; i++) {
-                const int idx = i * THREADS + tid, kr = idx >> 4, cc = idx & 15;
-                s_v[4 * cc + 0][kr] = ring[s][i].x;
-                s_v[4 * cc + 1][kr] = ring[s][i].y;
-                s_v[4 * cc + 2][kr] = ring[s][i].z;
-                s_v[4 * cc + 3][kr] = ring[s][i].w;
-            }
-            if (tile + DEPTH < tiles) load_tile(tile + DEPTH, ring[s]);
+        for (int i = 0; i < F4; i++) {
+            const int idx = i * THREADS + tid, kr = idx >> 4, cc = idx & 15;
+            s_v[4 * cc + 0][kr] = slot[i].x;
+            s_v[4 * cc + 1][kr] = slot[i].y;
+            s_v[4 * cc + 2][kr] = slot[i].z;
+            s_v[4 * cc + 3][kr] = slot[i].w;
         }
+        load_tile(min(tile + DEPTH, tiles - 1), slot);  // unconditional refill
         __syncthreads();
-        if (!active) continue;
+        if (!active || tile >= tiles) return;
         const int p0 = kfirst + tile * 64;
         int k_lo = my_first - p0, k_hi = my_pos - p0 + 1;  // this token's keys in the tile
         if (k_lo < 0) k_lo = 0;
@@ -376,6 +390,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
                 for (int e = 0; e < HPW; e++) o[e] = fmaf(prow[(size_t)e * stride + pk], vv, o[e]);
             }
         }
+    };
+    for (int tile = 0; tile < tiles; tile += DEPTH) {
+#pragma unroll
+        for (int s = 0; s < DEPTH; s++) step(tile + s, ring[s]);
     }
     if (active) {
 #pragma unroll
@@ -403,12 +421,12 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
     };
     const unsigned nn = (unsigned)n;
     if (head_dim == 256) {
-        constexpr int TQ = 8;
+        constexpr int TQ = 6;
         dim3 grid((unsigned)((span(TQ) + 63) / 64), (nn + TQ - 1) / TQ);
         hipLaunchKernelGGL((k_attn_scores<256, TQ>), grid, dim3(256), 0, s, q, key_cache, cache_len,
                            full, start_pos, (int)n, stride, scores);
     } else {
-        constexpr int TQ = 4;
+        constexpr int TQ = 3;
         dim3 grid((unsigned)((span(TQ) + 63) / 64), (nn + TQ - 1) / TQ);
         hipLaunchKernelGGL((k_attn_scores<512, TQ>), grid, dim3(256), 0, s, q, key_cache, cache_len,
                            full, start_pos, (int)n, stride, scores);
