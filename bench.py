@@ -49,6 +49,21 @@ def gemv_bytes(n: int, k: int) -> int:
     return n * k + n * k // 32 + k + k // 16 + 4 * n
 
 
+def pmc_traffic(name: str):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE passes scaled by a copy-kernel calibration,
+    written by the commands listed in the file), or None if it is absent."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def random_weight(torch, n: int, k: int, gen):
     """int8 U[-127, 127] packed weights, fp16 scales log-uniform in [1e-3, 1e-2]."""
     w = torch.randint(-127, 128, (n * k,), dtype=torch.int8, device="cuda", generator=gen)
@@ -102,6 +117,39 @@ def gemm_roofline(pkg, lib, torch) -> dict:
     tops = ops / (ms * 1e-3) / 1e12
     moved = n * k + n * k // 32 + m * k + m * k // 16 + 4 * m * n
     return {"kernel": "k_gemm", "ms_per_launch": ms, "tops": tops, "bytes": moved, "ops": ops}
+
+
+def probe(pkg, lib, torch, what: str, launches: int = 20) -> None:
+    """Launch one kernel alone, for hardware-counter runs under rocprofv3 --pmc:
+    `gemm` = the prefill GEMM above, `gemv` = the lm_head GEMV (262144 x 1536,
+    one token), `copy` = a 256 MiB device-to-device copy (the calibration
+    kernel: it reads and writes exactly 268,435,456 bytes)."""
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    stream = torch.cuda.current_stream().cuda_stream
+    if what == "copy":
+        a = torch.empty(64 << 20, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(launches):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        return
+    m, n, k = (512, 6144, 1536) if what == "gemm" else (1, 262144, 1536)
+    x = torch.randn((m, k), device="cuda", generator=gen)
+    xq = torch.empty((m, k), dtype=torch.int8, device="cuda")
+    xs = torch.empty((m, k // 64), dtype=torch.float32, device="cuda")
+    pkg.check(lib.g4_quantize(stream, xq.data_ptr(), xs.data_ptr(), x.data_ptr(), m, k))
+    copies = 8 if what == "gemm" else 2
+    ws = [random_weight(torch, n, k, gen) for _ in range(copies)]
+    recs = []
+    for w, s in ws:
+        rec = pkg.Tensor()
+        rec.data, rec.scales = w.data_ptr(), s.data_ptr()
+        rec.shape[0], rec.shape[1] = n, k
+        recs.append(rec)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    for i in range(launches):
+        pkg.check(lib.g4_matmul_int8(stream, out.data_ptr(), xq.data_ptr(), xs.data_ptr(), recs[i % copies], m))
+    torch.cuda.synchronize()
 
 
 def gemv_sweep(pkg, lib, torch) -> dict:
@@ -238,6 +286,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--order", choices=["reference", "parallel"], default="reference")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--probe", choices=["gemm", "gemv", "copy"],
+                    help="only launch one kernel 20 times (for rocprofv3 --pmc runs); no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -254,6 +304,9 @@ def main() -> int:
     pkg = __graft_entry__.load_package()
     lib = pkg.lib()
     lib.g4_set_order(pkg.ORDER_REFERENCE if args.order == "reference" else pkg.ORDER_PARALLEL)
+    if args.probe:
+        probe(pkg, lib, torch, args.probe)
+        return 0
 
     t = time.perf_counter()
     image = pkg.Image.synthetic(seed=MODEL_SEED)
@@ -303,7 +356,9 @@ def main() -> int:
             "peak": INT8_MFMA_PEAK_TOPS,
             "unit": "TOPS",
             "frac": round(gemm["tops"] / INT8_MFMA_PEAK_TOPS, 4),
-            "traffic": None,
+            "traffic": pmc_traffic("k_gemm_512x6144x1536_pmc.txt"),
+            "algorithmic_bytes": gemm["bytes"],
+            "traffic_source": "profiles/k_gemm_512x6144x1536_pmc.txt (HBM bytes per launch)",
         },
         "roofline_decode": {
             "bound": "hbm",
@@ -314,7 +369,8 @@ def main() -> int:
             "frac": round(sweep["byte_weighted_gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_token": sweep["bytes_per_token"],
             "per_shape_gbs": sweep["per_shape"],
-            "traffic": None,
+            "traffic": pmc_traffic("k_gemv_262144x1536_pmc.txt"),
+            "traffic_source": "profiles/k_gemv_262144x1536_pmc.txt (HBM bytes per lm_head launch)",
         },
         "cpu_baseline": cpu,
     }
