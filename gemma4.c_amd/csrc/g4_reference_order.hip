@@ -71,10 +71,84 @@ __device__ __forceinline__ float expf_libm(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// rmsnorm, reference order: one wave per row.
+// rmsnorm, reference order: one wave per row.  The sum of squares is the
+// reference's sequential fp32 chain (gemma4.c:366-368); the squares are
+// computed in parallel (each is rounded on its own in the reference too), so
+// only the dependent adds run on one lane.
 
 constexpr int kNormMaxWidth = 1536;
 
+// Runtime length (any width): 64 squares per step, loaded just before use.
+__device__ __forceinline__ float chain_lds(const float4 *sq, int batches) {
+    float sum = 0.0f;
+    for (int b = 0; b < batches; b++) {
+        float4 v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = sq[b * 16 + j];
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            sum += v[j].x;
+            sum += v[j].y;
+            sum += v[j].z;
+            sum += v[j].w;
+        }
+    }
+    return sum;
+}
+
+// Widths 256 * V (V = 1, 2, 6: per-head norms of 256 and 512, and the
+// hidden 1536).  Every lane holds its 4V values, squares and weights in
+// registers (loaded once, all loads in flight).  The chain then walks the
+// row in order, element k = 256 v + 4 l + c living in lane l, register
+// (v, c): each square is broadcast with v_readlane into a scalar register
+// and added by the whole wave, so every lane ends with the same sum and no
+// LDS or barrier is involved.  The readlanes do not depend on the chain and
+// fill its dependent-add stalls.
+template <int V>
+__global__ __launch_bounds__(256) void k_rmsnorm_reference_v(float *out, const float *in,
+                                                             const float *__restrict__ weight,
+                                                             float eps, size_t rows) {
+    constexpr int W = 256 * V;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t wave_row = (size_t)blockIdx.x * 4 + wave;
+    if (wave_row >= rows) return;  // uniform per wave; no block-level barrier follows
+    const float4 *x4 = reinterpret_cast<const float4 *>(in + wave_row * W);
+    float4 xv[V], wv[V];
+#pragma unroll
+    for (int v = 0; v < V; v++) xv[v] = x4[v * 64 + lane];
+    if (weight) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(weight);
+#pragma unroll
+        for (int v = 0; v < V; v++) wv[v] = w4[v * 64 + lane];
+    } else {
+#pragma unroll
+        for (int v = 0; v < V; v++) wv[v] = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
+    float sq[V][4];
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+        sq[v][0] = xv[v].x * xv[v].x;
+        sq[v][1] = xv[v].y * xv[v].y;
+        sq[v][2] = xv[v].z * xv[v].z;
+        sq[v][3] = xv[v].w * xv[v].w;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; v++)
+#pragma unroll
+        for (int l = 0; l < 64; l++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sq[v][c]), l));
+    const float inverse = 1.0f / sqrtf(sum / (float)W + eps);
+    float4 *y4 = reinterpret_cast<float4 *>(out + wave_row * W);
+#pragma unroll
+    for (int v = 0; v < V; v++)
+        y4[v * 64 + lane] = make_float4(wv[v].x * (inverse * xv[v].x), wv[v].y * (inverse * xv[v].y),
+                                        wv[v].z * (inverse * xv[v].z), wv[v].w * (inverse * xv[v].w));
+}
+
+// Any other width (per-op entry point): the same order, plainer loads.
 __global__ __launch_bounds__(256) void k_rmsnorm_reference(float *out, const float *in,
                                                            const float *__restrict__ weight,
                                                            int width, float eps, size_t rows) {
@@ -91,42 +165,8 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reference(float *out, const flo
     float sum = 0.0f;
     if (valid && lane == 0) {
         if (staged) {
-            // Batches of 64 squares are read into registers ahead of the add
-            // chain that consumes them (two alternating buffers), so the chain
-            // never waits on LDS.
-            const float4 *sq = reinterpret_cast<const float4 *>(s_sq[wave]);
             const int batches = width / 64;
-            float4 ba[16], bb[16];
-            if (batches > 0) {
-#pragma unroll
-                for (int j = 0; j < 16; j++) ba[j] = sq[j];
-            }
-            for (int b = 0; b < batches; b += 2) {
-                if (b + 1 < batches) {
-#pragma unroll
-                    for (int j = 0; j < 16; j++) bb[j] = sq[(b + 1) * 16 + j];
-                }
-#pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    sum += ba[j].x;
-                    sum += ba[j].y;
-                    sum += ba[j].z;
-                    sum += ba[j].w;
-                }
-                if (b + 2 < batches) {
-#pragma unroll
-                    for (int j = 0; j < 16; j++) ba[j] = sq[(b + 2) * 16 + j];
-                }
-                if (b + 1 < batches) {
-#pragma unroll
-                    for (int j = 0; j < 16; j++) {
-                        sum += bb[j].x;
-                        sum += bb[j].y;
-                        sum += bb[j].z;
-                        sum += bb[j].w;
-                    }
-                }
-            }
+            if (batches > 0) sum = chain_lds(reinterpret_cast<const float4 *>(s_sq[wave]), batches);
             for (int i = batches * 64; i < width; i++) sum += s_sq[wave][i];
         } else {
             for (int i = 0; i < width; i++) sum += x[i] * x[i];
@@ -141,8 +181,18 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reference(float *out, const flo
 void launch_rmsnorm_reference(hipStream_t s, float *out, const float *in, const float *weight,
                               int width, float eps, size_t rows) {
     if (!rows) return;
-    hipLaunchKernelGGL(k_rmsnorm_reference, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, out,
-                       in, weight, width, eps, rows);
+    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    // float4 paths need 16-byte aligned rows and weights
+    const bool aligned = ((uintptr_t)in % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
+                         ((uintptr_t)weight % 16 == 0);
+    if (aligned && width == 1536)
+        hipLaunchKernelGGL(k_rmsnorm_reference_v<6>, grid, block, 0, s, out, in, weight, eps, rows);
+    else if (aligned && width == 512)
+        hipLaunchKernelGGL(k_rmsnorm_reference_v<2>, grid, block, 0, s, out, in, weight, eps, rows);
+    else if (aligned && width == 256)
+        hipLaunchKernelGGL(k_rmsnorm_reference_v<1>, grid, block, 0, s, out, in, weight, eps, rows);
+    else
+        hipLaunchKernelGGL(k_rmsnorm_reference, grid, block, 0, s, out, in, weight, width, eps, rows);
 }
 
 void launch_rmsnorm(hipStream_t s, float *out, const float *in, const float *weight, int width,
@@ -158,6 +208,13 @@ void launch_rmsnorm(hipStream_t s, float *out, const float *in, const float *wei
 
 __device__ __forceinline__ int first_visible(int pos, int full) {
     return !full && pos + 1 > G4_WINDOW ? pos + 1 - G4_WINDOW : 0;
+}
+
+// Lane l of each 16-lane row receives x from lane l + N of the same row
+// (DPP row_shl; lanes past the row's end receive 0).
+template <int N>
+__device__ __forceinline__ float row_shl(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + N, 0xf, 0xf, true));
 }
 
 // Scores of every (token, head, visible key), exact (gemma4.c:281-294): 16
@@ -193,36 +250,67 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
         float kv[S];
 #pragma unroll
         for (int s = 0; s < S; s++) kv[s] = kr[16 * s];
-        for (int row = 0; row < tn * 8; row++) {
-            const int t = t0 + row / 8, pos = start_pos + t, first = first_visible(pos, full);
-            const float4 *qv = reinterpret_cast<const float4 *>(s_q[row][m]);
-            float acc = 0.0f;
+        // The 8 heads of a token are 8 independent chains: interleaving them
+        // hides the fma latency.
+        for (int tt = 0; tt < tn; tt++) {
+            const int t = t0 + tt, pos = start_pos + t, first = first_visible(pos, full);
+            float acc[8];
+#pragma unroll
+            for (int h = 0; h < 8; h++) acc[h] = 0.0f;
 #pragma unroll
             for (int s4 = 0; s4 < S / 4; s4++) {
-                const float4 qq = qv[s4];
-                acc = fmaf(qq.x, kv[4 * s4 + 0], acc);
-                acc = fmaf(qq.y, kv[4 * s4 + 1], acc);
-                acc = fmaf(qq.z, kv[4 * s4 + 2], acc);
-                acc = fmaf(qq.w, kv[4 * s4 + 3], acc);
+#pragma unroll
+                for (int h = 0; h < 8; h++) {
+                    const float4 qq = reinterpret_cast<const float4 *>(s_q[tt * 8 + h][m])[s4];
+                    acc[h] = fmaf(qq.x, kv[4 * s4 + 0], acc[h]);
+                    acc[h] = fmaf(qq.y, kv[4 * s4 + 1], acc[h]);
+                    acc[h] = fmaf(qq.z, kv[4 * s4 + 2], acc[h]);
+                    acc[h] = fmaf(qq.w, kv[4 * s4 + 3], acc[h]);
+                }
             }
-            acc += __shfl_down(acc, 8, 16);
-            acc += __shfl_down(acc, 4, 16);
-            acc += __shfl_down(acc, 2, 16);
-            acc += __shfl_down(acc, 1, 16);
-            if (m == 0 && p >= first && p <= pos)
-                scores[((size_t)t * 8 + (row & 7)) * stride + (p - first)] = acc;
+            // the reference's tree: (l, l+8), then (l, l+4), then
+            // (0+2) + (1+3); DPP row shifts stay inside each 16-lane group
+#pragma unroll
+            for (int h = 0; h < 8; h++) {
+                float a = acc[h];
+                a += row_shl<8>(a);
+                a += row_shl<4>(a);
+                a += row_shl<2>(a);
+                a += row_shl<1>(a);
+                acc[h] = a;
+            }
+            if (m == 0 && p >= first && p <= pos) {
+                float *dst = scores + (size_t)t * 8 * stride + (p - first);
+#pragma unroll
+                for (int h = 0; h < 8; h++) dst[(size_t)h * stride] = acc[h];
+            }
         }
     }
 }
 
-// Softmax of one row in place (gemma4.c:400-408), by one wave.  Per block of
-// 64 values: a prefix-max scan gives each value the maximum m seen before it;
-// a value above m contributes expf(m - v) as a rescale factor (the sum becomes
-// s * e + 1), any other value expf(v - m) as an addend.  Lane 0 applies the
-// recurrence in index order, reading its operands from LDS in batches so the
-// chain never waits on memory; the next block's values are loaded meanwhile.
-// Then p = expf(v - max) / sum.
-__device__ void softmax_row_reference(float *v, int count, float *s_e, int *s_new) {
+// Inclusive max-scan over the 64 lanes (max is exact in any order): DPP row
+// shifts within each 16-lane row, then row broadcasts across rows.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max_step(float x) {
+    const float y = __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+    return fmaxf(x, y);
+}
+__device__ __forceinline__ float wave_max_scan(float x) {
+    x = dpp_max_step<0x111, 0xf>(x);  // row_shr:1
+    x = dpp_max_step<0x112, 0xf>(x);  // row_shr:2
+    x = dpp_max_step<0x114, 0xf>(x);  // row_shr:4
+    x = dpp_max_step<0x118, 0xf>(x);  // row_shr:8
+    x = dpp_max_step<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+    x = dpp_max_step<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+    return x;
+}
+// Lane l receives lane l - 1's value (wave_shr:1; lane 0 receives 0).
+__device__ __forceinline__ float wave_shr1(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x138, 0xf, 0xf, false));
+}
+
+__device__ void softmax_row_reference(float *v, int count) {
     const int lane = threadIdx.x & 63;
     float carry = v[0];  // max = values[0], sum = 1 (gemma4.c:401)
     float sum = 1.0f;
@@ -231,77 +319,72 @@ __device__ void softmax_row_reference(float *v, int count, float *s_e, int *s_ne
         const float x = x_next;
         const int j_next = base + 64 + lane;
         x_next = j_next < count ? v[j_next] : -INFINITY;
-        float incl = x;
+        const float incl = fmaxf(wave_max_scan(x), carry);
+        // DPP reads inactive lanes as 0: shift with every lane active, then select
+        const float shifted = wave_shr1(incl);
+        const float before = lane == 0 ? carry : shifted;
+        const bool is_new = x > before;
+        // lanes past the end hold x = -inf: their term is expf(-inf) = 0 and
+        // adding +0 leaves the (positive) sum unchanged
+        const float e = is_new ? expf_libm(before - x) : expf_libm(x - before);
+        const uint64_t new_mask = __ballot(is_new);
+        // The running sum, in order: every lane runs the same chain, reading
+        // term j from lane j with v_readlane (no LDS, no barrier).
+        if (new_mask == 0) {
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const float y = __shfl_up(incl, o);
-            if (lane >= o) incl = fmaxf(incl, y);
-        }
-        incl = fmaxf(incl, carry);
-        float before = __shfl_up(incl, 1);
-        if (lane == 0) before = carry;
-        const int is_new = x > before;
-        s_e[lane] = is_new ? expf_libm(before - x) : expf_libm(x - before);
-        s_new[lane] = is_new;
-        const int any_new = __any(is_new);
-        __syncthreads();
-        if (lane == 0) {
+            for (int j = 0; j < 64; j++)
+                sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+        } else {
             const int n = count - base < 64 ? count - base : 64;
-            if (!any_new && n == 64) {
-                const float4 *e4 = reinterpret_cast<const float4 *>(s_e);
-                float4 e[16];
-#pragma unroll
-                for (int i = 0; i < 16; i++) e[i] = e4[i];
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    sum += e[i].x;
-                    sum += e[i].y;
-                    sum += e[i].z;
-                    sum += e[i].w;
-                }
-            } else {
-                for (int jj = 0; jj < n; jj++) {
-                    if (s_new[jj])
-                        sum = sum * s_e[jj] + 1.0f;
-                    else
-                        sum += s_e[jj];
-                }
+            for (int j = 0; j < n; j++) {
+                const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+                const float grown = sum * ej + 1.0f;  // a new maximum: rescale (two roundings)
+                const float added = sum + ej;
+                sum = (new_mask >> j) & 1 ? grown : added;
             }
         }
         carry = __shfl(incl, 63);
-        __syncthreads();
     }
-    sum = __shfl(sum, 0);
     const float max = carry;
-    for (int i = lane; i < count; i += 64) v[i] = expf_libm(v[i] - max) / sum;
+    // four values per lane per pass, loads issued together
+    for (int i0 = 0; i0 < count; i0 += 256) {
+        float r[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i0 + u * 64 + lane;
+            r[u] = v[min(i, count - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i0 + u * 64 + lane;
+            if (i < count) v[i] = expf_libm(r[u] - max) / sum;
+        }
+    }
 }
 
 // Attention probabilities of every (token, head) row, one wave each.
 __global__ __launch_bounds__(64) void k_attn_softmax_reference(float *__restrict__ scores,
                                                                int heads, int full, int start_pos,
                                                                size_t stride) {
-    __shared__ float s_e[64];
-    __shared__ int s_new[64];
     const int h = blockIdx.x, t = blockIdx.y;
     const int pos = start_pos + t, keys = pos + 1 - first_visible(pos, full);
-    softmax_row_reference(scores + ((size_t)t * heads + h) * stride, keys, s_e, s_new);
+    softmax_row_reference(scores + ((size_t)t * heads + h) * stride, keys);
 }
 
 // Independent rows of `count` values at `stride` (the per-op entry point).
 __global__ __launch_bounds__(64) void k_softmax_rows(float *values, int count, size_t stride) {
-    __shared__ float s_e[64];
-    __shared__ int s_new[64];
-    softmax_row_reference(values + (size_t)blockIdx.x * stride, count, s_e, s_new);
+    softmax_row_reference(values + (size_t)blockIdx.x * stride, count);
 }
 
 // out[t][h][d] = fma chain over keys in order (gemma4.c:296-307): one lane
 // per output channel and (token, head) chain.  A block takes a 64-channel
 // slice for WAVES waves; wave w runs the chains of token t0 + w / (8 / HPW)
-// for HPW heads.  V rows are staged in LDS 64 keys at a time, transposed to
-// [channel][key] so a lane reads four keys with one 16-byte load, and DEPTH
-// tiles are prefetched into registers ahead of the chains.  A key outside a
-// token's window is skipped by that token's chains (the order of the keys it
-// does see is unchanged).
+// for HPW heads.  Per 64-key tile, V rows are staged in LDS transposed to
+// [channel][key] (a lane reads four keys with one 16-byte load) and each
+// wave's probabilities [head][key] beside them (read as broadcasts); both are
+// prefetched DEPTH tiles ahead in registers with unconditional loads.  A key
+// outside a token's window is skipped by that token's chains (the order of
+// the keys it does see is unchanged).
 template <int HD, int WAVES, int HPW, int DEPTH>
 __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ out,
                                                             const float *__restrict__ probs,
@@ -312,8 +395,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
     constexpr int TOKENS = WAVES * HPW / 8;     // tokens per block
     constexpr int F4 = 64 * 64 / 4 / THREADS;   // float4 per thread per tile
     __shared__ __attribute__((aligned(16))) float s_v[64][64 + 4];
-    // wave is made provably uniform so the probability loads below are scalar
-    // loads: vector loads would retire in order behind the V prefetch ring.
+    __shared__ __attribute__((aligned(16))) float s_p[WAVES][HPW][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int d0 = blockIdx.x * 64, t0 = blockIdx.y * TOKENS;
@@ -325,10 +407,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
 
     const int my_t = t0 + wave / (8 / HPW), h0 = (wave % (8 / HPW)) * HPW;
     const bool active = my_t < t0 + tn;
-    const int my_pos = start_pos + my_t, my_first = first_visible(my_pos, full);
-    const float *prow = probs + ((size_t)my_t * 8 + h0) * stride;
+    const int ld_t = active ? my_t : t0 + tn - 1;  // inactive waves load a valid row
+    const int my_pos = start_pos + ld_t, my_first = first_visible(my_pos, full);
+    const int my_keys = my_pos - my_first + 1;
+    const float *prow = probs + ((size_t)ld_t * 8 + h0) * stride;
 
-    // tile loader: thread covers float4 (key kr, channels 4 cc .. 4 cc + 3)
+    // V tile loader: thread covers float4 (key kr, channels 4 cc .. 4 cc + 3)
     auto load_tile = [&](int tile, float4 (&r)[F4]) {
 #pragma unroll
         for (int i = 0; i < F4; i++) {
@@ -339,9 +423,19 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
             r[i] = *reinterpret_cast<const float4 *>(value_cache + (size_t)(p & mask) * HD + d0 + 4 * cc);
         }
     };
-    float4 ring[DEPTH][F4];
+    // probability loader: lane covers key kfirst + 64 tile + lane of its rows
+    auto load_p = [&](int tile, float (&r)[HPW]) {
+        const int j = min(max(kfirst + tile * 64 + lane - my_first, 0), my_keys - 1);
 #pragma unroll
-    for (int s = 0; s < DEPTH; s++) load_tile(min(s, tiles - 1), ring[s]);
+        for (int e = 0; e < HPW; e++) r[e] = prow[(size_t)e * stride + j];
+    };
+    float4 ring[DEPTH][F4];
+    float pring[DEPTH][HPW];
+#pragma unroll
+    for (int s = 0; s < DEPTH; s++) {
+        load_tile(min(s, tiles - 1), ring[s]);
+        load_p(min(s, tiles - 1), pring[s]);
+    }
 
     float o[HPW];
 #pragma unroll
@@ -350,7 +444,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
     // One tile: stage ring slot `s` in LDS, refill the slot DEPTH tiles ahead,
     // then run this wave's chains over the tile.  The loop below is unrolled by
     // DEPTH so every slot index is a compile-time constant (precise waits).
-    auto step = [&](int tile, float4 (&slot)[F4]) {
+    auto step = [&](int tile, float4 (&slot)[F4], float (&pslot)[HPW]) {
         __syncthreads();  // previous tile fully consumed
 #pragma unroll
         for (int i = 0; i < F4; i++) {
@@ -360,7 +454,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
             s_v[4 * cc + 2][kr] = slot[i].z;
             s_v[4 * cc + 3][kr] = slot[i].w;
         }
+#pragma unroll
+        for (int e = 0; e < HPW; e++) s_p[wave][e][lane] = pslot[e];
         load_tile(min(tile + DEPTH, tiles - 1), slot);  // unconditional refill
+        load_p(min(tile + DEPTH, tiles - 1), pslot);
         __syncthreads();
         if (!active || tile >= tiles) return;
         const int p0 = kfirst + tile * 64;
@@ -372,28 +469,26 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
 #pragma unroll 4
             for (int k4 = 0; k4 < 16; k4++) {
                 const float4 v4 = vr[k4];
-                const int pk = p0 + 4 * k4 - my_first;
 #pragma unroll
                 for (int e = 0; e < HPW; e++) {
-                    const float *pe = prow + (size_t)e * stride + pk;
-                    o[e] = fmaf(pe[0], v4.x, o[e]);
-                    o[e] = fmaf(pe[1], v4.y, o[e]);
-                    o[e] = fmaf(pe[2], v4.z, o[e]);
-                    o[e] = fmaf(pe[3], v4.w, o[e]);
+                    const float4 p4 = reinterpret_cast<const float4 *>(s_p[wave][e])[k4];
+                    o[e] = fmaf(p4.x, v4.x, o[e]);
+                    o[e] = fmaf(p4.y, v4.y, o[e]);
+                    o[e] = fmaf(p4.z, v4.z, o[e]);
+                    o[e] = fmaf(p4.w, v4.w, o[e]);
                 }
             }
         } else {
             for (int k = k_lo; k < k_hi; k++) {
                 const float vv = s_v[lane][k];
-                const int pk = p0 + k - my_first;
 #pragma unroll
-                for (int e = 0; e < HPW; e++) o[e] = fmaf(prow[(size_t)e * stride + pk], vv, o[e]);
+                for (int e = 0; e < HPW; e++) o[e] = fmaf(s_p[wave][e][k], vv, o[e]);
             }
         }
     };
     for (int tile = 0; tile < tiles; tile += DEPTH) {
 #pragma unroll
-        for (int s = 0; s < DEPTH; s++) step(tile + s, ring[s]);
+        for (int s = 0; s < DEPTH; s++) step(tile + s, ring[s], pring[s]);
     }
     if (active) {
 #pragma unroll
@@ -442,13 +537,13 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
         else
             hipLaunchKernelGGL((k_attn_values<512, 4, 2, 8>), grid, dim3(256), 0, s, out, scores,
                                value_cache, cache_len, full, start_pos, (int)n, stride);
-    } else {  // prefill: 16 tokens x 8 heads per block share each V tile
-        dim3 grid(slices, (nn + 15) / 16);
+    } else {  // prefill: 4 tokens x 8 heads per block share each V tile
+        dim3 grid(slices, (nn + 3) / 4);
         if (head_dim == 256)
-            hipLaunchKernelGGL((k_attn_values<256, 16, 8, 2>), grid, dim3(1024), 0, s, out, scores,
+            hipLaunchKernelGGL((k_attn_values<256, 4, 8, 2>), grid, dim3(256), 0, s, out, scores,
                                value_cache, cache_len, full, start_pos, (int)n, stride);
         else
-            hipLaunchKernelGGL((k_attn_values<512, 16, 8, 2>), grid, dim3(1024), 0, s, out, scores,
+            hipLaunchKernelGGL((k_attn_values<512, 4, 8, 2>), grid, dim3(256), 0, s, out, scores,
                                value_cache, cache_len, full, start_pos, (int)n, stride);
     }
     return G4_OK;
