@@ -43,6 +43,7 @@ struct Scratch {
     size_t dots_bytes = 0;
     float *attn = nullptr;    // attention partials (m, l, o per chunk) or scores
     size_t attn_bytes = 0;
+    unsigned generation = 0;  // bumped whenever a buffer moves (captured graphs hold the old one)
 };
 Scratch &scratch();
 int scratch_reserve(size_t dots_bytes, size_t attn_bytes);
@@ -70,9 +71,13 @@ void launch_rmsnorm_reference(hipStream_t s, float *out, const float *in, const 
                               int width, float eps, size_t rows);
 // gemma4.c:375-378
 void launch_add_and_scale(hipStream_t s, float *out, const float *add, size_t n, float scale);
+// Position-dependent launchers take start_pos and pos_dev: when pos_dev is
+// non-null the kernels read the position from that device int instead (so a
+// captured decode graph can be replayed at every position), and the grid no
+// longer depends on the position.
 // gemma4.c:381-398 (rows of v are heads*head_dim wide)
 void launch_rope(hipStream_t s, const float *cosines, const float *sines, int pairs, float *v,
-                 int heads, int head_dim, int start_pos, size_t n);
+                 int heads, int head_dim, int start_pos, const int *pos_dev, size_t n);
 // gemma4.c:310-331
 void launch_geglu(hipStream_t s, float *gate, const float *up, int rows, int width,
                   int up_stride, const float *table, int table_size, float lower, float upper);
@@ -81,22 +86,23 @@ void launch_geglu(hipStream_t s, float *gate, const float *up, int rows, int wid
 void launch_embedding(hipStream_t s, float *out, const int8_t *table, const uint16_t *scales,
                       int width, int table_rows, const int *tokens, size_t n, float multiplier);
 // gemma4.c:443-456: attention over a ring cache; dispatches on order().
+// pos_dev requires reference order and n == 1.
 int launch_attend(hipStream_t s, float *out, const float *q, const float *key_cache,
                   const float *value_cache, int cache_len, int head_dim, int heads, int full,
-                  int start_pos, size_t n);
+                  int start_pos, const int *pos_dev, size_t n);
 int launch_attend_parallel(hipStream_t s, float *out, const float *q, const float *key_cache,
                            const float *value_cache, int cache_len, int head_dim, int heads,
                            int full, int start_pos, size_t n);
 int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
                             const float *value_cache, int cache_len, int head_dim, int heads,
-                            int full, int start_pos, size_t n);
+                            int full, int start_pos, const int *pos_dev, size_t n);
 // Fused tail of the K/V projections (gemma4.c:437-440): rmsnorm+rope of the n
 // new keys and rmsnorm of the new values, written into the rings at
 // (start_pos + t) & (cache_len - 1).
 void launch_kv_finish(hipStream_t s, float *key_cache, float *value_cache, const float *k_new,
                       const float *v_new, const float *k_norm, const float *cosines,
                       const float *sines, int pairs, int head_dim, int cache_len, int start_pos,
-                      size_t n);
+                      const int *pos_dev, size_t n);
 // gemma4.c:518-519: 30 * tanh(x / 30) in place.
 void launch_softcap(hipStream_t s, float *x, size_t n);
 // First index of the maximum (gemma4.c:537-541) of each of `rows` rows.

@@ -31,6 +31,7 @@ int scratch_reserve(size_t dots_bytes, size_t attn_bytes) {
         s.dots_bytes = 0;
         G4_HIP(hipMalloc(&s.dots, dots_bytes));
         s.dots_bytes = dots_bytes;
+        s.generation++;
     }
     if (attn_bytes > s.attn_bytes) {
         if (s.attn) G4_HIP(hipFree(s.attn));
@@ -38,6 +39,7 @@ int scratch_reserve(size_t dots_bytes, size_t attn_bytes) {
         s.attn_bytes = 0;
         G4_HIP(hipMalloc(&s.attn, attn_bytes));
         s.attn_bytes = attn_bytes;
+        s.generation++;
     }
     return G4_OK;
 }
@@ -270,21 +272,16 @@ __global__ __launch_bounds__(256) void k_gemv_fold(float *__restrict__ out, size
 // covers exactly one group, so the group-ordered fp32 fold is the reference's
 // (bit-identical).
 //
-// Pipeline (one barrier per group): at the top of iteration g, LDS buffer
-// (g+1)&1 holds group g+1 and registers hold group g+2, loaded from global
-// memory during iteration g-1.  Each wave then
-//   1. reads its A/B fragments and scales of group g+1 from LDS,
-//   2. folds group g's int32 dots (computed by the MFMAs of iteration g-1),
-//   3. issues the MFMAs of group g+1 (they run on the matrix core while the
-//      next iteration's barrier, reads and fold proceed),
-//   4. stores group g+2 into buffer g&1 (read during iteration g-1) and
-//      issues the global loads of group g+3.
-// So the VALU fold of one group overlaps the MFMAs of the next.  The B tiles
-// are reordered on the way into LDS from the packed [chunk][row][4] layout to
-// row-major rows of 64 bytes, so each lane reads its B operand with one
-// 16-byte load; rows are padded to 80 bytes.
+// Pipeline: KG groups per stage, one barrier per stage.  LDS holds two
+// stages (double-buffered); while the waves multiply and fold the stage in
+// one buffer, the next stage (loaded from global memory during the previous
+// iteration) is stored into the other and the one after it is loaded into
+// registers.  Within a stage the fold of one group can overlap the MFMAs of
+// the next.  The B tiles are reordered on the way into LDS from the packed
+// [chunk][row][4] layout to row-major rows of 64 bytes, so each lane reads its
+// B operand with one 16-byte load; rows are padded to 80 bytes.
 
-template <int BN>
+template <int BN, int KG>
 __global__ __launch_bounds__(256) void k_gemm(float *__restrict__ out, size_t out_stride,
                                               const int8_t *__restrict__ xq,
                                               const float *__restrict__ xs,
@@ -293,11 +290,12 @@ __global__ __launch_bounds__(256) void k_gemm(float *__restrict__ out, size_t ou
                                               int n_out, int k) {
     constexpr int BM = 64, NT = BN / 16, WN = BN / 2, NI = WN / 16, RS = 80;
     constexpr int BV = NT / 4;  // 16-byte B loads per thread per group
-    __shared__ __attribute__((aligned(16))) int8_t s_a[2][BM * RS];
-    __shared__ __attribute__((aligned(16))) int8_t s_b[2][BN * RS];
-    __shared__ __attribute__((aligned(16))) float s_xs[2][BM];
-    __shared__ __attribute__((aligned(16))) float s_ws[2][BN];
-    const int groups = k >> 6, m0 = blockIdx.y * BM, nb0 = blockIdx.x * NT, n_blocks = n_out >> 4;
+    __shared__ __attribute__((aligned(16))) int8_t s_a[2][KG][BM * RS];
+    __shared__ __attribute__((aligned(16))) int8_t s_b[2][KG][BN * RS];
+    __shared__ __attribute__((aligned(16))) float s_xs[2][KG][BM];
+    __shared__ __attribute__((aligned(16))) float s_ws[2][KG][BN];
+    const int groups = k >> 6, stages = (groups + KG - 1) / KG;
+    const int m0 = blockIdx.y * BM, nb0 = blockIdx.x * NT, n_blocks = n_out >> 4;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1, q = lane >> 4, l16 = lane & 15;
     const v4i zero = {0, 0, 0, 0};
@@ -312,70 +310,40 @@ __global__ __launch_bounds__(256) void k_gemm(float *__restrict__ out, size_t ou
     const uint16_t *w_src = ws + (size_t)min(nb0 + (w_n >> 4), n_blocks - 1) * groups * 16 + (w_n & 15);
 
     struct Stage {
-        v4i a, b[BV];
-        float x;
-        uint16_t w;
+        v4i a[KG], b[KG][BV];
+        float x[KG];
+        uint16_t w[KG];
     };
-    auto gload = [&](int g, Stage &st) {
-        g = min(g, groups - 1);
-        st.a = *reinterpret_cast<const v4i *>(a_src + g * 64);
+    auto gload = [&](int st, Stage &r) {
 #pragma unroll
-        for (int j = 0; j < BV; j++) {
-            const int idx = j * 256 + tid, t = min(nb0 + (idx >> 6), n_blocks - 1);
-            st.b[j] = *reinterpret_cast<const v4i *>(w + ((size_t)t * groups + g) * 1024 + (idx & 63) * 16);
-        }
-        st.x = x_src[g];  // every thread loads a scale; threads < BM + BN keep theirs
-        st.w = w_src[g * 16];
-    };
-    auto sstore = [&](int buf, const Stage &st) {
-        *reinterpret_cast<v4i *>(s_a[buf] + a_row * RS + a_part * 16) = st.a;
+        for (int kg = 0; kg < KG; kg++) {
+            const int g = min(st * KG + kg, groups - 1);
+            r.a[kg] = *reinterpret_cast<const v4i *>(a_src + g * 64);
 #pragma unroll
-        for (int j = 0; j < BV; j++) {
-            const int idx = j * 256 + tid, t = idx >> 6, i = idx & 63, c = i >> 2, rq = i & 3;
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++)
-                *reinterpret_cast<int *>(s_b[buf] + (t * 16 + rq * 4 + jj) * RS + c * 4) = st.b[j][jj];
-        }
-        if (tid < BM)
-            s_xs[buf][tid] = st.x;
-        else if (tid < BM + BN)
-            s_ws[buf][tid - BM] = half_bits_to_float(st.w);
-    };
-
-    struct Frag {
-        v4i a[2], b[NI];
-        float4 x[2];
-        float w[NI];
-    };
-    auto fread = [&](int buf, Frag &f) {
-#pragma unroll
-        for (int mi = 0; mi < 2; mi++) {
-            const int r = wm * 32 + mi * 16;
-            f.a[mi] = *reinterpret_cast<const v4i *>(s_a[buf] + (r + l16) * RS + q * 16);
-            f.x[mi] = *reinterpret_cast<const float4 *>(&s_xs[buf][r + 4 * q]);
-        }
-#pragma unroll
-        for (int ni = 0; ni < NI; ni++) {
-            const int c = wn * WN + ni * 16 + l16;
-            f.b[ni] = *reinterpret_cast<const v4i *>(s_b[buf] + c * RS + q * 16);
-            f.w[ni] = s_ws[buf][c];
+            for (int j = 0; j < BV; j++) {
+                const int idx = j * 256 + tid, t = min(nb0 + (idx >> 6), n_blocks - 1);
+                r.b[kg][j] = *reinterpret_cast<const v4i *>(w + ((size_t)t * groups + g) * 1024 + (idx & 63) * 16);
+            }
+            r.x[kg] = x_src[g];  // every thread loads a scale; threads < BM + BN keep theirs
+            r.w[kg] = w_src[g * 16];
         }
     };
-    struct Dots {
-        v4i d[2][NI];
-        float4 x[2];
-        float w[NI];
-    };
-    auto mfma = [&](const Frag &f, Dots &o) {
+    auto sstore = [&](int buf, const Stage &r) {
 #pragma unroll
-        for (int ni = 0; ni < NI; ni++)
+        for (int kg = 0; kg < KG; kg++) {
+            *reinterpret_cast<v4i *>(s_a[buf][kg] + a_row * RS + a_part * 16) = r.a[kg];
 #pragma unroll
-            for (int mi = 0; mi < 2; mi++)
-                o.d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[mi], f.b[ni], zero, 0, 0, 0);
+            for (int j = 0; j < BV; j++) {
+                const int idx = j * 256 + tid, t = idx >> 6, i = idx & 63, c = i >> 2, rq = i & 3;
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++) o.x[mi] = f.x[mi];
-#pragma unroll
-        for (int ni = 0; ni < NI; ni++) o.w[ni] = f.w[ni];
+                for (int jj = 0; jj < 4; jj++)
+                    *reinterpret_cast<int *>(s_b[buf][kg] + (t * 16 + rq * 4 + jj) * RS + c * 4) = r.b[kg][j][jj];
+            }
+            if (tid < BM)
+                s_xs[buf][kg][tid] = r.x[kg];
+            else if (tid < BM + BN)
+                s_ws[buf][kg][tid - BM] = half_bits_to_float(r.w[kg]);
+        }
     };
 
     float acc[2][NI][4];
@@ -385,44 +353,47 @@ __global__ __launch_bounds__(256) void k_gemm(float *__restrict__ out, size_t ou
         for (int j = 0; j < NI; j++)
 #pragma unroll
             for (int v = 0; v < 4; v++) acc[i][j][v] = 0.0f;
-    auto fold = [&](const Dots &o) {
+
+    auto compute = [&](int buf, int kg) {
+        v4i a[2];
+        float4 xv[2];
 #pragma unroll
-        for (int ni = 0; ni < NI; ni++)
+        for (int mi = 0; mi < 2; mi++) {
+            const int r = wm * 32 + mi * 16;
+            a[mi] = *reinterpret_cast<const v4i *>(s_a[buf][kg] + (r + l16) * RS + q * 16);
+            xv[mi] = *reinterpret_cast<const float4 *>(&s_xs[buf][kg][r + 4 * q]);
+        }
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++) {
+            const int c = wn * WN + ni * 16 + l16;
+            const v4i b = *reinterpret_cast<const v4i *>(s_b[buf][kg] + c * RS + q * 16);
+            const float wsf = s_ws[buf][kg][c];
 #pragma unroll
             for (int mi = 0; mi < 2; mi++) {
-                acc[mi][ni][0] = fmaf((float)o.d[mi][ni][0], o.w[ni] * o.x[mi].x, acc[mi][ni][0]);
-                acc[mi][ni][1] = fmaf((float)o.d[mi][ni][1], o.w[ni] * o.x[mi].y, acc[mi][ni][1]);
-                acc[mi][ni][2] = fmaf((float)o.d[mi][ni][2], o.w[ni] * o.x[mi].z, acc[mi][ni][2]);
-                acc[mi][ni][3] = fmaf((float)o.d[mi][ni][3], o.w[ni] * o.x[mi].w, acc[mi][ni][3]);
+                const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b, zero, 0, 0, 0);
+                acc[mi][ni][0] = fmaf((float)d[0], wsf * xv[mi].x, acc[mi][ni][0]);
+                acc[mi][ni][1] = fmaf((float)d[1], wsf * xv[mi].y, acc[mi][ni][1]);
+                acc[mi][ni][2] = fmaf((float)d[2], wsf * xv[mi].z, acc[mi][ni][2]);
+                acc[mi][ni][3] = fmaf((float)d[3], wsf * xv[mi].w, acc[mi][ni][3]);
             }
-    };
-
-    Stage st;
-    Frag fr;
-    Dots dots[2];
-    gload(0, st);
-    sstore(0, st);
-    gload(1, st);
-    sstore(1, st);
-    gload(2, st);
-    __syncthreads();
-    fread(0, fr);
-    mfma(fr, dots[0]);
-    // One iteration per group; unrolled by two so the dots slot is static.
-    auto step = [&](int g, Dots &cur, Dots &next) {
-        __syncthreads();
-        const bool more = g + 1 < groups;  // uniform across the block
-        if (more) fread((g + 1) & 1, fr);
-        fold(cur);
-        if (more) {
-            mfma(fr, next);
-            sstore(g & 1, st);
-            gload(g + 3, st);
         }
     };
-    for (int g = 0; g < groups; g += 2) {
-        step(g, dots[0], dots[1]);
-        if (g + 1 < groups) step(g + 1, dots[1], dots[0]);
+
+    Stage r;
+    gload(0, r);
+    sstore(0, r);
+    gload(1, r);
+    __syncthreads();
+    for (int st = 0; st < stages; st++) {
+        const int buf = st & 1;
+#pragma unroll
+        for (int kg = 0; kg < KG; kg++)
+            if (st * KG + kg < groups) compute(buf, kg);  // uniform across the block
+        if (st + 1 < stages) {
+            sstore(buf ^ 1, r);
+            gload(st + 2, r);
+        }
+        __syncthreads();
     }
 #pragma unroll
     for (int mi = 0; mi < 2; mi++)
@@ -445,7 +416,7 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
     const int blocks = n_out / 16, groups = k / 64;
     if (rows > 8) {
         const unsigned mb = (unsigned)((rows + 63) / 64);
-        hipLaunchKernelGGL((k_gemm<64>), dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
+        hipLaunchKernelGGL((k_gemm<64, 1>), dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
                            out, out_stride, xq, xs, w, ws, rows, n_out, k);
         return G4_OK;
     }
@@ -532,9 +503,11 @@ void launch_add_and_scale(hipStream_t s, float *out, const float *add, size_t n,
 // gemma4.c:381-398, one thread per (token, head, pair).
 __global__ __launch_bounds__(256) void k_rope(const float *__restrict__ cosines,
                                               const float *__restrict__ sines, int pairs, float *v,
-                                              int heads, int head_dim, int start_pos, size_t total) {
+                                              int heads, int head_dim, int start_pos,
+                                              const int *__restrict__ pos_dev, size_t total) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= total) return;
+    if (pos_dev) start_pos = *pos_dev;
     const int j = (int)(i % pairs);
     const size_t th = i / pairs;  // token * heads + head
     const size_t t = th / heads;
@@ -547,11 +520,11 @@ __global__ __launch_bounds__(256) void k_rope(const float *__restrict__ cosines,
 }
 
 void launch_rope(hipStream_t s, const float *cosines, const float *sines, int pairs, float *v,
-                 int heads, int head_dim, int start_pos, size_t n) {
+                 int heads, int head_dim, int start_pos, const int *pos_dev, size_t n) {
     const size_t total = n * (size_t)heads * pairs;
     if (!total) return;
     hipLaunchKernelGGL(k_rope, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, cosines,
-                       sines, pairs, v, heads, head_dim, start_pos, total);
+                       sines, pairs, v, heads, head_dim, start_pos, pos_dev, total);
 }
 
 // gemma4.c:310-331.
@@ -626,8 +599,10 @@ __global__ __launch_bounds__(256) void k_kv_finish(float *key_cache, float *valu
                                                    const float *__restrict__ cosines,
                                                    const float *__restrict__ sines, int pairs,
                                                    int head_dim, int cache_len, int start_pos,
+                                                   const int *__restrict__ pos_dev,
                                                    int reference_order) {
     __shared__ float red[4];
+    if (pos_dev) start_pos = *pos_dev;
     __shared__ float row[512];
     const int t = blockIdx.x, is_value = blockIdx.y;
     const float *x = (is_value ? v_new : k_new) + (size_t)t * head_dim;
@@ -676,11 +651,11 @@ __global__ __launch_bounds__(256) void k_kv_finish(float *key_cache, float *valu
 void launch_kv_finish(hipStream_t s, float *key_cache, float *value_cache, const float *k_new,
                       const float *v_new, const float *k_norm, const float *cosines,
                       const float *sines, int pairs, int head_dim, int cache_len, int start_pos,
-                      size_t n) {
+                      const int *pos_dev, size_t n) {
     if (!n) return;
     hipLaunchKernelGGL(k_kv_finish, dim3((unsigned)n, 2), dim3(256), 0, s, key_cache, value_cache,
                        k_new, v_new, k_norm, cosines, sines, pairs, head_dim, cache_len, start_pos,
-                       order() == G4_ORDER_REFERENCE ? 1 : 0);
+                       pos_dev, order() == G4_ORDER_REFERENCE ? 1 : 0);
 }
 
 __global__ __launch_bounds__(256) void k_softcap(float *x, size_t n) {
@@ -958,7 +933,7 @@ extern "C" int g4_apply_rope(void *stream, const float *cosines, const float *si
     G4_CHECK(heads > 0 && head_dim > 0 && head_dim % 2 == 0 && pairs >= 0 && pairs <= head_dim / 2,
              "g4_apply_rope: bad geometry");
     G4_CHECK(start_pos >= 0, "g4_apply_rope: negative position");
-    launch_rope((hipStream_t)stream, cosines, sines, pairs, v, heads, head_dim, start_pos, n);
+    launch_rope((hipStream_t)stream, cosines, sines, pairs, v, heads, head_dim, start_pos, nullptr, n);
     G4_HIP(hipGetLastError());
     return G4_OK;
 }
@@ -1001,7 +976,7 @@ extern "C" int g4_attend(void *stream, float *out, const float *q, const float *
                                      : (long)(start_pos < G4_WINDOW - 1 ? start_pos : G4_WINDOW - 1) + (long)n;
     G4_CHECK(span <= cache_len, "g4_attend: %ld visible keys exceed the %d-row ring", span, cache_len);
     int rc = launch_attend((hipStream_t)stream, out, q, key_cache, value_cache, cache_len, head_dim,
-                           heads, full_attention, start_pos, n);
+                           heads, full_attention, start_pos, nullptr, n);
     if (rc) return rc;
     G4_HIP(hipGetLastError());
     return G4_OK;

@@ -59,7 +59,14 @@ struct Context {
     int cache_len[15] = {}, cache_dim[15] = {};
     int *tokens_dev = nullptr, *argmax_dev = nullptr;
     int *tokens_pinned = nullptr;
+    int *pos_dev = nullptr, *pos_pinned = nullptr;
     int last_n = 0;
+    // One-token steps replay a captured graph of the whole forward pass; the
+    // position is read from pos_dev.  Recaptured when the scratch buffers move
+    // or the summation order changes.
+    hipGraphExec_t decode_graph = nullptr;
+    unsigned graph_generation = 0;
+    int graph_order = -1;
 };
 
 static Context g_ctx;
@@ -98,7 +105,10 @@ static void free_all(Context &c) {
     for (int i = 0; i < 15; i++) release(c.cache[i]);
     release(c.tokens_dev);
     release(c.argmax_dev);
+    release(c.pos_dev);
     if (c.tokens_pinned) (void)hipHostFree(c.tokens_pinned);
+    if (c.pos_pinned) (void)hipHostFree(c.pos_pinned);
+    if (c.decode_graph) (void)hipGraphExecDestroy(c.decode_graph);
     if (c.stream) (void)hipStreamDestroy(c.stream);
     c = Context();
 }
@@ -282,10 +292,14 @@ static int init(const g4_tensor *records, int device) {
     G4_HIP(hipMalloc(&c.tokens_dev, G4_BATCH * sizeof(int)));
     G4_HIP(hipMalloc(&c.argmax_dev, G4_BATCH * sizeof(int)));
     G4_HIP(hipHostMalloc((void **)&c.tokens_pinned, G4_BATCH * sizeof(int), hipHostMallocDefault));
-    // Split-K scratch for the widest few-row product (1536 x 12288) and the
-    // decode attention partials for a full-length context.
+    G4_HIP(hipMalloc(&c.pos_dev, sizeof(int)));
+    G4_HIP(hipHostMalloc((void **)&c.pos_pinned, sizeof(int), hipHostMallocDefault));
+    // Split-K scratch for the widest few-row product (1536 x 12288), and the
+    // one-token attention scratch at full context (8 score rows plus the
+    // long-row softmax work, under 2 x 8 rows), so that a captured decode step
+    // never needs a larger buffer.
     G4_TRY(scratch_reserve((size_t)G4_VOCAB * (G4_HIDDEN / 64) * sizeof(int32_t),
-                           (size_t)G4_MAX_CONTEXT * 8 * sizeof(float) * 2));
+                           (size_t)G4_MAX_CONTEXT * 8 * sizeof(float) * 3));
     G4_HIP(hipDeviceSynchronize());
     c.ready = true;
     return G4_OK;
@@ -295,12 +309,12 @@ static int matmul(Context &c, float *out, size_t stride, const Weight &w, int ro
     return launch_matmul(c.stream, out, stride, c.q8, c.qs, w.data, w.scales, w.n, w.k, rows);
 }
 
-// The sequence of gemma4.c:463-509 (attention: 411-461).
-static int forward(Context &c, const int *tokens, int n, int start_pos) {
+// The sequence of gemma4.c:463-509 (attention: 411-461) for the n tokens in
+// c.tokens_dev, as launches on c.stream.  With pos_dev non-null (n == 1) the
+// position-dependent kernels read the position from the device, so the
+// launches can be captured once and replayed at every position.
+static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev) {
     hipStream_t s = c.stream;
-    memcpy(c.tokens_pinned, tokens, (size_t)n * sizeof(int));
-    G4_HIP(hipMemcpyAsync(c.tokens_dev, c.tokens_pinned, (size_t)n * sizeof(int),
-                          hipMemcpyHostToDevice, s));
     const int ple_width = G4_LAYERS * G4_PLE;
 
     launch_embedding(s, c.residual, c.embed.data, c.embed.scales, G4_HIDDEN, c.embed.n, c.tokens_dev,
@@ -321,7 +335,7 @@ static int forward(Context &c, const int *tokens, int n, int start_pos) {
         launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_HIDDEN / 64);
         G4_TRY(matmul(c, c.aux, qw, L.q, n));
         launch_rmsnorm(s, c.aux, c.aux, L.q_norm, hd, 1e-6f, (size_t)n * heads);
-        launch_rope(s, L.rope_cos, L.rope_sin, L.pairs, c.aux, heads, hd, start_pos, n);
+        launch_rope(s, L.rope_cos, L.rope_sin, L.pairs, c.aux, heads, hd, start_pos, pos_dev, n);
         float *keys = c.cache[L.owner];
         const int cache_len = c.cache_len[L.owner];
         float *values = keys + (size_t)cache_len * hd;
@@ -329,10 +343,10 @@ static int forward(Context &c, const int *tokens, int n, int start_pos) {
             G4_TRY(matmul(c, c.k_new, hd, L.k, n));
             G4_TRY(matmul(c, c.v_new, hd, L.v, n));
             launch_kv_finish(s, keys, values, c.k_new, c.v_new, L.k_norm, L.rope_cos, L.rope_sin,
-                             L.pairs, hd, cache_len, start_pos, n);
+                             L.pairs, hd, cache_len, start_pos, pos_dev, n);
         }
         G4_TRY(launch_attend(s, c.hidden, c.aux, keys, values, cache_len, hd, heads, L.full,
-                             start_pos, n));
+                             start_pos, pos_dev, n));
         launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * qw / 64);
         G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.o, n));
         launch_rmsnorm(s, c.hidden, c.hidden, L.post_attn_ln, G4_HIDDEN, 1e-6f, n);
@@ -361,6 +375,46 @@ static int forward(Context &c, const int *tokens, int n, int start_pos) {
         launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, L.layer_scalar);
     }
     G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+// Capture the one-token forward pass into c.decode_graph.
+static int capture_decode(Context &c) {
+    if (c.decode_graph) {
+        G4_HIP(hipGraphExecDestroy(c.decode_graph));
+        c.decode_graph = nullptr;
+    }
+    hipGraph_t graph = nullptr;
+    G4_HIP(hipStreamBeginCapture(c.stream, hipStreamCaptureModeRelaxed));
+    const int rc = enqueue_forward(c, 1, 0, c.pos_dev);
+    hipError_t end = hipStreamEndCapture(c.stream, &graph);
+    if (rc) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc;
+    }
+    G4_HIP(end);
+    hipError_t inst = hipGraphInstantiate(&c.decode_graph, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    G4_HIP(inst);
+    c.graph_generation = scratch().generation;
+    c.graph_order = order();
+    return G4_OK;
+}
+
+static int forward(Context &c, const int *tokens, int n, int start_pos) {
+    hipStream_t s = c.stream;
+    memcpy(c.tokens_pinned, tokens, (size_t)n * sizeof(int));
+    G4_HIP(hipMemcpyAsync(c.tokens_dev, c.tokens_pinned, (size_t)n * sizeof(int),
+                          hipMemcpyHostToDevice, s));
+    if (n == 1 && order() == G4_ORDER_REFERENCE) {
+        *c.pos_pinned = start_pos;
+        G4_HIP(hipMemcpyAsync(c.pos_dev, c.pos_pinned, sizeof(int), hipMemcpyHostToDevice, s));
+        if (!c.decode_graph || c.graph_generation != scratch().generation || c.graph_order != order())
+            G4_TRY(capture_decode(c));
+        G4_HIP(hipGraphLaunch(c.decode_graph, s));
+    } else {
+        G4_TRY(enqueue_forward(c, n, start_pos, nullptr));
+    }
     G4_HIP(hipStreamSynchronize(s));
     c.last_n = n;
     return G4_OK;

@@ -227,14 +227,16 @@ template <int HD, int TQ>
 __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q,
                                                      const float *__restrict__ key_cache,
                                                      int cache_len, int full, int start_pos, int n,
-                                                     size_t stride, float *__restrict__ scores) {
+                                                     const int *__restrict__ pos_dev, size_t stride,
+                                                     float *__restrict__ scores) {
     constexpr int S = HD / 16, SP = S + 4;  // +4 floats: the 16 lanes' 16-byte reads hit distinct banks
     __shared__ __attribute__((aligned(16))) float s_q[TQ * 8][16][SP];
     const int t0 = blockIdx.y * TQ;
     const int tn = n - t0 < TQ ? n - t0 : TQ;
+    if (pos_dev) start_pos = *pos_dev;
     const int pos_last = start_pos + t0 + tn - 1;
-    const int kbase = first_visible(start_pos + t0, full) + blockIdx.x * 64;
-    if (kbase > pos_last) return;
+    const int kfirst = first_visible(start_pos + t0, full);
+    if (kfirst + (int)blockIdx.x * 64 > pos_last) return;
     const int mask = cache_len - 1, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *qt = q + (size_t)t0 * 8 * HD;
     for (int i = tid; i < tn * 8 * HD; i += 256) {
@@ -243,6 +245,10 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     }
     __syncthreads();
     const int m = lane & 15, kg = lane >> 4;
+    // key blocks blockIdx.x, blockIdx.x + gridDim.x, ... (one per block when
+    // the grid spans the keys; a fixed grid strides when the position is read
+    // from the device)
+    for (int kbase = kfirst + blockIdx.x * 64; kbase <= pos_last; kbase += gridDim.x * 64)
     for (int kk = wave * 4 + kg; kk < 64; kk += 16) {
         const int p = kbase + kk;
         if (p > pos_last) break;  // uniform within the 16-lane group
@@ -362,10 +368,166 @@ __device__ void softmax_row_reference(float *v, int count) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Long rows (deep-context decode): the same arithmetic in five passes, so
+// that only the running sum is sequential.
+//   1. the maximum of every 64-value block;
+//   2. per row, the exclusive prefix maximum over blocks;
+//   3. every term in parallel: before_i = max(v_0 .. v_{i-1}), a new maximum
+//      when v_i > before_i, e_i = expf(before_i - v_i) then, else
+//      expf(v_i - before_i) (v_0 is the starting maximum, not a term);
+//   4. one wave per row runs the reference's running sum over the e_i in
+//      order (sum = sum * e + 1 at a new maximum, else sum += e);
+//   5. v_i = expf(v_i - max) / sum in parallel.
+// Each value of the result equals the one-wave kernel's bit for bit.
+
+// Which values a row holds: a fixed count, or an attention row (t, head)
+// whose visible keys follow from the position.
+struct SoftmaxRows {
+    int heads, full, start_pos, fixed_count;
+    const int *pos_dev;
+    __device__ __forceinline__ int count(int row) const {
+        if (fixed_count > 0) return fixed_count;
+        const int pos = (pos_dev ? *pos_dev : start_pos) + row / heads;
+        return pos + 1 - first_visible(pos, full);
+    }
+};
+
+__global__ __launch_bounds__(256) void k_lsm_blockmax(const float *__restrict__ v, size_t stride,
+                                                      SoftmaxRows spec, float *__restrict__ bmax,
+                                                      int nbs) {
+    const int row = blockIdx.y, lane = threadIdx.x & 63;
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6), count = spec.count(row);
+    if (b * 64 >= count) return;
+    const int i = b * 64 + lane;
+    const float x = i < count ? v[(size_t)row * stride + i] : -INFINITY;
+    const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_max_scan(x)), 63));
+    if (lane == 0) bmax[(size_t)row * nbs + b] = m;
+}
+
+__global__ __launch_bounds__(64) void k_lsm_prefix(SoftmaxRows spec, const float *__restrict__ bmax,
+                                                   float *__restrict__ pmax, float *__restrict__ info,
+                                                   int nbs) {
+    const int row = blockIdx.x, lane = threadIdx.x;
+    const int nb = (spec.count(row) + 63) / 64;
+    float carry = -INFINITY;
+    for (int i0 = 0; i0 < nb; i0 += 64) {
+        const int b = i0 + lane;
+        const float x = b < nb ? bmax[(size_t)row * nbs + b] : -INFINITY;
+        const float incl = fmaxf(wave_max_scan(x), carry);
+        const float shifted = wave_shr1(incl);
+        if (b < nb) pmax[(size_t)row * nbs + b] = lane == 0 ? carry : shifted;
+        carry = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), 63));
+    }
+    if (lane == 0) info[2 * row] = carry;  // the row's maximum
+}
+
+__global__ __launch_bounds__(256) void k_lsm_terms(const float *__restrict__ v, size_t stride,
+                                                   SoftmaxRows spec, const float *__restrict__ pmax,
+                                                   float *__restrict__ terms,
+                                                   uint64_t *__restrict__ new_masks, int nbs) {
+    const size_t tstride = (size_t)nbs * 64;  // terms rows: whole blocks
+    const int row = blockIdx.y, lane = threadIdx.x & 63;
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6), count = spec.count(row);
+    if (b * 64 >= count) return;
+    const int i = b * 64 + lane;
+    const float x = i < count ? v[(size_t)row * stride + i] : -INFINITY;
+    const float carry = pmax[(size_t)row * nbs + b];
+    const float incl = fmaxf(wave_max_scan(x), carry);
+    const float shifted = wave_shr1(incl);
+    const float before = lane == 0 ? carry : shifted;
+    bool is_new = x > before;
+    float e = is_new ? expf_libm(before - x) : expf_libm(x - before);
+    if (i == 0) {  // v_0 starts the running maximum (gemma4.c:401)
+        is_new = false;
+        e = 0.0f;
+    }
+    // past the end: x = -inf, so e = 0, which leaves the positive sum unchanged
+    terms[(size_t)row * tstride + i] = e;
+    const uint64_t mask = __ballot(is_new);
+    if (lane == 0) new_masks[(size_t)row * nbs + b] = mask;
+}
+
+__global__ __launch_bounds__(64) void k_lsm_chain(SoftmaxRows spec, const float *__restrict__ terms,
+                                                  const uint64_t *__restrict__ new_masks,
+                                                  float *__restrict__ info, int nbs) {
+    constexpr int R = 8;  // blocks of terms in flight ahead of the chain
+    const int row = blockIdx.x, lane = threadIdx.x;
+    const int nb = (spec.count(row) + 63) / 64;
+    const float *t = terms + (size_t)row * nbs * 64 + lane;
+    const uint64_t *nm = new_masks + (size_t)row * nbs;
+    float ring[R];
+#pragma unroll
+    for (int s = 0; s < R; s++) ring[s] = t[(size_t)min(s, nb - 1) * 64];
+    uint64_t masks = 0;  // lane j: new-maximum mask of block (b & ~63) + j
+    float sum = 1.0f;
+    for (int b0 = 0; b0 < nb; b0 += R) {
+        if ((b0 & 63) == 0) masks = nm[min(b0 + lane, nb - 1)];
+#pragma unroll
+        for (int s = 0; s < R; s++) {
+            const int b = b0 + s;
+            const float e = ring[s];
+            ring[s] = t[(size_t)min(b + R, nb - 1) * 64];  // unconditional refill
+            if (b < nb) {
+                const int j = b & 63;
+                const uint64_t mask =
+                    ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(masks >> 32), j) << 32) |
+                    (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)masks, j);
+                if (mask == 0) {
+#pragma unroll
+                    for (int k = 0; k < 64; k++)
+                        sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k));
+                } else {
+                    for (int k = 0; k < 64; k++) {
+                        const float ek = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k));
+                        const float grown = sum * ek + 1.0f;
+                        const float added = sum + ek;
+                        sum = (mask >> k) & 1 ? grown : added;
+                    }
+                }
+            }
+        }
+    }
+    if (lane == 0) info[2 * row + 1] = sum;
+}
+
+__global__ __launch_bounds__(256) void k_lsm_normalize(float *__restrict__ v, size_t stride,
+                                                       SoftmaxRows spec,
+                                                       const float *__restrict__ info) {
+    const int row = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= spec.count(row)) return;
+    float *x = v + (size_t)row * stride + i;
+    *x = expf_libm(*x - info[2 * row]) / info[2 * row + 1];
+}
+
+// Scratch floats the long-row path needs for rows of at most max_count values.
+static size_t long_softmax_floats(size_t rows, size_t max_count) {
+    const size_t nbs = (max_count + 63) / 64;
+    return rows * (nbs * 64 + 2 * nbs + 2 * nbs + 2);  // terms, bmax, pmax, masks (2 floats each), info
+}
+
+// Rows of v at `stride` floats, each at most max_count values long.
+static void launch_softmax_long(hipStream_t s, float *v, size_t stride, int max_count,
+                                SoftmaxRows spec, unsigned rows, float *work) {
+    const int nbs = (max_count + 63) / 64;
+    float *terms = work, *bmax = terms + (size_t)rows * nbs * 64, *pmax = bmax + (size_t)rows * nbs;
+    uint64_t *masks = reinterpret_cast<uint64_t *>(pmax + (size_t)rows * nbs);
+    float *info = reinterpret_cast<float *>(masks + (size_t)rows * nbs);
+    const dim3 blocks((unsigned)((nbs + 3) / 4), rows);
+    hipLaunchKernelGGL(k_lsm_blockmax, blocks, dim3(256), 0, s, v, stride, spec, bmax, nbs);
+    hipLaunchKernelGGL(k_lsm_prefix, dim3(rows), dim3(64), 0, s, spec, bmax, pmax, info, nbs);
+    hipLaunchKernelGGL(k_lsm_terms, blocks, dim3(256), 0, s, v, stride, spec, pmax, terms, masks, nbs);
+    hipLaunchKernelGGL(k_lsm_chain, dim3(rows), dim3(64), 0, s, spec, terms, masks, info, nbs);
+    hipLaunchKernelGGL(k_lsm_normalize, dim3((unsigned)((nbs * 64 + 255) / 256), rows), dim3(256), 0,
+                       s, v, stride, spec, info);
+}
+
 // Attention probabilities of every (token, head) row, one wave each.
 __global__ __launch_bounds__(64) void k_attn_softmax_reference(float *__restrict__ scores,
                                                                int heads, int full, int start_pos,
+                                                               const int *__restrict__ pos_dev,
                                                                size_t stride) {
+    if (pos_dev) start_pos = *pos_dev;
     const int h = blockIdx.x, t = blockIdx.y;
     const int pos = start_pos + t, keys = pos + 1 - first_visible(pos, full);
     softmax_row_reference(scores + ((size_t)t * heads + h) * stride, keys);
@@ -390,8 +552,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
                                                             const float *__restrict__ probs,
                                                             const float *__restrict__ value_cache,
                                                             int cache_len, int full, int start_pos,
-                                                            int n, size_t stride) {
+                                                            int n, const int *__restrict__ pos_dev,
+                                                            size_t stride) {
     constexpr int THREADS = WAVES * 64;
+    if (pos_dev) start_pos = *pos_dev;
     constexpr int TOKENS = WAVES * HPW / 8;     // tokens per block
     constexpr int F4 = 64 * 64 / 4 / THREADS;   // float4 per thread per tile
     __shared__ __attribute__((aligned(16))) float s_v[64][64 + 4];
@@ -496,65 +660,189 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
     }
 }
 
+// P.V for one token per block (decode): wave h runs the 64 chains of head
+// h over a 64-channel slice, one chain per lane, keys in order.  The 8 heads
+// share each 64-key tile of V, staged in LDS row-major ([key][channel]: a
+// lane reads its channel of key k with a 4-byte load) beside the 8 heads'
+// probabilities (read as broadcasts).  Tiles are prefetched DEPTH ahead in
+// registers with unconditional loads and stored into a double-buffered LDS
+// slot, one barrier per tile; each lane's chain is then 64 dependent fmas per
+// tile with nothing else on its critical path.
+template <int HD, int DEPTH>
+__global__ __launch_bounds__(512) void k_attn_values_decode(float *__restrict__ out,
+                                                            const float *__restrict__ probs,
+                                                            const float *__restrict__ value_cache,
+                                                            int cache_len, int full, int start_pos,
+                                                            const int *__restrict__ pos_dev,
+                                                            size_t stride) {
+    __shared__ __attribute__((aligned(16))) float s_v[2][64][64];
+    __shared__ __attribute__((aligned(16))) float s_p[2][8][64];
+    if (pos_dev) start_pos = *pos_dev;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int head = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int d0 = blockIdx.x * 64, t = blockIdx.y;
+    const int pos = start_pos + t, first = first_visible(pos, full);
+    const int keys = pos - first + 1, tiles = (keys + 63) / 64, mask = cache_len - 1;
+    const float *prow = probs + ((size_t)t * 8 + head) * stride;
+
+    // thread covers float4 (key kr, channels 4 cc .. 4 cc + 3) of a tile, twice
+    typedef float f4 __attribute__((ext_vector_type(4)));  // SROA-friendly (HIP's float4 is not)
+    struct Stage {
+        f4 v[2];
+        float p;
+    };
+    auto load_tile = [&](int tile, Stage &r) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int idx = i * 512 + tid, kr = idx >> 4, cc = idx & 15;
+            const int p = first + min(tile * 64 + kr, keys - 1);  // past the end: a valid row
+            r.v[i] = *reinterpret_cast<const f4 *>(value_cache + (size_t)(p & mask) * HD + d0 + 4 * cc);
+        }
+        r.p = prow[min(tile * 64 + lane, keys - 1)];
+    };
+    auto store_tile = [&](int slot, const Stage &r) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int idx = i * 512 + tid, kr = idx >> 4, cc = idx & 15;
+            *reinterpret_cast<f4 *>(&s_v[slot][kr][4 * cc]) = r.v[i];
+        }
+        s_p[slot][head][lane] = r.p;
+    };
+    Stage ring[DEPTH];
+    {
+        Stage head_tile;
+        load_tile(0, head_tile);
+#pragma unroll
+        for (int s = 0; s < DEPTH; s++) load_tile(min(s + 1, tiles - 1), ring[s]);
+        store_tile(0, head_tile);
+    }
+    float o = 0.0f;
+    // step: tile `tile` is in LDS slot tile & 1; ring slot holds tile + 1
+    // always_inline: called 16 times, and the ring must stay in registers
+    auto step = [&](int tile, Stage &slot, bool whole) __attribute__((always_inline)) {
+        __syncthreads();  // tile complete in LDS; every wave is done with tile - 1
+        // unconditional (past the last tile the slot is stored but never read):
+        // a conditional load would make the compiler drain the prefetch ring
+        store_tile((tile + 1) & 1, slot);
+        load_tile(min(tile + 1 + DEPTH, tiles - 1), slot);
+        const float(*v)[64] = s_v[tile & 1];
+        const float4 *pv = reinterpret_cast<const float4 *>(s_p[tile & 1][head]);
+        if (whole) {
+#pragma unroll
+            for (int k4 = 0; k4 < 16; k4++) {
+                const float4 p4 = pv[k4];
+                o = fmaf(p4.x, v[4 * k4 + 0][lane], o);
+                o = fmaf(p4.y, v[4 * k4 + 1][lane], o);
+                o = fmaf(p4.z, v[4 * k4 + 2][lane], o);
+                o = fmaf(p4.w, v[4 * k4 + 3][lane], o);
+            }
+        } else {
+            const int n = min(64, keys - tile * 64);
+            for (int k = 0; k < n; k++) o = fmaf(s_p[tile & 1][head][k], v[k][lane], o);
+        }
+    };
+    // Whole groups of DEPTH full tiles run with no branch at all (exact
+    // waits on the prefetch ring); the last < DEPTH tiles follow.  The steps
+    // are written out: a loop over them (barriers inside) is not unrolled, and
+    // a dynamically indexed ring would live in scratch memory.
+    const int full_tiles = keys / 64;
+    int tile = 0;
+    static_assert(DEPTH == 8, "the steps below are written out for 8 ring slots");
+    for (; tile + DEPTH <= full_tiles; tile += DEPTH) {
+        step(tile + 0, ring[0], true);
+        step(tile + 1, ring[1], true);
+        step(tile + 2, ring[2], true);
+        step(tile + 3, ring[3], true);
+        step(tile + 4, ring[4], true);
+        step(tile + 5, ring[5], true);
+        step(tile + 6, ring[6], true);
+        step(tile + 7, ring[7], true);
+    }
+#define G4_VALUES_TAIL(S) \
+    if (tile + S < tiles) step(tile + S, ring[S], false); /* uniform */
+    G4_VALUES_TAIL(0) G4_VALUES_TAIL(1) G4_VALUES_TAIL(2) G4_VALUES_TAIL(3)
+    G4_VALUES_TAIL(4) G4_VALUES_TAIL(5) G4_VALUES_TAIL(6) G4_VALUES_TAIL(7)
+#undef G4_VALUES_TAIL
+    out[((size_t)t * 8 + head) * HD + d0 + lane] = o;
+}
+
 int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
                             const float *value_cache, int cache_len, int head_dim, int heads,
-                            int full, int start_pos, size_t n) {
+                            int full, int start_pos, const int *pos_dev, size_t n) {
     if (!n) return G4_OK;
     if (heads != 8) return set_error(G4_ERR_ARG, "reference-order attention needs 8 query heads");
+    if (pos_dev && n != 1) return set_error(G4_ERR_ARG, "device-side positions are for one token");
     const int last_pos = start_pos + (int)n - 1;
-    const int max_keys = full ? last_pos + 1 : (last_pos + 1 < G4_WINDOW ? last_pos + 1 : G4_WINDOW);
+    // Keys a row can see, at most; with a device-side position the bound must
+    // hold for every position, so it is the cache's.
+    const int max_keys = pos_dev ? (full ? G4_MAX_CONTEXT : G4_WINDOW)
+                                 : full ? last_pos + 1 : (last_pos + 1 < G4_WINDOW ? last_pos + 1 : G4_WINDOW);
     const size_t stride = ((size_t)max_keys + 63) & ~(size_t)63;
-    int rc = scratch_reserve(0, n * heads * stride * sizeof(float));
+    // few rows of many keys (deep-context decode): the five-pass softmax
+    const bool long_rows = n <= 4 && max_keys > 1024;
+    const size_t score_floats = n * heads * stride;
+    const size_t work_floats = long_rows ? long_softmax_floats(n * heads, max_keys) : 0;
+    int rc = scratch_reserve(0, (score_floats + work_floats) * sizeof(float));
     if (rc) return rc;
     float *scores = scratch().attn;
-    // keys spanned by one block of tokens: its first token's window start to
-    // its last token
-    auto span = [&](int tq) {
+    // key blocks spanned by one block of tokens: its first token's window
+    // start to its last token (a fixed count with a device-side position:
+    // the kernel then strides over the blocks it needs)
+    auto key_blocks = [&](int tq) -> unsigned {
+        if (pos_dev) return full ? 512u : (unsigned)((G4_WINDOW + 63) / 64);
         const int tokens = (int)n < tq ? (int)n : tq;
         const int widest = full ? last_pos + 1 : G4_WINDOW - 1 + tokens;
-        return widest < last_pos + 1 ? widest : last_pos + 1;
+        const int span = widest < last_pos + 1 ? widest : last_pos + 1;
+        return (unsigned)((span + 63) / 64);
     };
     const unsigned nn = (unsigned)n;
     if (head_dim == 256) {
         constexpr int TQ = 6;
-        dim3 grid((unsigned)((span(TQ) + 63) / 64), (nn + TQ - 1) / TQ);
+        dim3 grid(key_blocks(TQ), (nn + TQ - 1) / TQ);
         hipLaunchKernelGGL((k_attn_scores<256, TQ>), grid, dim3(256), 0, s, q, key_cache, cache_len,
-                           full, start_pos, (int)n, stride, scores);
+                           full, start_pos, (int)n, pos_dev, stride, scores);
     } else {
         constexpr int TQ = 3;
-        dim3 grid((unsigned)((span(TQ) + 63) / 64), (nn + TQ - 1) / TQ);
+        dim3 grid(key_blocks(TQ), (nn + TQ - 1) / TQ);
         hipLaunchKernelGGL((k_attn_scores<512, TQ>), grid, dim3(256), 0, s, q, key_cache, cache_len,
-                           full, start_pos, (int)n, stride, scores);
+                           full, start_pos, (int)n, pos_dev, stride, scores);
     }
-    hipLaunchKernelGGL(k_attn_softmax_reference, dim3((unsigned)heads, nn), dim3(64), 0, s, scores,
-                       heads, full, start_pos, stride);
+    if (long_rows) {
+        const SoftmaxRows spec{heads, full, start_pos, 0, pos_dev};
+        launch_softmax_long(s, scores, stride, max_keys, spec, (unsigned)(n * heads),
+                            scores + score_floats);
+    } else {
+        hipLaunchKernelGGL(k_attn_softmax_reference, dim3((unsigned)heads, nn), dim3(64), 0, s,
+                           scores, heads, full, start_pos, pos_dev, stride);
+    }
     const unsigned slices = (unsigned)(head_dim / 64);
-    if (n <= 4) {  // decode: one token per block, 2 heads per lane, deep prefetch
+    if (n <= 4) {  // decode: one token per block, one head per wave, deep prefetch
         dim3 grid(slices, nn);
         if (head_dim == 256)
-            hipLaunchKernelGGL((k_attn_values<256, 4, 2, 8>), grid, dim3(256), 0, s, out, scores,
-                               value_cache, cache_len, full, start_pos, (int)n, stride);
+            hipLaunchKernelGGL((k_attn_values_decode<256, 8>), grid, dim3(512), 0, s, out, scores,
+                               value_cache, cache_len, full, start_pos, pos_dev, stride);
         else
-            hipLaunchKernelGGL((k_attn_values<512, 4, 2, 8>), grid, dim3(256), 0, s, out, scores,
-                               value_cache, cache_len, full, start_pos, (int)n, stride);
+            hipLaunchKernelGGL((k_attn_values_decode<512, 8>), grid, dim3(512), 0, s, out, scores,
+                               value_cache, cache_len, full, start_pos, pos_dev, stride);
     } else {  // prefill: 4 tokens x 8 heads per block share each V tile
         dim3 grid(slices, (nn + 3) / 4);
         if (head_dim == 256)
             hipLaunchKernelGGL((k_attn_values<256, 4, 8, 2>), grid, dim3(256), 0, s, out, scores,
-                               value_cache, cache_len, full, start_pos, (int)n, stride);
+                               value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride);
         else
             hipLaunchKernelGGL((k_attn_values<512, 4, 8, 2>), grid, dim3(256), 0, s, out, scores,
-                               value_cache, cache_len, full, start_pos, (int)n, stride);
+                               value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride);
     }
     return G4_OK;
 }
 
 int launch_attend(hipStream_t s, float *out, const float *q, const float *key_cache,
                   const float *value_cache, int cache_len, int head_dim, int heads, int full,
-                  int start_pos, size_t n) {
+                  int start_pos, const int *pos_dev, size_t n) {
     if (g_order == G4_ORDER_REFERENCE)
         return launch_attend_reference(s, out, q, key_cache, value_cache, cache_len, head_dim,
-                                       heads, full, start_pos, n);
+                                       heads, full, start_pos, pos_dev, n);
+    if (pos_dev) return set_error(G4_ERR_ARG, "device-side positions need reference order");
     return launch_attend_parallel(s, out, q, key_cache, value_cache, cache_len, head_dim, heads,
                                   full, start_pos, n);
 }
@@ -574,8 +862,16 @@ extern "C" int g4_set_order(int order) {
 extern "C" int g4_softmax(void *stream, float *values, int count, size_t rows) {
     G4_CHECK(values && count > 0, "g4_softmax: bad arguments");
     if (!rows) return G4_OK;
-    hipLaunchKernelGGL(g4::k_softmax_rows, dim3((unsigned)rows), dim3(64), 0, (hipStream_t)stream,
-                       values, count, (size_t)count);
+    if (count > 1024 && rows <= 64) {  // few long rows: the five-pass path
+        const int rc = g4::scratch_reserve(0, g4::long_softmax_floats(rows, count) * sizeof(float));
+        if (rc) return rc;
+        const g4::SoftmaxRows spec{1, 1, 0, count, nullptr};
+        g4::launch_softmax_long((hipStream_t)stream, values, (size_t)count, count, spec,
+                                (unsigned)rows, g4::scratch().attn);
+    } else {
+        hipLaunchKernelGGL(g4::k_softmax_rows, dim3((unsigned)rows), dim3(64), 0, (hipStream_t)stream,
+                           values, count, (size_t)count);
+    }
     G4_HIP(hipGetLastError());
     return G4_OK;
 }
