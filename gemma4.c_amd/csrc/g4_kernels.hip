@@ -208,6 +208,78 @@ __global__ __launch_bounds__(64) void k_gemv(float *__restrict__ out, size_t out
     }
 }
 
+// Few rows, split K inside one block: W = blockDim.x / 64 waves share one
+// 16-row weight strip, wave w taking groups [w G / W, (w + 1) G / W).  Each
+// group's exact dots go to LDS as floats together with the group's scale
+// product f16(ws) * xs; after one barrier, thread (m, r) folds its output's
+// groups in order (the reference's order, one fma each).  No second kernel.
+// Dynamic LDS: 2 x G x M x 16 floats.
+template <int M, int U>
+__global__ __launch_bounds__(1024) void k_gemv_split(float *__restrict__ out, size_t out_stride,
+                                                     const int8_t *__restrict__ xq,
+                                                     const float *__restrict__ xs,
+                                                     const int8_t *__restrict__ w,
+                                                     const uint16_t *__restrict__ ws, int k,
+                                                     int rows) {
+    extern __shared__ __attribute__((aligned(16))) float s_fold[];
+    const int groups = k >> 6, waves = blockDim.x >> 6;
+    float *s_d = s_fold, *s_c = s_fold + (size_t)groups * M * 16;  // [g][m][r]
+    const int block = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g_begin = (int)((long)wave * groups / waves);
+    const int g_end = (int)((long)(wave + 1) * groups / waves);
+    const int chunk = lane >> 2, b2 = (lane >> 2) & 1, b3 = (lane >> 3) & 1;
+    const int row = 4 * (lane & 3) + 2 * b2 + b3;
+    const uint4 *tiles = reinterpret_cast<const uint4 *>(w + (size_t)block * 16 * k) + lane;
+    const uint16_t *wscale = ws + (size_t)block * groups * 16 + row;
+    const int *xrow = reinterpret_cast<const int *>(xq) + chunk;
+
+    auto consume = [&](int gg, const uint4 &t, const int (&x4)[M], uint16_t wsr) {
+        int d[M];
+        gemv_group_dots<M>(t, x4, b2, b3, d);
+        if (lane < 16) {
+            const float wsf = half_bits_to_float(wsr);
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const int mm = min(m, rows - 1);
+                s_d[(gg * M + m) * 16 + row] = (float)d[m];
+                s_c[(gg * M + m) * 16 + row] = wsf * xs[(size_t)mm * groups + gg];
+            }
+        }
+    };
+    int g = g_begin;
+    for (; g + U <= g_end; g += U) {
+        uint4 t[U];
+        int x4[U][M];
+        uint16_t wsr[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            t[u] = tiles[(size_t)(g + u) * 64];
+#pragma unroll
+            for (int m = 0; m < M; m++)  // rows past `rows` reread the last row (unused)
+                x4[u][m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)(g + u) * 64) >> 2];
+            wsr[u] = wscale[(g + u) * 16];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) consume(g + u, t[u], x4[u], wsr[u]);
+    }
+    for (; g < g_end; g++) {
+        const uint4 t = tiles[(size_t)g * 64];
+        int x4[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) x4[m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)g * 64) >> 2];
+        consume(g, t, x4, wscale[g * 16]);
+    }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < 16 * M) {
+        const int m = tid >> 4, r = tid & 15;
+        const float *pd = s_d + m * 16 + r, *pc = s_c + m * 16 + r;
+        float acc = 0.0f;
+        for (int gg = 0; gg < groups; gg++) acc = fmaf(pd[gg * M * 16], pc[gg * M * 16], acc);
+        if (m < rows) out[(size_t)m * out_stride + (size_t)block * 16 + r] = acc;
+    }
+}
+
 // The group-ordered fold of split GEMV dots: one thread per output row.
 template <int M>
 __global__ __launch_bounds__(256) void k_gemv_fold(float *__restrict__ out, size_t out_stride,
@@ -428,6 +500,22 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
         splits = (2048 + blocks - 1) / blocks;
         const int max_splits = groups / 8 > 0 ? groups / 8 : 1;
         if (splits > max_splits) splits = max_splits;
+    }
+    // Split K inside one block when the per-group dots fit in LDS: no fold kernel.
+    const size_t fold_lds = (size_t)2 * groups * m_pad * 16 * sizeof(float);
+    if (splits > 1 && fold_lds <= 64 * 1024) {
+        const int waves = splits < 16 ? splits : 16;
+#define G4_GEMV_SPLIT(MM, UU)                                                                   \
+    hipLaunchKernelGGL((k_gemv_split<MM, UU>), dim3((unsigned)blocks), dim3(64 * waves), fold_lds, s, \
+                       out, out_stride, xq, xs, w, ws, k, rows)
+        switch (m_pad) {
+        case 1: G4_GEMV_SPLIT(1, 16); break;
+        case 2: G4_GEMV_SPLIT(2, 8); break;
+        case 4: G4_GEMV_SPLIT(4, 4); break;
+        default: G4_GEMV_SPLIT(8, 4); break;
+        }
+#undef G4_GEMV_SPLIT
+        return G4_OK;
     }
     int32_t *dots = nullptr;
     if (splits > 1) {
