@@ -71,6 +71,13 @@ void launch_rmsnorm_reference(hipStream_t s, float *out, const float *in, const 
                               int width, float eps, size_t rows);
 // gemma4.c:375-378
 void launch_add_and_scale(hipStream_t s, float *out, const float *add, size_t n, float scale);
+// Fused row tail for hidden rows of 1536, reference order (see k_row_tail):
+// optional rmsnorm of h, residual = (residual + h') * scale, optional rmsnorm
+// of the residual, optional quantize; y (may be null) receives the last value.
+// Supported flag sets: (1,1,1,1), (1,1,0,1), (1,1,0,0), (0,0,1,1).
+void launch_row_tail(hipStream_t s, const float *h, const float *w_in, float *residual, float scale,
+                     const float *w_out, float *y, int8_t *q8, float *qs, float eps, size_t rows,
+                     int norm_in, int add, int norm_out, int quant);
 // Position-dependent launchers take start_pos and pos_dev: when pos_dev is
 // non-null the kernels read the position from that device int instead (so a
 // captured decode graph can be replayed at every position), and the grid no

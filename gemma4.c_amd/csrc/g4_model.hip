@@ -326,13 +326,21 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
                      c.tokens_dev, n, sqrtf((float)G4_PLE));
     launch_add_and_scale(s, c.ple, c.hidden, (size_t)n * ple_width, 1.0f / sqrtf(2.0f));
 
+    // In reference order the row-local ops between matmuls run fused
+    // (launch_row_tail): the same arithmetic in one launch instead of up to four.
+    const bool fused = order() == G4_ORDER_REFERENCE;
+    if (fused)  // layer 0's input norm + quantize
+        launch_row_tail(s, nullptr, nullptr, c.residual, 1.0f, c.layers[0].input_ln, nullptr, c.q8,
+                        c.qs, 1e-6f, n, 0, 0, 1, 1);
     for (int l = 0; l < G4_LAYERS; l++) {
         const Layer &L = c.layers[l];
         const int hd = L.head_dim, qw = L.query_width, heads = qw / hd;
-        launch_rmsnorm(s, c.hidden, c.residual, L.input_ln, G4_HIDDEN, 1e-6f, n);
+        if (!fused) {
+            launch_rmsnorm(s, c.hidden, c.residual, L.input_ln, G4_HIDDEN, 1e-6f, n);
+            launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_HIDDEN / 64);
+        }
 
         // attention
-        launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_HIDDEN / 64);
         G4_TRY(matmul(c, c.aux, qw, L.q, n));
         launch_rmsnorm(s, c.aux, c.aux, L.q_norm, hd, 1e-6f, (size_t)n * heads);
         launch_rope(s, L.rope_cos, L.rope_sin, L.pairs, c.aux, heads, hd, start_pos, pos_dev, n);
@@ -349,30 +357,49 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
                              start_pos, pos_dev, n));
         launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * qw / 64);
         G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.o, n));
-        launch_rmsnorm(s, c.hidden, c.hidden, L.post_attn_ln, G4_HIDDEN, 1e-6f, n);
-        launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, 1.0f);
 
         // feed-forward
-        launch_rmsnorm(s, c.hidden, c.residual, L.pre_ffn_ln, G4_HIDDEN, 1e-6f, n);
-        launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_HIDDEN / 64);
+        if (fused) {
+            launch_row_tail(s, c.hidden, L.post_attn_ln, c.residual, 1.0f, L.pre_ffn_ln, nullptr,
+                            c.q8, c.qs, 1e-6f, n, 1, 1, 1, 1);
+        } else {
+            launch_rmsnorm(s, c.hidden, c.hidden, L.post_attn_ln, G4_HIDDEN, 1e-6f, n);
+            launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, 1.0f);
+            launch_rmsnorm(s, c.hidden, c.residual, L.pre_ffn_ln, G4_HIDDEN, 1e-6f, n);
+            launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_HIDDEN / 64);
+        }
         G4_TRY(matmul(c, c.hidden, L.ffn, L.gate, n));
         G4_TRY(matmul(c, c.aux, L.ffn, L.up, n));
         launch_geglu(s, c.hidden, c.aux, n, L.ffn, L.ffn, c.gelu, c.gelu_size, c.gelu_lower,
                      c.gelu_upper);
         launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * L.ffn / 64);
         G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.down, n));
-        launch_rmsnorm(s, c.hidden, c.hidden, L.post_ffn_ln, G4_HIDDEN, 1e-6f, n);
-        launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, 1.0f);
 
         // per-layer embedding
-        launch_quantize(s, c.q8, c.qs, c.residual, (size_t)n * G4_HIDDEN / 64);
+        if (fused) {
+            launch_row_tail(s, c.hidden, L.post_ffn_ln, c.residual, 1.0f, nullptr, nullptr, c.q8,
+                            c.qs, 1e-6f, n, 1, 1, 0, 1);
+        } else {
+            launch_rmsnorm(s, c.hidden, c.hidden, L.post_ffn_ln, G4_HIDDEN, 1e-6f, n);
+            launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, 1.0f);
+            launch_quantize(s, c.q8, c.qs, c.residual, (size_t)n * G4_HIDDEN / 64);
+        }
         G4_TRY(matmul(c, c.hidden, G4_PLE, L.ple_gate, n));
         launch_geglu(s, c.hidden, c.ple + (size_t)l * G4_PLE, n, G4_PLE, ple_width, c.gelu,
                      c.gelu_size, c.gelu_lower, c.gelu_upper);
         launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_PLE / 64);
         G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.ple_proj, n));
-        launch_rmsnorm(s, c.hidden, c.hidden, L.post_ple_ln, G4_HIDDEN, 1e-6f, n);
-        launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, L.layer_scalar);
+        if (fused) {
+            if (l + 1 < G4_LAYERS)  // + the next layer's input norm and quantize
+                launch_row_tail(s, c.hidden, L.post_ple_ln, c.residual, L.layer_scalar,
+                                c.layers[l + 1].input_ln, nullptr, c.q8, c.qs, 1e-6f, n, 1, 1, 1, 1);
+            else
+                launch_row_tail(s, c.hidden, L.post_ple_ln, c.residual, L.layer_scalar, nullptr,
+                                nullptr, nullptr, nullptr, 1e-6f, n, 1, 1, 0, 0);
+        } else {
+            launch_rmsnorm(s, c.hidden, c.hidden, L.post_ple_ln, G4_HIDDEN, 1e-6f, n);
+            launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, L.layer_scalar);
+        }
     }
     G4_HIP(hipGetLastError());
     return G4_OK;
@@ -423,8 +450,13 @@ static int forward(Context &c, const int *tokens, int n, int start_pos) {
 // gemma4.c:512-522 for `rows` consecutive rows starting at `row`, into dst.
 static int logits_rows(Context &c, float *dst, size_t row, int rows) {
     hipStream_t s = c.stream;
-    launch_rmsnorm(s, c.aux, c.residual + row * G4_HIDDEN, c.final_norm, G4_HIDDEN, 1e-6f, rows);
-    launch_quantize(s, c.q8, c.qs, c.aux, (size_t)rows * G4_HIDDEN / 64);
+    if (order() == G4_ORDER_REFERENCE) {
+        launch_row_tail(s, nullptr, nullptr, c.residual + row * G4_HIDDEN, 1.0f, c.final_norm, nullptr,
+                        c.q8, c.qs, 1e-6f, rows, 0, 0, 1, 1);
+    } else {
+        launch_rmsnorm(s, c.aux, c.residual + row * G4_HIDDEN, c.final_norm, G4_HIDDEN, 1e-6f, rows);
+        launch_quantize(s, c.q8, c.qs, c.aux, (size_t)rows * G4_HIDDEN / 64);
+    }
     G4_TRY(matmul(c, dst, G4_VOCAB, c.embed, rows));
     launch_softcap(s, dst, (size_t)rows * G4_VOCAB);
     G4_HIP(hipGetLastError());

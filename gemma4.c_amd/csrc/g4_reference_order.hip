@@ -96,14 +96,38 @@ __device__ __forceinline__ float chain_lds(const float4 *sq, int batches) {
     return sum;
 }
 
+// The reference's sequential sum of squares (gemma4.c:366-368) of a row held
+// by a wave as xv[v] = elements 256 v + 4 lane .. + 3.  Squares are computed
+// in parallel (each is rounded on its own in the reference too); the chain
+// walks the row in order, element k = 256 v + 4 l + c living in lane l,
+// register (v, c): each square is broadcast with v_readlane into a scalar
+// register and added by the whole wave, so every lane ends with the same sum
+// and no LDS or barrier is involved.  The readlanes do not depend on the
+// chain and fill its dependent-add stalls.
+template <int V>
+__device__ __forceinline__ float row_sum_squares(const float4 (&xv)[V]) {
+    float sq[V][4];
+#pragma unroll
+    for (int v = 0; v < V; v++) {
+        sq[v][0] = xv[v].x * xv[v].x;
+        sq[v][1] = xv[v].y * xv[v].y;
+        sq[v][2] = xv[v].z * xv[v].z;
+        sq[v][3] = xv[v].w * xv[v].w;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; v++)
+#pragma unroll
+        for (int l = 0; l < 64; l++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sq[v][c]), l));
+    return sum;
+}
+
 // Widths 256 * V (V = 1, 2, 6: per-head norms of 256 and 512, and the
-// hidden 1536).  Every lane holds its 4V values, squares and weights in
-// registers (loaded once, all loads in flight).  The chain then walks the
-// row in order, element k = 256 v + 4 l + c living in lane l, register
-// (v, c): each square is broadcast with v_readlane into a scalar register
-// and added by the whole wave, so every lane ends with the same sum and no
-// LDS or barrier is involved.  The readlanes do not depend on the chain and
-// fill its dependent-add stalls.
+// hidden 1536).  Every lane holds its 4V values and weights in registers
+// (loaded once, all loads in flight); the sum is row_sum_squares.
 template <int V>
 __global__ __launch_bounds__(256) void k_rmsnorm_reference_v(float *out, const float *in,
                                                              const float *__restrict__ weight,
@@ -124,28 +148,112 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reference_v(float *out, const f
 #pragma unroll
         for (int v = 0; v < V; v++) wv[v] = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
-    float sq[V][4];
-#pragma unroll
-    for (int v = 0; v < V; v++) {
-        sq[v][0] = xv[v].x * xv[v].x;
-        sq[v][1] = xv[v].y * xv[v].y;
-        sq[v][2] = xv[v].z * xv[v].z;
-        sq[v][3] = xv[v].w * xv[v].w;
-    }
-    float sum = 0.0f;
-#pragma unroll
-    for (int v = 0; v < V; v++)
-#pragma unroll
-        for (int l = 0; l < 64; l++)
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-                sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sq[v][c]), l));
-    const float inverse = 1.0f / sqrtf(sum / (float)W + eps);
+    const float inverse = 1.0f / sqrtf(row_sum_squares<V>(xv) / (float)W + eps);
     float4 *y4 = reinterpret_cast<float4 *>(out + wave_row * W);
 #pragma unroll
     for (int v = 0; v < V; v++)
         y4[v * 64 + lane] = make_float4(wv[v].x * (inverse * xv[v].x), wv[v].y * (inverse * xv[v].y),
                                         wv[v].z * (inverse * xv[v].z), wv[v].w * (inverse * xv[v].w));
+}
+
+// The row-local tail of a sublayer, fused for hidden rows of 1536 (one wave
+// per row, values in registers), reference order throughout:
+//   a = NORM_IN ? rmsnorm(h, w_in) : h                 (gemma4.c:360-373)
+//   if ADD:  residual = (residual + a) * scale         (gemma4.c:375-378)
+//   b = NORM_OUT ? rmsnorm(residual, w_out) : residual
+//   if QUANT: q8, qs = quantize(b)                     (gemma4.c:265-279)
+//   if y:     y = b
+// It replaces, e.g., rmsnorm + add_and_scale + rmsnorm + quantize between two
+// matmuls by one launch.  In-place use (y == h or y == residual) is allowed.
+template <bool NORM_IN, bool ADD, bool NORM_OUT, bool QUANT>
+__global__ __launch_bounds__(256) void k_row_tail(const float *h, const float *__restrict__ w_in,
+                                                  float *residual, float scale,
+                                                  const float *__restrict__ w_out, float *y,
+                                                  int8_t *__restrict__ q8, float *__restrict__ qs,
+                                                  float eps, size_t rows) {
+    constexpr int V = 6, W = 1536;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t row = (size_t)blockIdx.x * 4 + wave;
+    if (row >= rows) return;  // uniform per wave; no barrier follows
+    float4 rv[V];
+    const float4 *r4 = reinterpret_cast<const float4 *>(residual + row * W);
+#pragma unroll
+    for (int v = 0; v < V; v++) rv[v] = r4[v * 64 + lane];
+    if (ADD) {
+        float4 hv[V];
+        const float4 *h4 = reinterpret_cast<const float4 *>(h + row * W);
+#pragma unroll
+        for (int v = 0; v < V; v++) hv[v] = h4[v * 64 + lane];
+        if (NORM_IN) {
+            const float inverse = 1.0f / sqrtf(row_sum_squares<V>(hv) / (float)W + eps);
+            const float4 *w4 = reinterpret_cast<const float4 *>(w_in);
+#pragma unroll
+            for (int v = 0; v < V; v++) {
+                const float4 wv = w4[v * 64 + lane];
+                hv[v] = make_float4(wv.x * (inverse * hv[v].x), wv.y * (inverse * hv[v].y),
+                                    wv.z * (inverse * hv[v].z), wv.w * (inverse * hv[v].w));
+            }
+        }
+        float4 *rw = reinterpret_cast<float4 *>(residual + row * W);
+#pragma unroll
+        for (int v = 0; v < V; v++) {
+            rv[v] = make_float4((rv[v].x + hv[v].x) * scale, (rv[v].y + hv[v].y) * scale,
+                                (rv[v].z + hv[v].z) * scale, (rv[v].w + hv[v].w) * scale);
+            rw[v * 64 + lane] = rv[v];
+        }
+    }
+    if (NORM_OUT) {
+        const float inverse = 1.0f / sqrtf(row_sum_squares<V>(rv) / (float)W + eps);
+        const float4 *w4 = reinterpret_cast<const float4 *>(w_out);
+#pragma unroll
+        for (int v = 0; v < V; v++) {
+            const float4 wv = w4[v * 64 + lane];
+            rv[v] = make_float4(wv.x * (inverse * rv[v].x), wv.y * (inverse * rv[v].y),
+                                wv.z * (inverse * rv[v].z), wv.w * (inverse * rv[v].w));
+        }
+    }
+    if (y) {
+        float4 *y4 = reinterpret_cast<float4 *>(y + row * W);
+#pragma unroll
+        for (int v = 0; v < V; v++) y4[v * 64 + lane] = rv[v];
+    }
+    if (QUANT) {
+        // group 4v + lane/16 is the 16 lanes of one DPP row: absmax across them
+#pragma unroll
+        for (int v = 0; v < V; v++) {
+            const float4 x = rv[v];
+            float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+            const float gscale = m / 127.0f;
+            const float inverse = gscale > 0.0f ? 1.0f / gscale : 0.0f;
+            char4 out;
+            out.x = (signed char)(int)rintf(x.x * inverse);
+            out.y = (signed char)(int)rintf(x.y * inverse);
+            out.z = (signed char)(int)rintf(x.z * inverse);
+            out.w = (signed char)(int)rintf(x.w * inverse);
+            reinterpret_cast<char4 *>(q8 + row * W)[v * 64 + lane] = out;
+            if ((lane & 15) == 0) qs[row * (W / 64) + 4 * v + (lane >> 4)] = gscale;
+        }
+    }
+}
+
+void launch_row_tail(hipStream_t s, const float *h, const float *w_in, float *residual, float scale,
+                     const float *w_out, float *y, int8_t *q8, float *qs, float eps, size_t rows,
+                     int norm_in, int add, int norm_out, int quant) {
+    if (!rows) return;
+    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+#define G4_TAIL(A, B, C, D)                                                                    \
+    if (norm_in == A && add == B && norm_out == C && quant == D) {                             \
+        hipLaunchKernelGGL((k_row_tail<A, B, C, D>), grid, block, 0, s, h, w_in, residual, scale, \
+                           w_out, y, q8, qs, eps, rows);                                       \
+        return;                                                                                \
+    }
+    G4_TAIL(true, true, true, true)     // post-norm, residual add, pre-norm, quantize
+    G4_TAIL(true, true, false, true)    // post-norm, residual add, quantize the residual
+    G4_TAIL(true, true, false, false)   // post-norm, residual add
+    G4_TAIL(false, false, true, true)   // norm, quantize
+#undef G4_TAIL
 }
 
 // Any other width (per-op entry point): the same order, plainer loads.
