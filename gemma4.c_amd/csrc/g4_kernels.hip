@@ -482,14 +482,374 @@ __global__ __launch_bounds__(256) void k_gemm(float *__restrict__ out, size_t ou
         }
 }
 
+// Variant with B read straight from global memory: LDS then carries only the
+// activation tiles (and their scales), halving its traffic.  With the k-slots
+// of lane (l%16, l/16) taken as k = 16 (l/16) .. + 15, a lane's B operand is
+// four 4-byte words of the packed tile -- chunks 4 (l/16) .. + 3 of weight row
+// l%16 -- so B needs no reordering; A keeps its contiguous 16-byte reads.
+// B operands and weight scales are prefetched DEPTH groups ahead.
+template <int DEPTH>
+__global__ __launch_bounds__(256) void k_gemm_bg(float *__restrict__ out, size_t out_stride,
+                                                 const int8_t *__restrict__ xq,
+                                                 const float *__restrict__ xs,
+                                                 const int8_t *__restrict__ w,
+                                                 const uint16_t *__restrict__ ws, int rows,
+                                                 int n_out, int k) {
+    constexpr int BM = 64, BN = 64, NT = BN / 16, WN = BN / 2, NI = WN / 16, RS = 80;
+    __shared__ __attribute__((aligned(16))) int8_t s_a[2][BM * RS];
+    __shared__ __attribute__((aligned(16))) float s_xs[2][BM];
+    const int groups = k >> 6;
+    const int m0 = blockIdx.y * BM, nb0 = blockIdx.x * NT, n_blocks = n_out >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, q = lane >> 4, l16 = lane & 15;
+    const v4i zero = {0, 0, 0, 0};
+
+    const int a_row = tid >> 2, a_part = tid & 3;
+    const int8_t *a_src = xq + (size_t)min(m0 + a_row, rows - 1) * k + a_part * 16;
+    const float *x_src = xs + (size_t)min(m0 + (tid & (BM - 1)), rows - 1) * groups;
+    // this lane's words of its two B tiles: chunk 4q + i of row l16 at
+    // tile + (4q + i) * 64 + 4 l16; scales at [tile][g][l16]
+    const int *b_src[NI];
+    const uint16_t *w_src[NI];
+#pragma unroll
+    for (int ni = 0; ni < NI; ni++) {
+        const int t = min(nb0 + wn * (WN / 16) + ni, n_blocks - 1);
+        b_src[ni] = reinterpret_cast<const int *>(w + (size_t)t * groups * 1024) + q * 64 + l16;
+        w_src[ni] = ws + (size_t)t * groups * 16 + l16;
+    }
+    struct BStage {
+        v4i b[NI];
+        uint16_t w[NI];
+    };
+    auto bload = [&](int g, BStage &r) {
+        g = min(g, groups - 1);
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++) {
+            const int *src = b_src[ni] + (size_t)g * 256;
+#pragma unroll
+            for (int i = 0; i < 4; i++) r.b[ni][i] = src[i * 16];
+            r.w[ni] = w_src[ni][g * 16];
+        }
+    };
+    struct AStage {
+        v4i a;
+        float x;
+    };
+    auto aload = [&](int g, AStage &r) {
+        g = min(g, groups - 1);
+        r.a = *reinterpret_cast<const v4i *>(a_src + g * 64);
+        r.x = x_src[g];
+    };
+    auto astore = [&](int buf, const AStage &r) {
+        *reinterpret_cast<v4i *>(s_a[buf] + a_row * RS + a_part * 16) = r.a;
+        if (tid < BM) s_xs[buf][tid] = r.x;
+    };
+
+    float acc[2][NI][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < NI; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[i][j][v] = 0.0f;
+
+    auto compute = [&](int buf, const BStage &bs) {
+        v4i a[2];
+        float4 xv[2];
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+            const int r = wm * 32 + mi * 16;
+            a[mi] = *reinterpret_cast<const v4i *>(s_a[buf] + (r + l16) * RS + q * 16);
+            xv[mi] = *reinterpret_cast<const float4 *>(&s_xs[buf][r + 4 * q]);
+        }
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++) {
+            const float wsf = half_bits_to_float(bs.w[ni]);
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) {
+                const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], bs.b[ni], zero, 0, 0, 0);
+                acc[mi][ni][0] = fmaf((float)d[0], wsf * xv[mi].x, acc[mi][ni][0]);
+                acc[mi][ni][1] = fmaf((float)d[1], wsf * xv[mi].y, acc[mi][ni][1]);
+                acc[mi][ni][2] = fmaf((float)d[2], wsf * xv[mi].z, acc[mi][ni][2]);
+                acc[mi][ni][3] = fmaf((float)d[3], wsf * xv[mi].w, acc[mi][ni][3]);
+            }
+        }
+    };
+
+    // A: double-buffered LDS, next group in registers; B: DEPTH groups in
+    // registers.  One barrier per group.
+    AStage an;
+    BStage bring[DEPTH];
+    {
+        AStage a0;
+        aload(0, a0);
+        aload(1, an);
+#pragma unroll
+        for (int s2 = 0; s2 < DEPTH; s2++) bload(s2, bring[s2]);
+        astore(0, a0);
+    }
+    __syncthreads();
+    int g = 0;
+    for (; g + DEPTH <= groups; g += DEPTH) {
+#pragma unroll
+        for (int s2 = 0; s2 < DEPTH; s2++) {
+            const int gg = g + s2, buf = gg & 1;
+            compute(buf, bring[s2]);
+            bload(gg + DEPTH, bring[s2]);
+            astore(buf ^ 1, an);
+            aload(gg + 2, an);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < DEPTH; s2++) {
+        if (g + s2 < groups) {  // uniform
+            const int gg = g + s2, buf = gg & 1;
+            compute(buf, bring[s2]);
+            astore(buf ^ 1, an);
+            aload(gg + 2, an);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++) {
+            const int col = wn * WN + ni * 16;
+            if (nb0 + (col >> 4) >= n_blocks) continue;
+            const size_t n = (size_t)nb0 * 16 + col + l16;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = m0 + wm * 32 + mi * 16 + 4 * q + v;
+                if (m < rows) out[(size_t)m * out_stride + n] = acc[mi][ni][v];
+            }
+        }
+}
+
+// Prefill W8A8 GEMM with every operand brought into LDS by the gfx950 LDS-DMA
+// loads (global_load_lds): no registers hold tiles in flight, and the number
+// of vector-memory instructions -- what bounds this kernel -- is kept low:
+// each wave issues two 1-KB loads per group, plus one 1-KB load of scales
+// every 8 groups.  64 x 64 outputs per 256-thread block (2 x 2 waves of
+// 32 x 32), one 64-deep K step per quantization group, the group-ordered fp32
+// fold of the reference (bit-identical).  Requires groups % 8 == 0.
+//   A  64 rows x 64 B per group: wave w fetches rows 16w .. 16w + 15, lane L
+//      the 16-byte part (L & 3) ^ ((row >> 2) & 3) of row 16w + L / 4, so the
+//      parts of a row are stored XOR-swizzled and a lane's 16-byte operand
+//      read (row, part q) is bank-conflict free;
+//   B  4 packed tiles per group: wave w fetches tile w; LDS slot s holds the
+//      tile's 16-byte unit s ^ (4 (s / 16) & 12), so the four 4-byte reads of
+//      a lane's operand are conflict free;
+//   scales, per 8 groups: waves 0, 1 fetch the activation scales of groups
+//      0-3, 4-7 (16 bytes per row), wave 2 the weight scales of the 4 tiles
+//      (256 bytes per tile), wave 3 repeats wave 2 into padding.
+// k-slots: lane (l%16, l/16) covers k = 16 (l/16) + 0..15 -- for B that is
+// chunks 4 (l/16) .. + 3 of weight row l%16.
+__global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_t out_stride,
+                                                  const int8_t *__restrict__ xq,
+                                                  const float *__restrict__ xs,
+                                                  const int8_t *__restrict__ w,
+                                                  const uint16_t *__restrict__ ws, int rows,
+                                                  int n_out, int k) {
+    constexpr int BM = 64, BN = 64, NT = BN / 16, WN = BN / 2, NI = WN / 16;
+    struct alignas(16) Stage {
+        int8_t a[BM * 64];
+        int8_t b[NT * 1024];
+    };
+    struct alignas(16) Scales {  // 8 groups
+        float x[2][BM][4];          // [group / 4][row][group % 4]
+        uint16_t s[2][NT][8][16];   // [0]: [tile][group][row]; [1]: padding
+    };
+    // One __shared__ object per stage: the compiler then tells a read of one
+    // stage from the DMA writes still landing in the others (with one array
+    // it would wait for every DMA before every LDS read).
+    __shared__ Stage st0, st1, st2, st3;
+    __shared__ Scales sc0, sc1;
+    const int groups = k >> 6;
+    const int m0 = blockIdx.y * BM, nb0 = blockIdx.x * NT, n_blocks = n_out >> 4;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1, q = lane >> 4, l16 = lane & 15;
+    const v4i zero = {0, 0, 0, 0};
+
+    // DMA sources (group 0, chunk 0); the builtin wants plain void pointers
+    const int a_row = 16 * wave + (lane >> 2);
+    const int8_t *a_src = xq + (size_t)min(m0 + a_row, rows - 1) * k +
+                          16 * ((lane & 3) ^ ((a_row >> 2) & 3));
+    const int unit = lane ^ ((lane >> 4) << 2);
+    const int8_t *b_src = w + (size_t)min(nb0 + wave, n_blocks - 1) * groups * 1024 + unit * 16;
+    const char *c_src;  // scales: 16 bytes a lane, advancing 8 groups per chunk
+    size_t c_step;
+    if (wave < 2) {
+        c_src = (const char *)(xs + (size_t)min(m0 + lane, rows - 1) * groups + 4 * wave);
+        c_step = 8 * sizeof(float);
+    } else {
+        c_src = (const char *)(ws + (size_t)min(nb0 + (lane >> 4), n_blocks - 1) * groups * 16 + 8 * l16);
+        c_step = 8 * 16 * sizeof(uint16_t);
+    }
+    const int c_dst = wave < 2 ? wave * (BM * 16) : 2 * BM * 16 + (wave - 2) * (NT * 8 * 16 * 2);
+    auto issue = [&](int g, Stage &d) __attribute__((always_inline)) {
+        g = min(g, groups - 1);  // past the end: reload the last group (never read)
+        __builtin_amdgcn_global_load_lds((const void *)(a_src + g * 64), (void *)(d.a + wave * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void *)(b_src + (size_t)g * 1024), (void *)(d.b + wave * 1024), 16, 0, 0);
+    };
+    auto issue_scales = [&](int chunk, Scales &d) __attribute__((always_inline)) {
+        chunk = min(chunk, groups / 8 - 1);
+        __builtin_amdgcn_global_load_lds((const void *)(c_src + (size_t)chunk * c_step),
+                                         (void *)((char *)&d + c_dst), 16, 0, 0);
+    };
+    // LDS read addresses (loop invariant)
+    int a_off[2];
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++) {
+        const int r = wm * 32 + mi * 16 + l16;
+        a_off[mi] = r * 64 + 16 * (q ^ ((r >> 2) & 3));
+    }
+    int b_off[NI][4];
+#pragma unroll
+    for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            // chunk c = 4q + i of row l16 is global unit u = 4c + l16 / 4,
+            // stored at slot u ^ (4 (u / 16) & 12)
+            const int u = 4 * (4 * q + i) + (l16 >> 2), slot = u ^ ((u >> 4) << 2);
+            b_off[ni][i] = (wn * NI + ni) * 1024 + slot * 16 + (l16 & 3) * 4;
+        }
+
+    float acc[2][NI][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < NI; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[i][j][v] = 0.0f;
+
+    // A group's four MFMAs are issued together into their own registers and
+    // folded one step later, while the next group's MFMAs run: the fold never
+    // waits on a fresh MFMA result.
+    struct Dots {
+        v4i d[2][NI];
+        float x[2][4];
+        float w[NI];
+    };
+    struct Frags {
+        v4i a[2], b[NI];
+    };
+    auto fetch = [&](const Stage &d, const Scales &s, int j, Frags &f, Dots &o)
+                     __attribute__((always_inline)) {
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) {
+            f.a[mi] = *reinterpret_cast<const v4i *>(d.a + a_off[mi]);
+#pragma unroll
+            for (int v = 0; v < 4; v++) o.x[mi][v] = s.x[j >> 2][wm * 32 + mi * 16 + 4 * q + v][j & 3];
+        }
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) f.b[ni][i] = *reinterpret_cast<const int *>(d.b + b_off[ni][i]);
+            o.w[ni] = half_bits_to_float(s.s[0][wn * NI + ni][j][l16]);
+        }
+    };
+    auto multiply = [&](const Frags &f, Dots &o) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+                o.d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[mi], f.b[ni], zero, 0, 0, 0);
+    };
+    auto fold = [&](const Dots &o) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    acc[mi][ni][v] = fmaf((float)o.d[mi][ni][v], o.w[ni] * o.x[mi][v], acc[mi][ni][v]);
+    };
+
+    // Step g (j = g % 8): issue group g + 2 into the stage of group g - 2
+    // (whose reads every wave finished before the previous barrier), plus the
+    // next chunk's scales when g + 2 starts one; wait until group g (and its
+    // chunk's scales) has landed -- the loads of groups g + 1, g + 2 may still
+    // be in flight -- and let the barrier publish it; then read its operands,
+    // fold group g - 1 and issue group g's MFMAs.
+    auto step = [&](int g, int j, Stage &fill, const Stage &use, const Scales &sc_use,
+                    Scales &sc_fill, Dots &cur, const Dots &prev) __attribute__((always_inline)) {
+        issue(g + 2, fill);
+        if (j == 6) issue_scales(g / 8 + 1, sc_fill);
+        if (j == 6 || j == 7)
+            __builtin_amdgcn_s_waitcnt(0xF70 | 5);  // vmcnt(5): 2 + 2 + the scale chunk
+        else
+            __builtin_amdgcn_s_waitcnt(0xF70 | 4);  // vmcnt(4)
+        __builtin_amdgcn_s_barrier();
+        Frags f;
+        fetch(use, sc_use, j, f, cur);  // LDS reads in flight ...
+        __builtin_amdgcn_sched_barrier(0);
+        fold(prev);                     // ... while group g - 1 is folded
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(f, cur);               // results are folded one step later
+    };
+    Dots d0, d1;  // d1 starts as zeros: fmaf(0, 0, acc) = acc
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) d1.x[mi][v] = 0.0f;
+#pragma unroll
+    for (int ni = 0; ni < NI; ni++) {
+        d1.w[ni] = 0.0f;
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++) d1.d[mi][ni] = zero;
+    }
+    issue(0, st0);
+    issue_scales(0, sc0);
+    issue(1, st1);
+    // 16 groups per pass so that every stage and scale buffer is a fixed
+    // object (chunk c = g / 8 lives in sc0 for even c, sc1 for odd c)
+    auto eight = [&](int g, Scales &sc_use, Scales &sc_next) __attribute__((always_inline)) {
+        step(g + 0, 0, st2, st0, sc_use, sc_next, d0, d1);
+        step(g + 1, 1, st3, st1, sc_use, sc_next, d1, d0);
+        step(g + 2, 2, st0, st2, sc_use, sc_next, d0, d1);
+        step(g + 3, 3, st1, st3, sc_use, sc_next, d1, d0);
+        step(g + 4, 4, st2, st0, sc_use, sc_next, d0, d1);
+        step(g + 5, 5, st3, st1, sc_use, sc_next, d1, d0);
+        step(g + 6, 6, st0, st2, sc_use, sc_next, d0, d1);
+        step(g + 7, 7, st1, st3, sc_use, sc_next, d1, d0);
+    };
+    int g = 0;
+    for (; g + 16 <= groups; g += 16) {
+        eight(g, sc0, sc1);
+        eight(g + 8, sc1, sc0);
+    }
+    if (g < groups) eight(g, sc0, sc1);  // uniform: groups % 16 == 8
+    fold(d1);  // the last group (groups % 8 == 0: it went to d1)
+    __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): no DMA outlives the block
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++) {
+            const int col = wn * WN + ni * 16;
+            if (nb0 + (col >> 4) >= n_blocks) continue;
+            const size_t n = (size_t)nb0 * 16 + col + l16;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = m0 + wm * 32 + mi * 16 + 4 * q + v;
+                if (m < rows) out[(size_t)m * out_stride + n] = acc[mi][ni][v];
+            }
+        }
+}
+
 int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq, const float *xs,
                   const int8_t *w, const uint16_t *ws, int n_out, int k, int rows) {
     if (rows <= 0) return G4_OK;
     const int blocks = n_out / 16, groups = k / 64;
     if (rows > 8) {
         const unsigned mb = (unsigned)((rows + 63) / 64);
-        hipLaunchKernelGGL((k_gemm<64, 1>), dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
-                           out, out_stride, xq, xs, w, ws, rows, n_out, k);
+        if (groups % 8 == 0)
+            hipLaunchKernelGGL(k_gemm_dma, dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
+                               out, out_stride, xq, xs, w, ws, rows, n_out, k);
+        else
+            hipLaunchKernelGGL((k_gemm<64, 1>), dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
+                               out, out_stride, xq, xs, w, ws, rows, n_out, k);
         return G4_OK;
     }
     const int m_pad = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
