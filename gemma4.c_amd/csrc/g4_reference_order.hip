@@ -96,6 +96,95 @@ __device__ __forceinline__ float chain_lds(const float4 *sq, int batches) {
     return sum;
 }
 
+// ---------------------------------------------------------------------------
+// The sequential fp32 sum of non-negative terms, computed in parallel and bit
+// for bit.  s_0 = 0, s_k = RN(s_{k-1} + t_k) in order (the reference's loop).
+// While s stays inside one binade [2^e, 2^(e+1)) every partial sum is a
+// multiple of u = 2^(e-23), and adding t_k rounds it to the nearest multiple:
+// s_k = s_{k-1} + R_k u with R_k = rint(t_k / u) -- independent of s_{k-1}
+// except at an exact half (a tie, where round-to-even looks at s_{k-1}).  So a
+// run of steps is an integer prefix sum over the wave; the run ends at the
+// first step that reaches 2^(e+1) (the grid changes) or is a tie, and that
+// one step is done as the plain fp32 add before the next run starts.  The
+// terms are held "block-major": t[b] in lane l is term 64 b + l.
+__device__ __forceinline__ int wave_add_scan(int x) {  // inclusive, over 64 lanes
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return x;
+}
+
+// Advance the running sum s over the 64 terms of one block (lane l holds
+// term l), from term p0 to the end of the block, in order.  Lanes flagged in
+// `special` are a new running maximum of a softmax: s = s * t + 1 there
+// (two roundings, gemma4.c:403) instead of s + t.  Terms must be >= 0; with
+// no special lanes s must start >= 0, with special lanes s >= 1.
+__device__ __forceinline__ float block_advance(float s, float tb, int p0, uint64_t special) {
+    const int lane = threadIdx.x & 63;
+    int p = p0;
+    while (p < 64) {  // uniform
+        const uint32_t bits = __float_as_uint(s);
+        const int e = (int)((bits >> 23) & 0xff) - 127;  // exponent of s (s >= 0)
+        if (e < -100 || e > 100) {  // zero, tiny, huge, inf, nan: one plain step
+            const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tb), p));
+            s = (special >> p) & 1 ? s * t + 1.0f : s + t;
+            p++;
+            continue;
+        }
+        const int ue = e - 23;                     // log2 of the grid u
+        const int S = (int)ldexpf(s, -ue);         // s / u, exact, in [2^23, 2^24)
+        const bool active = lane >= p;
+        // t / u, exact; clamped at 2^24 (such a term ends the run anyway), so
+        // 64 of them cannot overflow the int prefix sum
+        const float T = active ? fminf(ldexpf(tb, -ue), 16777216.0f) : 0.0f;
+        const bool tie = active && (T - floorf(T) == 0.5f);
+        const int P = wave_add_scan((int)rintf(T));  // nearest, ties to even
+        const bool stop = active && (tie || ((special >> lane) & 1) || S + P >= (1 << 24));
+        const uint64_t mask = __ballot(stop);
+        if (mask == 0) {  // the run covers the rest of the block
+            s = ldexpf((float)(S + __builtin_amdgcn_readlane(P, 63)), ue);
+            break;
+        }
+        // the run ends before term L, which is applied plainly
+        const int L = (int)__builtin_ctzll(mask);
+        const int before = L > 0 ? __builtin_amdgcn_readlane(P, L - 1) : 0;
+        s = ldexpf((float)(S + before), ue);
+        const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tb), L));
+        s = (special >> L) & 1 ? s * t + 1.0f : s + t;
+        p = L + 1;
+    }
+    return s;
+}
+
+template <int NB>
+__device__ __forceinline__ float exact_sequential_sum(const float (&t)[NB]) {
+    float s = 0.0f;
+#pragma unroll
+    for (int b = 0; b < NB; b++) s = block_advance(s, t[b], 0, 0);
+    return s;
+}
+
+// The sum of squares of a row of 256 V held as xv[v] = elements 256 v +
+// 4 lane .. + 3, through exact_sequential_sum: the row is re-read block-major
+// from this wave's LDS row buffer (W floats), the squares recomputed there.
+template <int V>
+__device__ __forceinline__ float row_sum_squares_fast(const float4 (&xv)[V], float *lds_row) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int v = 0; v < V; v++) reinterpret_cast<float4 *>(lds_row)[v * 64 + lane] = xv[v];
+    // (a wave's LDS accesses complete in order: no barrier, the compiler waits)
+    float t[4 * V];
+#pragma unroll
+    for (int b = 0; b < 4 * V; b++) {
+        const float x = lds_row[64 * b + lane];
+        t[b] = x * x;
+    }
+    return exact_sequential_sum<4 * V>(t);
+}
+
 // The reference's sequential sum of squares (gemma4.c:366-368) of a row held
 // by a wave as xv[v] = elements 256 v + 4 lane .. + 3.  Squares are computed
 // in parallel (each is rounded on its own in the reference too); the chain
@@ -172,24 +261,35 @@ __global__ __launch_bounds__(256) void k_row_tail(const float *h, const float *_
                                                   int8_t *__restrict__ q8, float *__restrict__ qs,
                                                   float eps, size_t rows) {
     constexpr int V = 6, W = 1536;
+    __shared__ __attribute__((aligned(16))) float s_rows[4][W];  // per-wave transpose buffer
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t row = (size_t)blockIdx.x * 4 + wave;
     if (row >= rows) return;  // uniform per wave; no barrier follows
-    float4 rv[V];
+    float4 rv[V], wiv[V], wov[V];
     const float4 *r4 = reinterpret_cast<const float4 *>(residual + row * W);
 #pragma unroll
     for (int v = 0; v < V; v++) rv[v] = r4[v * 64 + lane];
+    // weights first: their loads overlap the sums instead of following them
+    if (NORM_IN) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(w_in);
+#pragma unroll
+        for (int v = 0; v < V; v++) wiv[v] = w4[v * 64 + lane];
+    }
+    if (NORM_OUT) {
+        const float4 *w4 = reinterpret_cast<const float4 *>(w_out);
+#pragma unroll
+        for (int v = 0; v < V; v++) wov[v] = w4[v * 64 + lane];
+    }
     if (ADD) {
         float4 hv[V];
         const float4 *h4 = reinterpret_cast<const float4 *>(h + row * W);
 #pragma unroll
         for (int v = 0; v < V; v++) hv[v] = h4[v * 64 + lane];
         if (NORM_IN) {
-            const float inverse = 1.0f / sqrtf(row_sum_squares<V>(hv) / (float)W + eps);
-            const float4 *w4 = reinterpret_cast<const float4 *>(w_in);
+            const float inverse = 1.0f / sqrtf(row_sum_squares_fast<V>(hv, s_rows[wave]) / (float)W + eps);
 #pragma unroll
             for (int v = 0; v < V; v++) {
-                const float4 wv = w4[v * 64 + lane];
+                const float4 wv = wiv[v];
                 hv[v] = make_float4(wv.x * (inverse * hv[v].x), wv.y * (inverse * hv[v].y),
                                     wv.z * (inverse * hv[v].z), wv.w * (inverse * hv[v].w));
             }
@@ -203,11 +303,10 @@ __global__ __launch_bounds__(256) void k_row_tail(const float *h, const float *_
         }
     }
     if (NORM_OUT) {
-        const float inverse = 1.0f / sqrtf(row_sum_squares<V>(rv) / (float)W + eps);
-        const float4 *w4 = reinterpret_cast<const float4 *>(w_out);
+        const float inverse = 1.0f / sqrtf(row_sum_squares_fast<V>(rv, s_rows[wave]) / (float)W + eps);
 #pragma unroll
         for (int v = 0; v < V; v++) {
-            const float4 wv = w4[v * 64 + lane];
+            const float4 wv = wov[v];
             rv[v] = make_float4(wv.x * (inverse * rv[v].x), wv.y * (inverse * rv[v].y),
                                 wv.z * (inverse * rv[v].z), wv.w * (inverse * rv[v].w));
         }
@@ -442,21 +541,8 @@ __device__ void softmax_row_reference(float *v, int count) {
         // adding +0 leaves the (positive) sum unchanged
         const float e = is_new ? expf_libm(before - x) : expf_libm(x - before);
         const uint64_t new_mask = __ballot(is_new);
-        // The running sum, in order: every lane runs the same chain, reading
-        // term j from lane j with v_readlane (no LDS, no barrier).
-        if (new_mask == 0) {
-#pragma unroll
-            for (int j = 0; j < 64; j++)
-                sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-        } else {
-            const int n = count - base < 64 ? count - base : 64;
-            for (int j = 0; j < n; j++) {
-                const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-                const float grown = sum * ej + 1.0f;  // a new maximum: rescale (two roundings)
-                const float added = sum + ej;
-                sum = (new_mask >> j) & 1 ? grown : added;
-            }
-        }
+        // the running sum over this block, in order (exact, see block_advance)
+        sum = block_advance(sum, e, 0, new_mask);
         carry = __shfl(incl, 63);
     }
     const float max = carry;
@@ -581,18 +667,7 @@ __global__ __launch_bounds__(64) void k_lsm_chain(SoftmaxRows spec, const float 
                 const uint64_t mask =
                     ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(masks >> 32), j) << 32) |
                     (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)masks, j);
-                if (mask == 0) {
-#pragma unroll
-                    for (int k = 0; k < 64; k++)
-                        sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k));
-                } else {
-                    for (int k = 0; k < 64; k++) {
-                        const float ek = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), k));
-                        const float grown = sum * ek + 1.0f;
-                        const float added = sum + ek;
-                        sum = (mask >> k) & 1 ? grown : added;
-                    }
-                }
+                sum = block_advance(sum, e, 0, mask);  // exact, in order
             }
         }
     }
