@@ -222,6 +222,9 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reference_v(float *out, const f
                                                              const float *__restrict__ weight,
                                                              float eps, size_t rows) {
     constexpr int W = 256 * V;
+    // rows of 1536: the exact parallel sum (LDS transpose buffer per wave);
+    // shorter rows: the readlane chain
+    __shared__ __attribute__((aligned(16))) float s_rows[V == 6 ? 4 : 1][V == 6 ? W : 4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t wave_row = (size_t)blockIdx.x * 4 + wave;
     if (wave_row >= rows) return;  // uniform per wave; no block-level barrier follows
@@ -237,7 +240,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reference_v(float *out, const f
 #pragma unroll
         for (int v = 0; v < V; v++) wv[v] = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
-    const float inverse = 1.0f / sqrtf(row_sum_squares<V>(xv) / (float)W + eps);
+    float sum;
+    if constexpr (V == 6)
+        sum = row_sum_squares_fast<V>(xv, s_rows[wave]);
+    else
+        sum = row_sum_squares<V>(xv);
+    const float inverse = 1.0f / sqrtf(sum / (float)W + eps);
     float4 *y4 = reinterpret_cast<float4 *>(out + wave_row * W);
 #pragma unroll
     for (int v = 0; v < V; v++)

@@ -142,6 +142,34 @@ def test_rmsnorm_reference_order_bitexact(pkg, g4lib, torch_gpu, ok, order):
         assert np.array_equal(out, ref), width
 
 
+@pytest.mark.parametrize("order", [0], indirect=True)
+def test_rmsnorm_reference_order_adversarial(pkg, g4lib, torch_gpu, ok, order):
+    """Rows that stress the exact parallel evaluation of the sequential sum of
+    squares: many exact half-ulp ties (1 + k 2^-12 squared), leading and
+    scattered zeros, magnitudes spread over 2^-60 .. 2^60, tiny values,
+    all-equal rows, a single nonzero at the end -- bit for bit."""
+    g = rng(47)
+    w = 1536
+    rows = [
+        (1.0 + g.integers(0, 4, w) * 2.0 ** -12).astype(np.float32),
+        (1.0 + g.integers(0, 64, w) * 2.0 ** -12).astype(np.float32),
+        np.where(g.random(w) < 0.9, 0.0, g.standard_normal(w)).astype(np.float32),
+        np.concatenate([np.zeros(700), g.standard_normal(w - 700)]).astype(np.float32),
+        (g.standard_normal(w) * np.exp2(g.uniform(-60, 60, w))).astype(np.float32),
+        (g.standard_normal(w) * 1e-20).astype(np.float32),
+        np.full(w, 3.0, np.float32),
+        np.concatenate([np.zeros(w - 1), [5.0]]).astype(np.float32),
+        np.exp2(np.arange(w) % 40 - 20).astype(np.float32),
+        np.exp2(-(np.arange(w) % 40)).astype(np.float32),
+    ]
+    x = np.stack(rows)
+    wt = g.uniform(0.5, 1.5, w).astype(np.float32)
+    out = gpu_rmsnorm(pkg, g4lib, torch_gpu, x, wt, w)
+    ref = ok.rmsnorm(x, HostF32(pkg, wt).record, w, 1e-6)
+    for i in range(len(rows)):
+        assert np.array_equal(out[i], ref[i]), i
+
+
 def test_rmsnorm_golden(pkg, g4lib, torch_gpu):
     gold = load_golden("ops.npz")
     out = gpu_rmsnorm(pkg, g4lib, torch_gpu, gold["rms_x"], gold["rms_w"], 1536)
