@@ -11,6 +11,8 @@
 #include <float.h>
 #include <math.h>
 
+#include <type_traits>
+
 #include "g4_internal.h"
 
 namespace g4 {
@@ -178,29 +180,31 @@ __global__ __launch_bounds__(64) void k_gemv(float *__restrict__ out, size_t out
         }
     };
 
-    int g = g_begin;
-    for (; g + U <= g_end; g += U) {
-        uint4 t[U];
-        int x4[U][M];
-        uint16_t wsr[U];
+    // Loads for a batch of B groups are issued before any is consumed; the
+    // range is covered by batches of U, then U/2, U/4, ... (all loads of a
+    // batch in flight together), so a wave's few groups never go one by one.
+    auto batch = [&](int g0, auto bsize) __attribute__((always_inline)) {
+        constexpr int B = decltype(bsize)::value;
+        uint4 t[B];
+        int x4[B][M];
+        uint16_t wsr[B];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            t[u] = tiles[(size_t)(g + u) * 64];
+        for (int u = 0; u < B; u++) {
+            t[u] = tiles[(size_t)(g0 + u) * 64];
 #pragma unroll
             for (int m = 0; m < M; m++)  // rows past `rows` reread the last row (unused)
-                x4[u][m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)(g + u) * 64) >> 2];
-            wsr[u] = wscale[(g + u) * 16];
+                x4[u][m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)(g0 + u) * 64) >> 2];
+            wsr[u] = wscale[(g0 + u) * 16];
         }
 #pragma unroll
-        for (int u = 0; u < U; u++) consume(g + u, t[u], x4[u], wsr[u]);
-    }
-    for (; g < g_end; g++) {
-        const uint4 t = tiles[(size_t)g * 64];
-        int x4[M];
-#pragma unroll
-        for (int m = 0; m < M; m++) x4[m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)g * 64) >> 2];
-        consume(g, t, x4, wscale[g * 16]);
-    }
+        for (int u = 0; u < B; u++) consume(g0 + u, t[u], x4[u], wsr[u]);
+    };
+    int g = g_begin;
+    for (; g + U <= g_end; g += U) batch(g, std::integral_constant<int, U>());
+    if constexpr (U >= 16) if (g + 8 <= g_end) { batch(g, std::integral_constant<int, 8>()); g += 8; }
+    if constexpr (U >= 8) if (g + 4 <= g_end) { batch(g, std::integral_constant<int, 4>()); g += 4; }
+    if constexpr (U >= 4) if (g + 2 <= g_end) { batch(g, std::integral_constant<int, 2>()); g += 2; }
+    if (g < g_end) batch(g, std::integral_constant<int, 1>());
     if (fold && lane < 16) {
 #pragma unroll
         for (int m = 0; m < M; m++)
@@ -246,29 +250,31 @@ __global__ __launch_bounds__(1024) void k_gemv_split(float *__restrict__ out, si
             }
         }
     };
-    int g = g_begin;
-    for (; g + U <= g_end; g += U) {
-        uint4 t[U];
-        int x4[U][M];
-        uint16_t wsr[U];
+    // Loads for a batch of B groups are issued before any is consumed; the
+    // range is covered by batches of U, then U/2, U/4, ... (all loads of a
+    // batch in flight together), so a wave's few groups never go one by one.
+    auto batch = [&](int g0, auto bsize) __attribute__((always_inline)) {
+        constexpr int B = decltype(bsize)::value;
+        uint4 t[B];
+        int x4[B][M];
+        uint16_t wsr[B];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            t[u] = tiles[(size_t)(g + u) * 64];
+        for (int u = 0; u < B; u++) {
+            t[u] = tiles[(size_t)(g0 + u) * 64];
 #pragma unroll
             for (int m = 0; m < M; m++)  // rows past `rows` reread the last row (unused)
-                x4[u][m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)(g + u) * 64) >> 2];
-            wsr[u] = wscale[(g + u) * 16];
+                x4[u][m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)(g0 + u) * 64) >> 2];
+            wsr[u] = wscale[(g0 + u) * 16];
         }
 #pragma unroll
-        for (int u = 0; u < U; u++) consume(g + u, t[u], x4[u], wsr[u]);
-    }
-    for (; g < g_end; g++) {
-        const uint4 t = tiles[(size_t)g * 64];
-        int x4[M];
-#pragma unroll
-        for (int m = 0; m < M; m++) x4[m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)g * 64) >> 2];
-        consume(g, t, x4, wscale[g * 16]);
-    }
+        for (int u = 0; u < B; u++) consume(g0 + u, t[u], x4[u], wsr[u]);
+    };
+    int g = g_begin;
+    for (; g + U <= g_end; g += U) batch(g, std::integral_constant<int, U>());
+    if constexpr (U >= 16) if (g + 8 <= g_end) { batch(g, std::integral_constant<int, 8>()); g += 8; }
+    if constexpr (U >= 8) if (g + 4 <= g_end) { batch(g, std::integral_constant<int, 4>()); g += 4; }
+    if constexpr (U >= 4) if (g + 2 <= g_end) { batch(g, std::integral_constant<int, 2>()); g += 2; }
+    if (g < g_end) batch(g, std::integral_constant<int, 1>());
     __syncthreads();
     const int tid = threadIdx.x;
     if (tid < 16 * M) {
