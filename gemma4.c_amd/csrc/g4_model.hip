@@ -295,11 +295,10 @@ static int init(const g4_tensor *records, int device) {
     G4_HIP(hipMalloc(&c.pos_dev, sizeof(int)));
     G4_HIP(hipHostMalloc((void **)&c.pos_pinned, sizeof(int), hipHostMallocDefault));
     // Split-K scratch for the widest few-row product (1536 x 12288), and the
-    // one-token attention scratch at full context (8 score rows plus the
-    // long-row softmax work, under 2 x 8 rows), so that a captured decode step
-    // never needs a larger buffer.
+    // one-token attention scratch at full context (8 score rows), so that a
+    // captured decode step never needs a larger buffer.
     G4_TRY(scratch_reserve((size_t)G4_VOCAB * (G4_HIDDEN / 64) * sizeof(int32_t),
-                           (size_t)G4_MAX_CONTEXT * 8 * sizeof(float) * 3));
+                           (size_t)G4_MAX_CONTEXT * 8 * sizeof(float)));
     G4_HIP(hipDeviceSynchronize());
     c.ready = true;
     return G4_OK;

@@ -159,30 +159,330 @@ __device__ __forceinline__ float block_advance(float s, float tb, int p0, uint64
     return s;
 }
 
-template <int NB>
-__device__ __forceinline__ float exact_sequential_sum(const float (&t)[NB]) {
-    float s = 0.0f;
+// ---------------------------------------------------------------------------
+// The same sequential sum over a whole row at once, with the binades
+// predicted.  NW waves of a block own 64 NW J consecutive terms, lane-major:
+// t[j] of thread T = 64 w + l is term k = J T + j.  A pass
+//  1. predicts every partial sum with a cheap fp32 prefix (thread-serial
+//     sums, then scans over lanes and waves; only its binade is used);
+//  2. marks as an event every step that is not a grid step under that
+//     prediction: the predicted binade changes, a tie, a softmax new maximum,
+//     a term or partial sum outside the normal range;
+//  3. takes R_k = rint(t_k / u), u from the predicted binade, for every
+//     other step, and the prefix sums of R within each run between events;
+//  4. lists the events in order in LDS: the run sum before each, its term,
+//     the binade predicted after it;
+//  5. resolves them in order.  Run i adds exactly d_i u_i when the exact sum
+//     is in the predicted binade at its start and stays in it (the add is
+//     then exact); the event is the plain fp32 step.  The chain is computed
+//     first and the checks afterwards, all runs at once.
+// Where a prediction was wrong a check fails.  s is exact at the start of the
+// first failing run.  A run that leaves its binade early is advanced exactly
+// up to the step that does, which is taken plainly; the next pass starts
+// there.  A pass resolves at most kEsumEvents events.  Terms must be >= 0 (a
+// NaN or inf term is an event, so it propagates as in the plain loop), s >= 0.
+constexpr int kEsumEvents = 63;  // the table's last lane holds the final run
+constexpr int kEsumMaxWaves = 16;
+struct EsumEvent {
+    int d;     // run sum (in the run's grid) before the event
+    float t;   // the event's term
+    int k;     // its index
+    int meta;  // bit 0: new maximum; bits 8..15: predicted biased exponent after it
+};
+struct EsumShared {  // one per block (per wave when NW = 1)
+    EsumEvent table[kEsumEvents];
+    float wave_a[kEsumMaxWaves], wave_b[kEsumMaxWaves];  // predicted map of each wave
+    int wave_seg[kEsumMaxWaves], wave_count[kEsumMaxWaves];
+    int last_d;
+    int found_k[kEsumMaxWaves], found_before[kEsumMaxWaves];
+    float found_t[kEsumMaxWaves];
+};
+
+__device__ __forceinline__ int biased_exponent(float x) {
+    return (int)((__float_as_uint(x) >> 23) & 0xff);
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_float(float x, float old) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_int(int x, int old) {
+    return __builtin_amdgcn_update_dpp(old, x, CTRL, ROW_MASK, 0xf, false);
+}
+
+// Inclusive scan of fp32 adds over the wave (any association: a prediction).
+__device__ __forceinline__ float wave_fadd_inclusive(float x) {
+    x += dpp_float<0x111, 0xf>(x, 0.0f);
+    x += dpp_float<0x112, 0xf>(x, 0.0f);
+    x += dpp_float<0x114, 0xf>(x, 0.0f);
+    x += dpp_float<0x118, 0xf>(x, 0.0f);
+    x += dpp_float<0x142, 0xa>(x, 0.0f);
+    x += dpp_float<0x143, 0xc>(x, 0.0f);
+    return x;
+}
+
+// Inclusive scan of affine maps x -> a x + b (lower lanes applied first).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void affine_step(float &a, float &b) {
+    const float pa = dpp_float<CTRL, ROW_MASK>(a, 1.0f), pb = dpp_float<CTRL, ROW_MASK>(b, 0.0f);
+    b = fmaf(pb, a, b);
+    a = pa * a;
+}
+__device__ __forceinline__ void wave_affine_inclusive(float &a, float &b) {
+    affine_step<0x111, 0xf>(a, b);
+    affine_step<0x112, 0xf>(a, b);
+    affine_step<0x114, 0xf>(a, b);
+    affine_step<0x118, 0xf>(a, b);
+    affine_step<0x142, 0xa>(a, b);
+    affine_step<0x143, 0xc>(a, b);
+}
+
+// Run sums saturate at kEsumCap (any sum that large already leaves a binade);
+// kEsumFlag marks "a run starts inside" in the segmented scan.
+constexpr int kEsumCap = 1 << 29, kEsumFlag = 1 << 30;
+__device__ __forceinline__ int segmented_join(int left, int x) {
+    return (x & kEsumFlag) ? x : ((left & kEsumFlag) | min(x + (left & (kEsumFlag - 1)), kEsumCap));
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int segmented_step(int x) {
+    return segmented_join(dpp_int<CTRL, ROW_MASK>(x, 0), x);
+}
+__device__ __forceinline__ int wave_segmented_inclusive(int x) {
+    x = segmented_step<0x111, 0xf>(x);
+    x = segmented_step<0x112, 0xf>(x);
+    x = segmented_step<0x114, 0xf>(x);
+    x = segmented_step<0x118, 0xf>(x);
+    x = segmented_step<0x142, 0xa>(x);
+    x = segmented_step<0x143, 0xc>(x);
+    return x;
+}
+
+template <int NW>
+__device__ __forceinline__ void esum_barrier() {
+    if constexpr (NW > 1) __syncthreads();
+}
+
+// One pass from term k0 with the exact sum s before it.  Returns true when
+// every term is summed (s is then the result); otherwise s and k0 are the
+// exact state the next pass starts from.  Every thread of the NW waves calls
+// it (all lanes active); s and k0 are the same in all of them.
+template <int NW, int J, bool SPECIAL>
+__device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0, EsumShared &sh) {
+    static_assert(NW >= 1 && NW <= kEsumMaxWaves && J <= 32, "esum shape");
+    constexpr int N = 64 * NW * J;
+    const int lane = threadIdx.x & 63, wave = NW > 1 ? (int)(threadIdx.x >> 6) : 0;
+    const int kb = (wave * 64 + lane) * J;
+    // 1. the predicted prefix before this thread's first term
+    float c;
+    {
+        float la = 1.0f, lb = 0.0f;
 #pragma unroll
-    for (int b = 0; b < NB; b++) s = block_advance(s, t[b], 0, 0);
+        for (int j = 0; j < J; j++) {
+            const bool act = kb + j >= k0, sp = SPECIAL && ((spec >> j) & 1);
+            if (SPECIAL) {
+                const float a = act && sp ? t[j] : 1.0f, b = act ? (sp ? 1.0f : t[j]) : 0.0f;
+                lb = fmaf(lb, a, b);
+                la *= a;
+            } else {
+                lb += act ? t[j] : 0.0f;
+            }
+        }
+        float x = s;  // the sum before this wave's first term
+        if (SPECIAL) {
+            wave_affine_inclusive(la, lb);
+            if constexpr (NW > 1) {
+                if (lane == 63) {
+                    sh.wave_a[wave] = la;
+                    sh.wave_b[wave] = lb;
+                }
+                esum_barrier<NW>();
+                for (int w = 0; w < wave; w++) x = fmaf(x, sh.wave_a[w], sh.wave_b[w]);
+            }
+            c = fmaf(x, dpp_float<0x138, 0xf>(la, 1.0f), dpp_float<0x138, 0xf>(lb, 0.0f));
+        } else {
+            lb = wave_fadd_inclusive(lb);
+            if constexpr (NW > 1) {
+                if (lane == 63) sh.wave_b[wave] = lb;
+                esum_barrier<NW>();
+                for (int w = 0; w < wave; w++) x += sh.wave_b[w];
+            }
+            c = x + dpp_float<0x138, 0xf>(lb, 0.0f);
+        }
+    }
+    // 2. events, grid steps and this thread's run sums
+    int P[J];
+    uint32_t evbits = 0;
+    {
+        float A = c;
+        int run = 0;
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const bool act = kb + j >= k0, sp = SPECIAL && ((spec >> j) & 1);
+            const float prev = A;
+            if (act) A = sp ? fmaf(A, t[j], 1.0f) : A + t[j];
+            const int ep = biased_exponent(prev), ec = biased_exponent(A);
+            const float T = fminf(ldexpf(t[j], 150 - ep), 16777216.0f);
+            const float R = rintf(T);  // nearest, ties to even
+            const bool ev = act && (sp || ep != ec || (unsigned)(ep - 27) > 200u ||
+                                    fabsf(T - R) == 0.5f || !(t[j] <= 3.40282347e38f));
+            run = ev ? 0 : min(run + (act ? (int)R : 0), kEsumCap);
+            P[j] = run;
+            evbits |= (uint32_t)ev << j;
+        }
+    }
+    // 3. run sums across threads, event numbering
+    const int seg = wave_segmented_inclusive((evbits ? kEsumFlag : 0) | P[J - 1]);
+    int carry = dpp_int<0x138, 0xf>(seg, 0);  // through the previous thread, flagged if a run starts
+    const int count = __popc(evbits), numbered = wave_add_scan(count);
+    int idx = numbered - count, total;
+    if constexpr (NW > 1) {
+        if (lane == 63) {
+            sh.wave_seg[wave] = seg;
+            sh.wave_count[wave] = numbered;
+        }
+        esum_barrier<NW>();
+        int incoming = 0;
+        total = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            if (w < wave) {
+                incoming = segmented_join(incoming, sh.wave_seg[w]);
+                idx += sh.wave_count[w];
+            }
+            total += sh.wave_count[w];
+        }
+        carry = segmented_join(incoming, carry);
+    } else {
+        total = __builtin_amdgcn_readlane(numbered, 63);
+    }
+    carry &= kEsumFlag - 1;
+    // 4. the event table; P becomes the run sum through each term
+    {
+        float A = c;
+        int before = carry;
+        bool open = true;  // no event yet in this thread: the carry continues its run
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const bool act = kb + j >= k0, sp = SPECIAL && ((spec >> j) & 1);
+            if (act) A = sp ? fmaf(A, t[j], 1.0f) : A + t[j];
+            if ((evbits >> j) & 1) {
+                if (idx < kEsumEvents)
+                    sh.table[idx] = EsumEvent{before, t[j], kb + j, (int)sp | biased_exponent(A) << 8};
+                idx++;
+                open = false;
+            }
+            if (open) P[j] = min(P[j] + carry, kEsumCap);
+            before = P[j];
+        }
+        if (wave == NW - 1 && lane == 63) sh.last_d = P[J - 1];
+    }
+    esum_barrier<NW>();
+    // 5. resolve: entry i (lane i) is the run before event i and the event; the
+    // final run is one more entry, with no step
+    const bool more = total > kEsumEvents;
+    const int events = more ? kEsumEvents : total, entries = more ? events : events + 1;
+    const EsumEvent e = lane < events ? sh.table[lane] : EsumEvent{sh.last_d, 0.0f, N, 0};
+    const int prev_meta = dpp_int<0x138, 0xf>(e.meta, 0), prev_k = dpp_int<0x138, 0xf>(e.k, 0);
+    const int e_run = lane == 0 ? biased_exponent(s) : (prev_meta >> 8) & 0xff;
+    const int start = lane == 0 ? k0 : prev_k + 1;
+    const bool nonempty = e.k > start;
+    const float du = nonempty ? ldexpf((float)e.d, e_run - 150) : 0.0f;
+    const bool sp = e.meta & 1;
+    const float fa = sp ? e.t : 1.0f, fb = sp ? 1.0f : e.t;
+    float sv = s, at_start = 0.0f, at_end = 0.0f;
+    for (int i = 0; i < entries; i++) {
+        at_start = lane == i ? sv : at_start;
+        sv += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(du), i));
+        at_end = lane == i ? sv : at_end;
+        sv = sv * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fa), i)) +
+             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fb), i));  // two roundings
+    }
+    const int e0 = biased_exponent(at_start), e1 = biased_exponent(at_end);
+    const uint64_t bad = __ballot(lane < entries && nonempty &&
+                                  (e0 != e_run || (unsigned)(e0 - 27) > 200u || e1 != e_run));
+    if (!bad) {
+        s = sv;
+        if (more) {
+            k0 = __builtin_amdgcn_readlane(e.k, entries - 1) + 1;
+            return false;
+        }
+        k0 = N;
+        return true;
+    }
+    const int i = (int)__builtin_ctzll(bad);
+    const float sb = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(at_start), i));
+    const int st = __builtin_amdgcn_readlane(start, i), kend = __builtin_amdgcn_readlane(e.k, i);
+    const int eb = biased_exponent(sb);
+    if (eb != __builtin_amdgcn_readlane(e_run, i) || (unsigned)(eb - 27) > 200u) {
+        s = sb;  // the predicted binade was wrong: start over from this run
+        k0 = st;
+        return false;
+    }
+    // the run leaves its binade early: find the first step that does
+    const int S = (int)ldexpf(sb, 150 - eb);  // in [2^23, 2^24)
+    int found = J, before_found = 0, prevP = carry;
+    float t_found = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int k = kb + j;
+        if (found == J && k >= st && k < kend && S + P[j] >= (1 << 24)) {
+            found = j;
+            before_found = prevP;
+            t_found = t[j];
+        }
+        prevP = P[j];
+    }
+    const uint64_t hit = __ballot(found < J);
+    int kf = N, bf = 0;
+    float tf = 0.0f;
+    if (hit) {
+        const int L = (int)__builtin_ctzll(hit);
+        kf = (wave * 64 + L) * J + __builtin_amdgcn_readlane(found, L);
+        bf = __builtin_amdgcn_readlane(before_found, L);
+        tf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t_found), L));
+    }
+    if constexpr (NW > 1) {
+        if (lane == 0) {
+            sh.found_k[wave] = kf;
+            sh.found_before[wave] = bf;
+            sh.found_t[wave] = tf;
+        }
+        esum_barrier<NW>();
+        kf = N;
+#pragma unroll
+        for (int w = NW - 1; w >= 0; w--) {
+            if (sh.found_k[w] < N) {
+                kf = sh.found_k[w];
+                bf = sh.found_before[w];
+                tf = sh.found_t[w];
+            }
+        }
+        esum_barrier<NW>();  // the slots are free for the next pass's search
+    }
+    s = ldexpf((float)(S + bf), eb - 150) + tf;
+    k0 = kf + 1;
+    return false;
+}
+
+// The sequential sum s_init + t_0 + ... (or, for flagged terms, s = s t + 1)
+// of the block's 64 NW J terms, lane-major.  Every thread of the NW waves
+// calls it; all get the result.
+template <int NW, int J, bool SPECIAL>
+__device__ __forceinline__ float exact_sum_events(const float (&t)[J], uint32_t spec, float s,
+                                                  EsumShared &sh) {
+    int k0 = 0;
+    while (!esum_pass<NW, J, SPECIAL>(t, spec, s, k0, sh)) {
+    }
     return s;
 }
 
-// The sum of squares of a row of 256 V held as xv[v] = elements 256 v +
-// 4 lane .. + 3, through exact_sequential_sum: the row is re-read block-major
-// from this wave's LDS row buffer (W floats), the squares recomputed there.
-template <int V>
-__device__ __forceinline__ float row_sum_squares_fast(const float4 (&xv)[V], float *lds_row) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int v = 0; v < V; v++) reinterpret_cast<float4 *>(lds_row)[v * 64 + lane] = xv[v];
-    // (a wave's LDS accesses complete in order: no barrier, the compiler waits)
-    float t[4 * V];
-#pragma unroll
-    for (int b = 0; b < 4 * V; b++) {
-        const float x = lds_row[64 * b + lane];
-        t[b] = x * x;
-    }
-    return exact_sequential_sum<4 * V>(t);
+// The sum of squares of a row of 1536 held one float4 per thread of a
+// 384-thread block (thread T: elements 4 T .. 4 T + 3), in index order.
+__device__ __forceinline__ float row_sum_squares_block(float4 x, EsumShared &sh) {
+    const float t[4] = {x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w};
+    return exact_sum_events<6, 4, false>(t, 0u, 0.0f, sh);
 }
 
 // The reference's sequential sum of squares (gemma4.c:366-368) of a row held
@@ -214,17 +514,14 @@ __device__ __forceinline__ float row_sum_squares(const float4 (&xv)[V]) {
     return sum;
 }
 
-// Widths 256 * V (V = 1, 2, 6: per-head norms of 256 and 512, and the
-// hidden 1536).  Every lane holds its 4V values and weights in registers
-// (loaded once, all loads in flight); the sum is row_sum_squares.
+// Widths 256 * V (V = 1, 2: per-head norms of 256 and 512).  Every lane
+// holds its 4V values and weights in registers (loaded once, all loads in
+// flight); the sum is row_sum_squares.
 template <int V>
 __global__ __launch_bounds__(256) void k_rmsnorm_reference_v(float *out, const float *in,
                                                              const float *__restrict__ weight,
                                                              float eps, size_t rows) {
     constexpr int W = 256 * V;
-    // rows of 1536: the exact parallel sum (LDS transpose buffer per wave);
-    // shorter rows: the readlane chain
-    __shared__ __attribute__((aligned(16))) float s_rows[V == 6 ? 4 : 1][V == 6 ? W : 4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t wave_row = (size_t)blockIdx.x * 4 + wave;
     if (wave_row >= rows) return;  // uniform per wave; no block-level barrier follows
@@ -240,12 +537,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reference_v(float *out, const f
 #pragma unroll
         for (int v = 0; v < V; v++) wv[v] = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
-    float sum;
-    if constexpr (V == 6)
-        sum = row_sum_squares_fast<V>(xv, s_rows[wave]);
-    else
-        sum = row_sum_squares<V>(xv);
-    const float inverse = 1.0f / sqrtf(sum / (float)W + eps);
+    const float inverse = 1.0f / sqrtf(row_sum_squares<V>(xv) / (float)W + eps);
     float4 *y4 = reinterpret_cast<float4 *>(out + wave_row * W);
 #pragma unroll
     for (int v = 0; v < V; v++)
@@ -253,95 +545,71 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reference_v(float *out, const f
                                         wv[v].z * (inverse * xv[v].z), wv[v].w * (inverse * xv[v].w));
 }
 
-// The row-local tail of a sublayer, fused for hidden rows of 1536 (one wave
-// per row, values in registers), reference order throughout:
+__device__ __forceinline__ float4 scale_by(float4 w, float inverse, float4 x) {
+    return make_float4(w.x * (inverse * x.x), w.y * (inverse * x.y), w.z * (inverse * x.z),
+                       w.w * (inverse * x.w));
+}
+
+// Rows of 1536 (the hidden width): one row per 384-thread block, one float4
+// per thread, the sum through row_sum_squares_block.
+__global__ __launch_bounds__(384) void k_rmsnorm_1536(float *out, const float *in,
+                                                      const float *__restrict__ weight, float eps) {
+    __shared__ EsumShared sh;
+    const int T = threadIdx.x;
+    const size_t row = blockIdx.x;
+    const float4 x = reinterpret_cast<const float4 *>(in + row * 1536)[T];
+    const float4 w = weight ? reinterpret_cast<const float4 *>(weight)[T] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    const float inverse = 1.0f / sqrtf(row_sum_squares_block(x, sh) / 1536.0f + eps);
+    reinterpret_cast<float4 *>(out + row * 1536)[T] = scale_by(w, inverse, x);
+}
+
+// The row-local tail of a sublayer, fused for hidden rows of 1536 (one row
+// per 384-thread block, one float4 per thread), reference order throughout:
 //   a = NORM_IN ? rmsnorm(h, w_in) : h                 (gemma4.c:360-373)
 //   if ADD:  residual = (residual + a) * scale         (gemma4.c:375-378)
 //   b = NORM_OUT ? rmsnorm(residual, w_out) : residual
 //   if QUANT: q8, qs = quantize(b)                     (gemma4.c:265-279)
 //   if y:     y = b
 // It replaces, e.g., rmsnorm + add_and_scale + rmsnorm + quantize between two
-// matmuls by one launch.  In-place use (y == h or y == residual) is allowed.
+// matmuls by one launch.  In-place use (y == h or y == residual) is allowed:
+// each thread reads only the elements it writes.
 template <bool NORM_IN, bool ADD, bool NORM_OUT, bool QUANT>
-__global__ __launch_bounds__(256) void k_row_tail(const float *h, const float *__restrict__ w_in,
+__global__ __launch_bounds__(384) void k_row_tail(const float *h, const float *__restrict__ w_in,
                                                   float *residual, float scale,
                                                   const float *__restrict__ w_out, float *y,
                                                   int8_t *__restrict__ q8, float *__restrict__ qs,
-                                                  float eps, size_t rows) {
-    constexpr int V = 6, W = 1536;
-    __shared__ __attribute__((aligned(16))) float s_rows[4][W];  // per-wave transpose buffer
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const size_t row = (size_t)blockIdx.x * 4 + wave;
-    if (row >= rows) return;  // uniform per wave; no barrier follows
-    float4 rv[V], wiv[V], wov[V];
-    const float4 *r4 = reinterpret_cast<const float4 *>(residual + row * W);
-#pragma unroll
-    for (int v = 0; v < V; v++) rv[v] = r4[v * 64 + lane];
+                                                  float eps) {
+    constexpr int W = 1536;
+    __shared__ EsumShared sh;
+    const int T = threadIdx.x, lane = T & 63;
+    const size_t row = blockIdx.x;
+    float4 r = reinterpret_cast<const float4 *>(residual + row * W)[T];
+    float4 wi, wo;
     // weights first: their loads overlap the sums instead of following them
-    if (NORM_IN) {
-        const float4 *w4 = reinterpret_cast<const float4 *>(w_in);
-#pragma unroll
-        for (int v = 0; v < V; v++) wiv[v] = w4[v * 64 + lane];
-    }
-    if (NORM_OUT) {
-        const float4 *w4 = reinterpret_cast<const float4 *>(w_out);
-#pragma unroll
-        for (int v = 0; v < V; v++) wov[v] = w4[v * 64 + lane];
-    }
+    if (NORM_IN) wi = reinterpret_cast<const float4 *>(w_in)[T];
+    if (NORM_OUT) wo = reinterpret_cast<const float4 *>(w_out)[T];
     if (ADD) {
-        float4 hv[V];
-        const float4 *h4 = reinterpret_cast<const float4 *>(h + row * W);
-#pragma unroll
-        for (int v = 0; v < V; v++) hv[v] = h4[v * 64 + lane];
-        if (NORM_IN) {
-            const float inverse = 1.0f / sqrtf(row_sum_squares_fast<V>(hv, s_rows[wave]) / (float)W + eps);
-#pragma unroll
-            for (int v = 0; v < V; v++) {
-                const float4 wv = wiv[v];
-                hv[v] = make_float4(wv.x * (inverse * hv[v].x), wv.y * (inverse * hv[v].y),
-                                    wv.z * (inverse * hv[v].z), wv.w * (inverse * hv[v].w));
-            }
-        }
-        float4 *rw = reinterpret_cast<float4 *>(residual + row * W);
-#pragma unroll
-        for (int v = 0; v < V; v++) {
-            rv[v] = make_float4((rv[v].x + hv[v].x) * scale, (rv[v].y + hv[v].y) * scale,
-                                (rv[v].z + hv[v].z) * scale, (rv[v].w + hv[v].w) * scale);
-            rw[v * 64 + lane] = rv[v];
-        }
+        float4 a = reinterpret_cast<const float4 *>(h + row * W)[T];
+        if (NORM_IN) a = scale_by(wi, 1.0f / sqrtf(row_sum_squares_block(a, sh) / (float)W + eps), a);
+        r = make_float4((r.x + a.x) * scale, (r.y + a.y) * scale, (r.z + a.z) * scale, (r.w + a.w) * scale);
+        reinterpret_cast<float4 *>(residual + row * W)[T] = r;
     }
-    if (NORM_OUT) {
-        const float inverse = 1.0f / sqrtf(row_sum_squares_fast<V>(rv, s_rows[wave]) / (float)W + eps);
-#pragma unroll
-        for (int v = 0; v < V; v++) {
-            const float4 wv = wov[v];
-            rv[v] = make_float4(wv.x * (inverse * rv[v].x), wv.y * (inverse * rv[v].y),
-                                wv.z * (inverse * rv[v].z), wv.w * (inverse * rv[v].w));
-        }
-    }
-    if (y) {
-        float4 *y4 = reinterpret_cast<float4 *>(y + row * W);
-#pragma unroll
-        for (int v = 0; v < V; v++) y4[v * 64 + lane] = rv[v];
-    }
+    if (NORM_OUT) r = scale_by(wo, 1.0f / sqrtf(row_sum_squares_block(r, sh) / (float)W + eps), r);
+    if (y) reinterpret_cast<float4 *>(y + row * W)[T] = r;
     if (QUANT) {
-        // group 4v + lane/16 is the 16 lanes of one DPP row: absmax across them
+        // group T / 16 is the 16 lanes of one DPP row: absmax across them
+        float m = fmaxf(fmaxf(fabsf(r.x), fabsf(r.y)), fmaxf(fabsf(r.z), fabsf(r.w)));
 #pragma unroll
-        for (int v = 0; v < V; v++) {
-            const float4 x = rv[v];
-            float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
-#pragma unroll
-            for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
-            const float gscale = m / 127.0f;
-            const float inverse = gscale > 0.0f ? 1.0f / gscale : 0.0f;
-            char4 out;
-            out.x = (signed char)(int)rintf(x.x * inverse);
-            out.y = (signed char)(int)rintf(x.y * inverse);
-            out.z = (signed char)(int)rintf(x.z * inverse);
-            out.w = (signed char)(int)rintf(x.w * inverse);
-            reinterpret_cast<char4 *>(q8 + row * W)[v * 64 + lane] = out;
-            if ((lane & 15) == 0) qs[row * (W / 64) + 4 * v + (lane >> 4)] = gscale;
-        }
+        for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+        const float gscale = m / 127.0f;
+        const float inverse = gscale > 0.0f ? 1.0f / gscale : 0.0f;
+        char4 out;
+        out.x = (signed char)(int)rintf(r.x * inverse);
+        out.y = (signed char)(int)rintf(r.y * inverse);
+        out.z = (signed char)(int)rintf(r.z * inverse);
+        out.w = (signed char)(int)rintf(r.w * inverse);
+        reinterpret_cast<char4 *>(q8 + row * W)[T] = out;
+        if ((lane & 15) == 0) qs[row * (W / 64) + T / 16] = gscale;
     }
 }
 
@@ -349,11 +617,11 @@ void launch_row_tail(hipStream_t s, const float *h, const float *w_in, float *re
                      const float *w_out, float *y, int8_t *q8, float *qs, float eps, size_t rows,
                      int norm_in, int add, int norm_out, int quant) {
     if (!rows) return;
-    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    const dim3 grid((unsigned)rows), block(384);
 #define G4_TAIL(A, B, C, D)                                                                    \
     if (norm_in == A && add == B && norm_out == C && quant == D) {                             \
         hipLaunchKernelGGL((k_row_tail<A, B, C, D>), grid, block, 0, s, h, w_in, residual, scale, \
-                           w_out, y, q8, qs, eps, rows);                                       \
+                           w_out, y, q8, qs, eps);                                       \
         return;                                                                                \
     }
     G4_TAIL(true, true, true, true)     // post-norm, residual add, pre-norm, quantize
@@ -401,7 +669,7 @@ void launch_rmsnorm_reference(hipStream_t s, float *out, const float *in, const 
     const bool aligned = ((uintptr_t)in % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
                          ((uintptr_t)weight % 16 == 0);
     if (aligned && width == 1536)
-        hipLaunchKernelGGL(k_rmsnorm_reference_v<6>, grid, block, 0, s, out, in, weight, eps, rows);
+        hipLaunchKernelGGL(k_rmsnorm_1536, dim3((unsigned)rows), dim3(384), 0, s, out, in, weight, eps);
     else if (aligned && width == 512)
         hipLaunchKernelGGL(k_rmsnorm_reference_v<2>, grid, block, 0, s, out, in, weight, eps, rows);
     else if (aligned && width == 256)
@@ -571,17 +839,17 @@ __device__ void softmax_row_reference(float *v, int count) {
 }
 
 // ---------------------------------------------------------------------------
-// Long rows (deep-context decode): the same arithmetic in five passes, so
-// that only the running sum is sequential.
-//   1. the maximum of every 64-value block;
-//   2. per row, the exclusive prefix maximum over blocks;
-//   3. every term in parallel: before_i = max(v_0 .. v_{i-1}), a new maximum
-//      when v_i > before_i, e_i = expf(before_i - v_i) then, else
-//      expf(v_i - before_i) (v_0 is the starting maximum, not a term);
-//   4. one wave per row runs the reference's running sum over the e_i in
-//      order (sum = sum * e + 1 at a new maximum, else sum += e);
-//   5. v_i = expf(v_i - max) / sum in parallel.
-// Each value of the result equals the one-wave kernel's bit for bit.
+// Long rows (deep-context decode, few rows): one block of NW waves per row,
+// in chunks of 64 NW J values, thread T holding values J T .. J T + J - 1 of
+// the chunk.  Per chunk:
+//   before_i = max(v_0 .. v_{i-1}) (thread-serial, then across lanes and
+//   waves, and the maximum of the earlier chunks); a new maximum when
+//   v_i > before_i, e_i = expf(before_i - v_i) then, else expf(v_i - before_i)
+//   (v_0 is the starting maximum, not a term);
+//   the reference's running sum over the e_i in order (sum = sum * e + 1 at a
+//   new maximum, else sum += e) through exact_sum_events.
+// Then v_i = expf(v_i - max) / sum.  Each value of the result equals the
+// one-wave kernel's bit for bit.
 
 // Which values a row holds: a fixed count, or an attention row (t, head)
 // whose visible keys follow from the position.
@@ -595,122 +863,62 @@ struct SoftmaxRows {
     }
 };
 
-__global__ __launch_bounds__(256) void k_lsm_blockmax(const float *__restrict__ v, size_t stride,
-                                                      SoftmaxRows spec, float *__restrict__ bmax,
-                                                      int nbs) {
-    const int row = blockIdx.y, lane = threadIdx.x & 63;
-    const int b = blockIdx.x * 4 + (threadIdx.x >> 6), count = spec.count(row);
-    if (b * 64 >= count) return;
-    const int i = b * 64 + lane;
-    const float x = i < count ? v[(size_t)row * stride + i] : -INFINITY;
-    const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_max_scan(x)), 63));
-    if (lane == 0) bmax[(size_t)row * nbs + b] = m;
-}
-
-__global__ __launch_bounds__(64) void k_lsm_prefix(SoftmaxRows spec, const float *__restrict__ bmax,
-                                                   float *__restrict__ pmax, float *__restrict__ info,
-                                                   int nbs) {
-    const int row = blockIdx.x, lane = threadIdx.x;
-    const int nb = (spec.count(row) + 63) / 64;
-    float carry = -INFINITY;
-    for (int i0 = 0; i0 < nb; i0 += 64) {
-        const int b = i0 + lane;
-        const float x = b < nb ? bmax[(size_t)row * nbs + b] : -INFINITY;
-        const float incl = fmaxf(wave_max_scan(x), carry);
-        const float shifted = wave_shr1(incl);
-        if (b < nb) pmax[(size_t)row * nbs + b] = lane == 0 ? carry : shifted;
-        carry = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), 63));
-    }
-    if (lane == 0) info[2 * row] = carry;  // the row's maximum
-}
-
-__global__ __launch_bounds__(256) void k_lsm_terms(const float *__restrict__ v, size_t stride,
-                                                   SoftmaxRows spec, const float *__restrict__ pmax,
-                                                   float *__restrict__ terms,
-                                                   uint64_t *__restrict__ new_masks, int nbs) {
-    const size_t tstride = (size_t)nbs * 64;  // terms rows: whole blocks
-    const int row = blockIdx.y, lane = threadIdx.x & 63;
-    const int b = blockIdx.x * 4 + (threadIdx.x >> 6), count = spec.count(row);
-    if (b * 64 >= count) return;
-    const int i = b * 64 + lane;
-    const float x = i < count ? v[(size_t)row * stride + i] : -INFINITY;
-    const float carry = pmax[(size_t)row * nbs + b];
-    const float incl = fmaxf(wave_max_scan(x), carry);
-    const float shifted = wave_shr1(incl);
-    const float before = lane == 0 ? carry : shifted;
-    bool is_new = x > before;
-    float e = is_new ? expf_libm(before - x) : expf_libm(x - before);
-    if (i == 0) {  // v_0 starts the running maximum (gemma4.c:401)
-        is_new = false;
-        e = 0.0f;
-    }
-    // past the end: x = -inf, so e = 0, which leaves the positive sum unchanged
-    terms[(size_t)row * tstride + i] = e;
-    const uint64_t mask = __ballot(is_new);
-    if (lane == 0) new_masks[(size_t)row * nbs + b] = mask;
-}
-
-__global__ __launch_bounds__(64) void k_lsm_chain(SoftmaxRows spec, const float *__restrict__ terms,
-                                                  const uint64_t *__restrict__ new_masks,
-                                                  float *__restrict__ info, int nbs) {
-    constexpr int R = 8;  // blocks of terms in flight ahead of the chain
-    const int row = blockIdx.x, lane = threadIdx.x;
-    const int nb = (spec.count(row) + 63) / 64;
-    const float *t = terms + (size_t)row * nbs * 64 + lane;
-    const uint64_t *nm = new_masks + (size_t)row * nbs;
-    float ring[R];
+template <int NW, int J>
+__global__ __launch_bounds__(64 * NW) void k_softmax_block(float *__restrict__ v, size_t stride,
+                                                           SoftmaxRows spec) {
+    constexpr int C = 64 * NW * J;
+    __shared__ EsumShared sh;
+    __shared__ float s_max[NW];
+    const int row = blockIdx.x, count = spec.count(row);
+    const int T = threadIdx.x, lane = T & 63, wave = T >> 6;
+    float *x = v + (size_t)row * stride;
+    float run_max = x[0], sum = 1.0f;  // gemma4.c:401
+    for (int base = 0; base < count; base += C) {
+        float val[J];
 #pragma unroll
-    for (int s = 0; s < R; s++) ring[s] = t[(size_t)min(s, nb - 1) * 64];
-    uint64_t masks = 0;  // lane j: new-maximum mask of block (b & ~63) + j
-    float sum = 1.0f;
-    for (int b0 = 0; b0 < nb; b0 += R) {
-        if ((b0 & 63) == 0) masks = nm[min(b0 + lane, nb - 1)];
-#pragma unroll
-        for (int s = 0; s < R; s++) {
-            const int b = b0 + s;
-            const float e = ring[s];
-            ring[s] = t[(size_t)min(b + R, nb - 1) * 64];  // unconditional refill
-            if (b < nb) {
-                const int j = b & 63;
-                const uint64_t mask =
-                    ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(masks >> 32), j) << 32) |
-                    (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)masks, j);
-                sum = block_advance(sum, e, 0, mask);  // exact, in order
-            }
+        for (int j = 0; j < J; j++) {
+            const int i = base + J * T + j;
+            val[j] = i > 0 && i < count ? x[i] : -INFINITY;  // -inf: a zero term
         }
+        float m = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < J; j++) m = fmaxf(m, val[j]);
+        const float incl = wave_max_scan(m);
+        if (lane == 63) s_max[wave] = incl;
+        __syncthreads();
+        float before = run_max, chunk_max = run_max;
+        for (int w = 0; w < NW; w++) {
+            if (w < wave) before = fmaxf(before, s_max[w]);
+            chunk_max = fmaxf(chunk_max, s_max[w]);
+        }
+        before = fmaxf(before, dpp_float<0x138, 0xf>(incl, -INFINITY));  // lanes below
+        float t[J];
+        uint32_t fresh = 0;
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const bool is_new = val[j] > before;
+            t[j] = is_new ? expf_libm(before - val[j]) : expf_libm(val[j] - before);
+            fresh |= (uint32_t)is_new << j;
+            before = fmaxf(before, val[j]);
+        }
+        // (the engine's barriers also order these s_max reads before the next
+        // chunk's writes)
+        sum = exact_sum_events<NW, J, true>(t, fresh, sum, sh);
+        run_max = chunk_max;
     }
-    if (lane == 0) info[2 * row + 1] = sum;
+    for (int i = T; i < count; i += 64 * NW) x[i] = expf_libm(x[i] - run_max) / sum;
 }
 
-__global__ __launch_bounds__(256) void k_lsm_normalize(float *__restrict__ v, size_t stride,
-                                                       SoftmaxRows spec,
-                                                       const float *__restrict__ info) {
-    const int row = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= spec.count(row)) return;
-    float *x = v + (size_t)row * stride + i;
-    *x = expf_libm(*x - info[2 * row]) / info[2 * row + 1];
-}
-
-// Scratch floats the long-row path needs for rows of at most max_count values.
-static size_t long_softmax_floats(size_t rows, size_t max_count) {
-    const size_t nbs = (max_count + 63) / 64;
-    return rows * (nbs * 64 + 2 * nbs + 2 * nbs + 2);  // terms, bmax, pmax, masks (2 floats each), info
-}
-
-// Rows of v at `stride` floats, each at most max_count values long.
-static void launch_softmax_long(hipStream_t s, float *v, size_t stride, int max_count,
-                                SoftmaxRows spec, unsigned rows, float *work) {
-    const int nbs = (max_count + 63) / 64;
-    float *terms = work, *bmax = terms + (size_t)rows * nbs * 64, *pmax = bmax + (size_t)rows * nbs;
-    uint64_t *masks = reinterpret_cast<uint64_t *>(pmax + (size_t)rows * nbs);
-    float *info = reinterpret_cast<float *>(masks + (size_t)rows * nbs);
-    const dim3 blocks((unsigned)((nbs + 3) / 4), rows);
-    hipLaunchKernelGGL(k_lsm_blockmax, blocks, dim3(256), 0, s, v, stride, spec, bmax, nbs);
-    hipLaunchKernelGGL(k_lsm_prefix, dim3(rows), dim3(64), 0, s, spec, bmax, pmax, info, nbs);
-    hipLaunchKernelGGL(k_lsm_terms, blocks, dim3(256), 0, s, v, stride, spec, pmax, terms, masks, nbs);
-    hipLaunchKernelGGL(k_lsm_chain, dim3(rows), dim3(64), 0, s, spec, terms, masks, info, nbs);
-    hipLaunchKernelGGL(k_lsm_normalize, dim3((unsigned)((nbs * 64 + 255) / 256), rows), dim3(256), 0,
-                       s, v, stride, spec, info);
+// Softmax of `rows` rows (attention rows (t, head) or rows of a fixed count)
+// with at most max_count values, one block per row.
+static void launch_softmax_block(hipStream_t s, float *v, size_t stride, int max_count,
+                                 SoftmaxRows spec, unsigned rows) {
+    if (max_count <= 512)
+        hipLaunchKernelGGL((k_softmax_block<8, 1>), dim3(rows), dim3(512), 0, s, v, stride, spec);
+    else if (max_count <= 4096)
+        hipLaunchKernelGGL((k_softmax_block<16, 4>), dim3(rows), dim3(1024), 0, s, v, stride, spec);
+    else
+        hipLaunchKernelGGL((k_softmax_block<16, 16>), dim3(rows), dim3(1024), 0, s, v, stride, spec);
 }
 
 // Attention probabilities of every (token, head) row, one wave each.
@@ -969,11 +1177,8 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
     const int max_keys = pos_dev ? (full ? G4_MAX_CONTEXT : G4_WINDOW)
                                  : full ? last_pos + 1 : (last_pos + 1 < G4_WINDOW ? last_pos + 1 : G4_WINDOW);
     const size_t stride = ((size_t)max_keys + 63) & ~(size_t)63;
-    // few rows of many keys (deep-context decode): the five-pass softmax
-    const bool long_rows = n <= 4 && max_keys > 1024;
     const size_t score_floats = n * heads * stride;
-    const size_t work_floats = long_rows ? long_softmax_floats(n * heads, max_keys) : 0;
-    int rc = scratch_reserve(0, (score_floats + work_floats) * sizeof(float));
+    int rc = scratch_reserve(0, score_floats * sizeof(float));
     if (rc) return rc;
     float *scores = scratch().attn;
     // key blocks spanned by one block of tokens: its first token's window
@@ -998,10 +1203,9 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
         hipLaunchKernelGGL((k_attn_scores<512, TQ>), grid, dim3(256), 0, s, q, key_cache, cache_len,
                            full, start_pos, (int)n, pos_dev, stride, scores);
     }
-    if (long_rows) {
+    if (n <= 4) {  // decode: few rows, a block per row
         const SoftmaxRows spec{heads, full, start_pos, 0, pos_dev};
-        launch_softmax_long(s, scores, stride, max_keys, spec, (unsigned)(n * heads),
-                            scores + score_floats);
+        launch_softmax_block(s, scores, stride, max_keys, spec, (unsigned)(n * heads));
     } else {
         hipLaunchKernelGGL(k_attn_softmax_reference, dim3((unsigned)heads, nn), dim3(64), 0, s,
                            scores, heads, full, start_pos, pos_dev, stride);
@@ -1053,12 +1257,10 @@ extern "C" int g4_set_order(int order) {
 extern "C" int g4_softmax(void *stream, float *values, int count, size_t rows) {
     G4_CHECK(values && count > 0, "g4_softmax: bad arguments");
     if (!rows) return G4_OK;
-    if (count > 1024 && rows <= 64) {  // few long rows: the five-pass path
-        const int rc = g4::scratch_reserve(0, g4::long_softmax_floats(rows, count) * sizeof(float));
-        if (rc) return rc;
+    if (count > 1024 && rows <= 64) {  // few long rows: a block per row
         const g4::SoftmaxRows spec{1, 1, 0, count, nullptr};
-        g4::launch_softmax_long((hipStream_t)stream, values, (size_t)count, count, spec,
-                                (unsigned)rows, g4::scratch().attn);
+        g4::launch_softmax_block((hipStream_t)stream, values, (size_t)count, count, spec,
+                                 (unsigned)rows);
     } else {
         hipLaunchKernelGGL(g4::k_softmax_rows, dim3((unsigned)rows), dim3(64), 0, (hipStream_t)stream,
                            values, count, (size_t)count);

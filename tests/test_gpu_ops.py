@@ -205,6 +205,12 @@ def test_softmax_bitexact(pkg, g4lib, torch_gpu, ok):
         (g.standard_normal(4096) * 200).astype(np.float32),
         np.array([0.0], np.float32),
         (g.uniform(-1e-3, 1e-3, 65)).astype(np.float32),
+        # long rows (a block per row, in chunks of 16384 values): three chunks,
+        # a new maximum at every one of 5000 steps, a long falling row
+        (g.standard_normal(40000) * 8).astype(np.float32),
+        np.linspace(-30, 30, 5000).astype(np.float32),
+        np.linspace(30, -30, 20000).astype(np.float32),
+        np.full(1500, -2.0, np.float32),
     ]
     for v in rows:
         d = dev(torch, v)
