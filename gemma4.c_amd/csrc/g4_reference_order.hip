@@ -1059,110 +1059,140 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
     }
 }
 
-// P.V for one token per block (decode): wave h runs the 64 chains of head
-// h over a 64-channel slice, one chain per lane, keys in order.  The 8 heads
-// share each 64-key tile of V, staged in LDS row-major ([key][channel]: a
-// lane reads its channel of key k with a 4-byte load) beside the 8 heads'
-// probabilities (read as broadcasts).  Tiles are prefetched DEPTH ahead in
-// registers with unconditional loads and stored into a double-buffered LDS
-// slot, one barrier per tile; each lane's chain is then 64 dependent fmas per
-// tile with nothing else on its critical path.
+// P.V for one token (decode): one wave per block, four heads per wave.  Lane
+// 16 r + j runs the fma chain of head 4 g + r over channel c0 + j (block
+// (c0 / 16, g, token)), keys in order (gemma4.c:296-307).  Per 64-key tile
+// the wave stages V[64 keys][16 channels] in its own LDS, transposed to
+// [channel][key], so a lane reads four keys of its channel with one 16-byte
+// load; the four heads share it (the four lanes of a channel read the same
+// address).  Lane 16 r + j holds head 4 g + r's probabilities of keys
+// 4 j .. 4 j + 3 (one 16-byte load); key 4 J + e reaches every lane of row r
+// as the DPP source of its fma (component e, row_newbcast:J).  Per key a wave
+// spends one fma and a quarter of a 16-byte LDS read, with no barrier: tiles
+// are prefetched DEPTH ahead in registers by unconditional loads (5 per tile,
+// all of them countable by vmcnt).  Keys past the row's end (in the last tile
+// and in padding steps) get probability 0 and a valid V row, and
+// fma(0, v, o) = o exactly (o is never -0), so every tile is whole.
+// o = fma(p from lane J of this lane's 16-lane row, v, o): one VALU
+// instruction, the broadcast being the fma's DPP source operand.  The caller
+// issues s_nop 1 first when p may have been written by the VALU within the
+// two preceding instructions (the DPP source read hazard).
+#define G4_FMA_ROW_BROADCAST(J)                                                            \
+    __device__ __forceinline__ void fma_row_broadcast_##J(float &o, float p, float v) {     \
+        asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:" #J " row_mask:0xf bank_mask:0xf" \
+                     : "+v"(o)                                                              \
+                     : "v"(p), "v"(v));                                                     \
+    }
+G4_FMA_ROW_BROADCAST(0) G4_FMA_ROW_BROADCAST(1) G4_FMA_ROW_BROADCAST(2) G4_FMA_ROW_BROADCAST(3)
+G4_FMA_ROW_BROADCAST(4) G4_FMA_ROW_BROADCAST(5) G4_FMA_ROW_BROADCAST(6) G4_FMA_ROW_BROADCAST(7)
+G4_FMA_ROW_BROADCAST(8) G4_FMA_ROW_BROADCAST(9) G4_FMA_ROW_BROADCAST(10) G4_FMA_ROW_BROADCAST(11)
+G4_FMA_ROW_BROADCAST(12) G4_FMA_ROW_BROADCAST(13) G4_FMA_ROW_BROADCAST(14) G4_FMA_ROW_BROADCAST(15)
+#undef G4_FMA_ROW_BROADCAST
+
 template <int HD, int DEPTH>
-__global__ __launch_bounds__(512) void k_attn_values_decode(float *__restrict__ out,
-                                                            const float *__restrict__ probs,
-                                                            const float *__restrict__ value_cache,
-                                                            int cache_len, int full, int start_pos,
-                                                            const int *__restrict__ pos_dev,
-                                                            size_t stride) {
-    __shared__ __attribute__((aligned(16))) float s_v[2][64][64];
-    __shared__ __attribute__((aligned(16))) float s_p[2][8][64];
+__global__ __launch_bounds__(64) void k_attn_values_decode(float *__restrict__ out,
+                                                           const float *__restrict__ probs,
+                                                           const float *__restrict__ value_cache,
+                                                           int cache_len, int full, int start_pos,
+                                                           const int *__restrict__ pos_dev,
+                                                           size_t stride) {
+    __shared__ __attribute__((aligned(16))) float s_v[2][16][68];  // [slot][channel][key]
     if (pos_dev) start_pos = *pos_dev;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int head = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int d0 = blockIdx.x * 64, t = blockIdx.y;
+    const int lane = threadIdx.x, r = lane >> 4, j = lane & 15;
+    const int c0 = blockIdx.x * 16, head = 4 * blockIdx.y + r, t = blockIdx.z;
     const int pos = start_pos + t, first = first_visible(pos, full);
     const int keys = pos - first + 1, tiles = (keys + 63) / 64, mask = cache_len - 1;
     const float *prow = probs + ((size_t)t * 8 + head) * stride;
-
-    // thread covers float4 (key kr, channels 4 cc .. 4 cc + 3) of a tile, twice
+    const int last4 = (int)stride - 4;  // the row holds `stride` floats
+    // V loads: lane (kq, cc) = (lane >> 2, lane & 3) takes keys 4 kq .. 4 kq + 3
+    // of channels c0 + 4 cc .. + 3
+    const int kq = lane >> 2, cc = lane & 3;
     typedef float f4 __attribute__((ext_vector_type(4)));  // SROA-friendly (HIP's float4 is not)
     struct Stage {
-        f4 v[2];
-        float p;
+        f4 v[4];
+        f4 p;
     };
-    auto load_tile = [&](int tile, Stage &r) __attribute__((always_inline)) {
+    auto load_tile = [&](int tile, Stage &st) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int idx = i * 512 + tid, kr = idx >> 4, cc = idx & 15;
-            const int p = first + min(tile * 64 + kr, keys - 1);  // past the end: a valid row
-            r.v[i] = *reinterpret_cast<const f4 *>(value_cache + (size_t)(p & mask) * HD + d0 + 4 * cc);
+        for (int i = 0; i < 4; i++) {
+            const int key = min(tile * 64 + 4 * kq + i, keys - 1);  // past the end: a valid row
+            st.v[i] = *reinterpret_cast<const f4 *>(value_cache + (size_t)((first + key) & mask) * HD +
+                                                    c0 + 4 * cc);
         }
-        r.p = prow[min(tile * 64 + lane, keys - 1)];
+        st.p = *reinterpret_cast<const f4 *>(prow + min(tile * 64 + 4 * j, last4));  // masked at use
     };
-    auto store_tile = [&](int slot, const Stage &r) __attribute__((always_inline)) {
+    auto masked = [&](int tile, f4 p) __attribute__((always_inline)) {
+        const int kb = tile * 64 + 4 * j;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int idx = i * 512 + tid, kr = idx >> 4, cc = idx & 15;
-            *reinterpret_cast<f4 *>(&s_v[slot][kr][4 * cc]) = r.v[i];
-        }
-        s_p[slot][head][lane] = r.p;
+        for (int e = 0; e < 4; e++) p[e] = kb + e < keys ? p[e] : 0.0f;
+        return p;
     };
-    Stage ring[DEPTH];
-    {
-        Stage head_tile;
-        load_tile(0, head_tile);
+    auto store_tile = [&](int slot, const Stage &st) __attribute__((always_inline)) {
 #pragma unroll
-        for (int s = 0; s < DEPTH; s++) load_tile(min(s + 1, tiles - 1), ring[s]);
-        store_tile(0, head_tile);
-    }
+        for (int e = 0; e < 4; e++)
+            *reinterpret_cast<f4 *>(&s_v[slot][4 * cc + e][4 * kq]) =
+                f4{st.v[0][e], st.v[1][e], st.v[2][e], st.v[3][e]};
+    };
     float o = 0.0f;
-    // step: tile `tile` is in LDS slot tile & 1; ring slot holds tile + 1
-    // always_inline: called 16 times, and the ring must stay in registers
-    auto step = [&](int tile, Stage &slot, bool whole) __attribute__((always_inline)) {
-        __syncthreads();  // tile complete in LDS; every wave is done with tile - 1
-        // unconditional (past the last tile the slot is stored but never read):
-        // a conditional load would make the compiler drain the prefetch ring
-        store_tile((tile + 1) & 1, slot);
-        load_tile(min(tile + 1 + DEPTH, tiles - 1), slot);
-        const float(*v)[64] = s_v[tile & 1];
-        const float4 *pv = reinterpret_cast<const float4 *>(s_p[tile & 1][head]);
-        if (whole) {
-#pragma unroll
-            for (int k4 = 0; k4 < 16; k4++) {
-                const float4 p4 = pv[k4];
-                o = fmaf(p4.x, v[4 * k4 + 0][lane], o);
-                o = fmaf(p4.y, v[4 * k4 + 1][lane], o);
-                o = fmaf(p4.z, v[4 * k4 + 2][lane], o);
-                o = fmaf(p4.w, v[4 * k4 + 3][lane], o);
-            }
-        } else {
-            const int n = min(64, keys - tile * 64);
-            for (int k = 0; k < n; k++) o = fmaf(s_p[tile & 1][head][k], v[k][lane], o);
-        }
-    };
-    // Whole groups of DEPTH full tiles run with no branch at all (exact
-    // waits on the prefetch ring); the last < DEPTH tiles follow.  The steps
-    // are written out: a loop over them (barriers inside) is not unrolled, and
-    // a dynamically indexed ring would live in scratch memory.
-    const int full_tiles = keys / 64;
-    int tile = 0;
-    static_assert(DEPTH == 8, "the steps below are written out for 8 ring slots");
-    for (; tile + DEPTH <= full_tiles; tile += DEPTH) {
-        step(tile + 0, ring[0], true);
-        step(tile + 1, ring[1], true);
-        step(tile + 2, ring[2], true);
-        step(tile + 3, ring[3], true);
-        step(tile + 4, ring[4], true);
-        step(tile + 5, ring[5], true);
-        step(tile + 6, ring[6], true);
-        step(tile + 7, ring[7], true);
+    // keys 4 J .. 4 J + 3 of a tile: V column quad a, probabilities in row lane J
+#define G4_KEYS4(J)                                   \
+    {                                                 \
+        const f4 a = col[J];                          \
+        fma_row_broadcast_##J(o, p.x, a.x);           \
+        fma_row_broadcast_##J(o, p.y, a.y);           \
+        fma_row_broadcast_##J(o, p.z, a.z);           \
+        fma_row_broadcast_##J(o, p.w, a.w);           \
     }
-#define G4_VALUES_TAIL(S) \
-    if (tile + S < tiles) step(tile + S, ring[S], false); /* uniform */
-    G4_VALUES_TAIL(0) G4_VALUES_TAIL(1) G4_VALUES_TAIL(2) G4_VALUES_TAIL(3)
-    G4_VALUES_TAIL(4) G4_VALUES_TAIL(5) G4_VALUES_TAIL(6) G4_VALUES_TAIL(7)
-#undef G4_VALUES_TAIL
-    out[((size_t)t * 8 + head) * HD + d0 + lane] = o;
+    auto chain64 = [&](const f4 (&col)[16], f4 p) __attribute__((always_inline)) {
+        // p is final before the nop: no VALU write of it within two instructions
+        // of a DPP read (the hazard is not checked across inline asm)
+        asm volatile("" : "+v"(p.x), "+v"(p.y), "+v"(p.z), "+v"(p.w));
+        asm volatile("s_nop 1");
+        G4_KEYS4(0) G4_KEYS4(1) G4_KEYS4(2) G4_KEYS4(3) G4_KEYS4(4) G4_KEYS4(5) G4_KEYS4(6)
+        G4_KEYS4(7) G4_KEYS4(8) G4_KEYS4(9) G4_KEYS4(10) G4_KEYS4(11) G4_KEYS4(12) G4_KEYS4(13)
+        G4_KEYS4(14) G4_KEYS4(15)
+    };
+#undef G4_KEYS4
+    Stage ring[DEPTH];
+    f4 p_cur;  // probabilities of the tile in LDS
+    {
+        Stage first_tile;
+        load_tile(0, first_tile);
+#pragma unroll
+        for (int s = 0; s < DEPTH; s++) load_tile(s + 1, ring[s]);
+        store_tile(0, first_tile);
+        p_cur = masked(0, first_tile.p);
+    }
+    // step: tile `tile` is in LDS slot tile & 1 (its probabilities in p_cur);
+    // its column is read, then the ring slot's tile + 1 goes to the other LDS
+    // slot (last read by tile - 1: a wave's LDS accesses complete in order) and
+    // the ring slot is refilled with tile + 1 + DEPTH.  always_inline: the
+    // ring must stay in registers.
+    auto step = [&](int tile, Stage &slot) __attribute__((always_inline)) {
+        f4 col[16];  // this lane's channel, the tile's 64 keys: all reads issued first
+        const f4 *src = reinterpret_cast<const f4 *>(&s_v[tile & 1][j][0]);
+#pragma unroll
+        for (int i = 0; i < 16; i++) col[i] = src[i];
+        store_tile((tile + 1) & 1, slot);
+        const f4 p_next = slot.p;
+        load_tile(tile + 1 + DEPTH, slot);  // unconditional: past the end, whole no-op tiles
+        chain64(col, p_cur);
+        p_cur = masked(tile + 1, p_next);
+    };
+    // The steps are written out (a dynamically indexed ring would live in
+    // scratch memory); steps past the last tile add nothing.
+    static_assert(DEPTH == 8, "the steps below are written out for 8 ring slots");
+    for (int tile = 0; tile < tiles; tile += DEPTH) {
+        step(tile + 0, ring[0]);
+        step(tile + 1, ring[1]);
+        step(tile + 2, ring[2]);
+        step(tile + 3, ring[3]);
+        step(tile + 4, ring[4]);
+        step(tile + 5, ring[5]);
+        step(tile + 6, ring[6]);
+        step(tile + 7, ring[7]);
+    }
+    out[((size_t)t * 8 + head) * HD + c0 + j] = o;
 }
 
 int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
@@ -1211,13 +1241,13 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
                            scores, heads, full, start_pos, pos_dev, stride);
     }
     const unsigned slices = (unsigned)(head_dim / 64);
-    if (n <= 4) {  // decode: one token per block, one head per wave, deep prefetch
-        dim3 grid(slices, nn);
+    if (n <= 4) {  // decode: one wave per (16 channels, 4 heads, token), deep prefetch
+        dim3 grid((unsigned)(head_dim / 16), 2, nn);
         if (head_dim == 256)
-            hipLaunchKernelGGL((k_attn_values_decode<256, 8>), grid, dim3(512), 0, s, out, scores,
+            hipLaunchKernelGGL((k_attn_values_decode<256, 8>), grid, dim3(64), 0, s, out, scores,
                                value_cache, cache_len, full, start_pos, pos_dev, stride);
         else
-            hipLaunchKernelGGL((k_attn_values_decode<512, 8>), grid, dim3(512), 0, s, out, scores,
+            hipLaunchKernelGGL((k_attn_values_decode<512, 8>), grid, dim3(64), 0, s, out, scores,
                                value_cache, cache_len, full, start_pos, pos_dev, stride);
     } else {  // prefill: 4 tokens x 8 heads per block share each V tile
         dim3 grid(slices, (nn + 3) / 4);
