@@ -33,6 +33,24 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     return __half2float(__ushort_as_half(h));  // exact
 }
 
+// The reference's table GELU (gemma4.c:243-262): linear interpolation inside
+// [lower, upper), table[0] below, identity above.
+__device__ __forceinline__ float gelu_table_lookup(float x, const float *table, int size,
+                                                   float lower, float upper) {
+    const float scale = (float)(size - 1) / (upper - lower);
+    if (x <= lower) return table[0];
+    if (!(x >= upper)) {
+        const float position = (x - lower) * scale;
+        const int index = (int)position;
+        // x just below `upper` can round to position == size - 1 (x + 8 -> 16);
+        // the fraction is then 0 and the reference's result is table[size - 1].
+        if (index >= size - 1) return table[size - 1];
+        const float fraction = position - (float)index;
+        return table[index] + fraction * (table[index + 1] - table[index]);
+    }
+    return x;
+}
+
 // ---- scratch owned by the library ------------------------------------------
 
 // Device scratch for split-K matmul dot products and attention partials or
@@ -86,6 +104,30 @@ void launch_row_tail(hipStream_t s, const float *h, const float *w_in, float *re
 void launch_rope(hipStream_t s, const float *cosines, const float *sines, int pairs, float *v,
                  int heads, int head_dim, int start_pos, const int *pos_dev, size_t n);
 // gemma4.c:310-331
+// One token's fused products (k_gemv_fused): up to three matrices on one
+// input, fp32 input quantized in the kernel, GELU epilogues.
+struct GemvMat {
+    const int8_t *w;
+    const uint16_t *ws;
+    float *out;
+    int strips;  // output rows / 16
+};
+struct GemvJob {
+    GemvMat m[3];
+    int count;
+    const int8_t *xq;  // quantized input and its group scales, or
+    const float *xs;
+    const float *xf;   // the fp32 input
+    const float *mul;  // EPI_GELU_MUL
+    const float *gelu_table;
+    int gelu_size;
+    float gelu_lower, gelu_upper;
+    int k;
+};
+enum { EPI_PLAIN = 0, EPI_GELU_PAIR = 1, EPI_GELU_MUL = 2 };
+
+int launch_gemv_fused(hipStream_t s, const GemvJob &job, int epi, bool xf32);
+
 void launch_geglu(hipStream_t s, float *gate, const float *up, int rows, int width,
                   int up_stride, const float *table, int table_size, float lower, float upper);
 // gemma4.c:337-358

@@ -844,6 +844,147 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
         }
 }
 
+
+// ---------------------------------------------------------------------------
+// One token's products, fused with what surrounds them in the decode step.
+// Up to three weight matrices that read the same input run in one launch
+// (q, k and v), and the block layout is k_gemv_split's: one 16-row strip per
+// block, W waves splitting its groups, exact group dots and scale products
+// folded in group order from LDS (the reference's order).
+//   XF32: the input is fp32; each wave quantizes the groups it reads exactly
+//     as k_quantize does (absmax over the group, scale = absmax / 127,
+//     rint(x / scale)), so no quantize launch precedes the product.
+//   EPI_GELU_PAIR: a block takes strip b of matrices 0 and 1 (gate, up), half
+//     of its waves each, and writes gelu(gate) * up (gemma4.c geglu).
+//   EPI_GELU_MUL: out = gelu(acc) * mul[n] (the per-layer-embedding gate).
+template <int U, bool XF32, int EPI>
+__global__ __launch_bounds__(1024) void k_gemv_fused(GemvJob job) {
+    extern __shared__ __attribute__((aligned(16))) float s_fold[];
+    constexpr int NM = EPI == EPI_GELU_PAIR ? 2 : 1;  // matrices folded per block
+    const int k = job.k, groups = k >> 6;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int waves_per = (blockDim.x >> 6) / NM;
+    // which matrix and strip this wave works on (uniform per block / wave)
+    int mi = 0, strip = blockIdx.x;
+    if (EPI == EPI_GELU_PAIR) {
+        mi = wave / waves_per;
+    } else {
+        while (mi + 1 < job.count && strip >= job.m[mi].strips) strip -= job.m[mi++].strips;
+    }
+    const int wv = wave - (EPI == EPI_GELU_PAIR ? mi * waves_per : 0);
+    const int g_begin = (int)((long)wv * groups / waves_per);
+    const int g_end = (int)((long)(wv + 1) * groups / waves_per);
+    const GemvMat mat = job.m[mi];
+    float *s_d = s_fold + (size_t)(EPI == EPI_GELU_PAIR ? mi : 0) * groups * 16;  // [nm][g][r]
+    float *s_c = s_fold + (size_t)NM * groups * 16 + (size_t)(EPI == EPI_GELU_PAIR ? mi : 0) * groups * 16;
+    const int chunk = lane >> 2, b2 = (lane >> 2) & 1, b3 = (lane >> 3) & 1;
+    const int row = 4 * (lane & 3) + 2 * b2 + b3;
+    const uint4 *tiles = reinterpret_cast<const uint4 *>(mat.w + (size_t)strip * 16 * k) + lane;
+    const uint16_t *wscale = mat.ws + (size_t)strip * groups * 16 + row;
+
+    auto batch = [&](int g0, auto bsize) __attribute__((always_inline)) {
+        constexpr int B = decltype(bsize)::value;
+        uint4 t[B];
+        uint16_t wsr[B];
+        int x4[B];
+        float xsc[B];
+        float4 xf[B];
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            t[u] = tiles[(size_t)(g0 + u) * 64];
+            if (XF32) {
+                xf[u] = reinterpret_cast<const float4 *>(job.xf + (size_t)(g0 + u) * 64)[chunk];
+            } else {
+                x4[u] = reinterpret_cast<const int *>(job.xq)[(g0 + u) * 16 + chunk];
+                xsc[u] = job.xs[g0 + u];
+            }
+            wsr[u] = wscale[(g0 + u) * 16];
+        }
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            if (XF32) {  // k_quantize's arithmetic for this lane's four values
+                const float4 v = xf[u];
+                float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+                for (int o = 4; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+                const float scale = m / 127.0f;
+                const float inverse = scale > 0.0f ? 1.0f / scale : 0.0f;
+                const int q0 = (int)rintf(v.x * inverse), q1 = (int)rintf(v.y * inverse);
+                const int q2 = (int)rintf(v.z * inverse), q3 = (int)rintf(v.w * inverse);
+                x4[u] = (q0 & 0xff) | (q1 & 0xff) << 8 | (q2 & 0xff) << 16 | (int)((unsigned)q3 << 24);
+                xsc[u] = scale;
+            }
+            int d[1];
+            const int xx[1] = {x4[u]};
+            gemv_group_dots<1>(t[u], xx, b2, b3, d);
+            if (lane < 16) {
+                s_d[(g0 + u) * 16 + row] = (float)d[0];
+                s_c[(g0 + u) * 16 + row] = half_bits_to_float(wsr[u]) * xsc[u];
+            }
+        }
+    };
+    int g = g_begin;
+    for (; g + U <= g_end; g += U) batch(g, std::integral_constant<int, U>());
+    if constexpr (U >= 16) if (g + 8 <= g_end) { batch(g, std::integral_constant<int, 8>()); g += 8; }
+    if constexpr (U >= 8) if (g + 4 <= g_end) { batch(g, std::integral_constant<int, 4>()); g += 4; }
+    if constexpr (U >= 4) if (g + 2 <= g_end) { batch(g, std::integral_constant<int, 2>()); g += 2; }
+    if (g < g_end) batch(g, std::integral_constant<int, 1>());
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < 16 * NM) {  // wave 0
+        const int mm = tid >> 4, r = tid & 15;
+        const float *pd = s_fold + (size_t)mm * groups * 16 + r;
+        const float *pc = s_fold + (size_t)NM * groups * 16 + (size_t)mm * groups * 16 + r;
+        float acc = 0.0f;
+        for (int gg = 0; gg < groups; gg++) acc = fmaf(pd[gg * 16], pc[gg * 16], acc);
+        const int n = strip * 16 + r;
+        if (EPI == EPI_PLAIN) {
+            mat.out[n] = acc;
+        } else if (EPI == EPI_GELU_MUL) {
+            mat.out[n] = gelu_table_lookup(acc, job.gelu_table, job.gelu_size, job.gelu_lower,
+                                           job.gelu_upper) * job.mul[n];
+        } else {
+            const float up = __shfl(acc, r + 16);  // lanes 16..31 hold matrix 1
+            if (mm == 0)
+                job.m[0].out[n] = gelu_table_lookup(acc, job.gelu_table, job.gelu_size,
+                                                    job.gelu_lower, job.gelu_upper) * up;
+        }
+    }
+}
+
+// The decode products of one token with their fused neighbours; `epi` one of
+// EPI_*, xf32: the input is job.xf.  Waves per strip: enough for ~2048 waves
+// in all, at most 16 per block and at least 8 groups each.
+int launch_gemv_fused(hipStream_t s, const GemvJob &job, int epi, bool xf32) {
+    const int groups = job.k / 64;
+    int strips = 0;
+    for (int i = 0; i < job.count; i++) strips += job.m[i].strips;
+    const int blocks = epi == EPI_GELU_PAIR ? job.m[0].strips : strips;
+    const int nm = epi == EPI_GELU_PAIR ? 2 : 1;
+    if (job.k % 64 || blocks <= 0 || (epi == EPI_GELU_PAIR && (job.count != 2 || job.m[1].strips != blocks)))
+        return set_error(G4_ERR_ARG, "fused product: bad shape");
+    int waves = (2048 + blocks * nm - 1) / (blocks * nm);
+    const int max_waves = groups / 8 > 0 ? groups / 8 : 1;
+    if (waves > max_waves) waves = max_waves;
+    if (waves * nm > 16) waves = 16 / nm;
+    if (waves < 1) waves = 1;
+    const size_t lds = (size_t)2 * nm * groups * 16 * sizeof(float);
+    if (lds > 64 * 1024) return set_error(G4_ERR_ARG, "fused product: K too large");
+    const dim3 grid((unsigned)blocks), block((unsigned)(64 * waves * nm));
+#define G4_FUSED(XF, EP) hipLaunchKernelGGL((k_gemv_fused<16, XF, EP>), grid, block, lds, s, job)
+    if (xf32) {
+        if (epi == EPI_PLAIN) G4_FUSED(true, EPI_PLAIN);
+        else if (epi == EPI_GELU_MUL) G4_FUSED(true, EPI_GELU_MUL);
+        else G4_FUSED(true, EPI_GELU_PAIR);
+    } else {
+        if (epi == EPI_PLAIN) G4_FUSED(false, EPI_PLAIN);
+        else if (epi == EPI_GELU_MUL) G4_FUSED(false, EPI_GELU_MUL);
+        else G4_FUSED(false, EPI_GELU_PAIR);
+    }
+#undef G4_FUSED
+    return G4_OK;
+}
+
 int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq, const float *xs,
                   const int8_t *w, const uint16_t *ws, int n_out, int k, int rows) {
     if (rows <= 0) return G4_OK;
@@ -982,22 +1123,6 @@ void launch_rope(hipStream_t s, const float *cosines, const float *sines, int pa
 }
 
 // gemma4.c:310-331.
-__device__ __forceinline__ float gelu_table_lookup(float x, const float *table, int size,
-                                                   float lower, float upper) {
-    const float scale = (float)(size - 1) / (upper - lower);
-    if (x <= lower) return table[0];
-    if (!(x >= upper)) {
-        const float position = (x - lower) * scale;
-        const int index = (int)position;
-        // x just below `upper` can round to position == size - 1 (x + 8 -> 16);
-        // the fraction is then 0 and the reference's result is table[size - 1].
-        if (index >= size - 1) return table[size - 1];
-        const float fraction = position - (float)index;
-        return table[index] + fraction * (table[index + 1] - table[index]);
-    }
-    return x;
-}
-
 __global__ __launch_bounds__(256) void k_geglu(float *gate, const float *up, int width, int up_stride,
                                                size_t total, const float *__restrict__ table,
                                                int size, float lower, float upper) {

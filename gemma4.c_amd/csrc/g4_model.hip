@@ -331,6 +331,23 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
     if (fused)  // layer 0's input norm + quantize
         launch_row_tail(s, nullptr, nullptr, c.residual, 1.0f, c.layers[0].input_ln, nullptr, c.q8,
                         c.qs, 1e-6f, n, 0, 0, 1, 1);
+    // One token in reference order: the products fused with their neighbours
+    // (k_gemv_fused): q, k and v in one launch; the quantize before o, down
+    // and ple_proj done inside those products (they read fp32 and write
+    // c.aux, so input and output never alias); geglu in the gate/up and
+    // ple_gate epilogues.
+    const bool one = fused && n == 1;
+    auto job_on = [&](const float *xf) {
+        GemvJob job{};
+        job.xq = c.q8;
+        job.xs = c.qs;
+        job.xf = xf;
+        job.gelu_table = c.gelu;
+        job.gelu_size = c.gelu_size;
+        job.gelu_lower = c.gelu_lower;
+        job.gelu_upper = c.gelu_upper;
+        return job;
+    };
     for (int l = 0; l < G4_LAYERS; l++) {
         const Layer &L = c.layers[l];
         const int hd = L.head_dim, qw = L.query_width, heads = qw / hd;
@@ -340,26 +357,51 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
         }
 
         // attention
-        G4_TRY(matmul(c, c.aux, qw, L.q, n));
-        launch_rmsnorm(s, c.aux, c.aux, L.q_norm, hd, 1e-6f, (size_t)n * heads);
-        launch_rope(s, L.rope_cos, L.rope_sin, L.pairs, c.aux, heads, hd, start_pos, pos_dev, n);
         float *keys = c.cache[L.owner];
         const int cache_len = c.cache_len[L.owner];
         float *values = keys + (size_t)cache_len * hd;
+        if (one) {
+            GemvJob job = job_on(nullptr);
+            job.k = G4_HIDDEN;
+            job.m[0] = GemvMat{L.q.data, L.q.scales, c.aux, qw / 16};
+            job.count = 1;
+            if (L.k.data) {
+                job.m[1] = GemvMat{L.k.data, L.k.scales, c.k_new, hd / 16};
+                job.m[2] = GemvMat{L.v.data, L.v.scales, c.v_new, hd / 16};
+                job.count = 3;
+            }
+            G4_TRY(launch_gemv_fused(s, job, EPI_PLAIN, false));
+        } else {
+            G4_TRY(matmul(c, c.aux, qw, L.q, n));
+        }
+        launch_rmsnorm(s, c.aux, c.aux, L.q_norm, hd, 1e-6f, (size_t)n * heads);
+        launch_rope(s, L.rope_cos, L.rope_sin, L.pairs, c.aux, heads, hd, start_pos, pos_dev, n);
         if (L.k.data) {
-            G4_TRY(matmul(c, c.k_new, hd, L.k, n));
-            G4_TRY(matmul(c, c.v_new, hd, L.v, n));
+            if (!one) {
+                G4_TRY(matmul(c, c.k_new, hd, L.k, n));
+                G4_TRY(matmul(c, c.v_new, hd, L.v, n));
+            }
             launch_kv_finish(s, keys, values, c.k_new, c.v_new, L.k_norm, L.rope_cos, L.rope_sin,
                              L.pairs, hd, cache_len, start_pos, pos_dev, n);
         }
         G4_TRY(launch_attend(s, c.hidden, c.aux, keys, values, cache_len, hd, heads, L.full,
                              start_pos, pos_dev, n));
-        launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * qw / 64);
-        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.o, n));
+        float *o_out = c.hidden;  // where the sublayer's output lands
+        if (one) {
+            GemvJob job = job_on(c.hidden);
+            job.k = qw;
+            job.m[0] = GemvMat{L.o.data, L.o.scales, c.aux, G4_HIDDEN / 16};
+            job.count = 1;
+            G4_TRY(launch_gemv_fused(s, job, EPI_PLAIN, true));
+            o_out = c.aux;
+        } else {
+            launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * qw / 64);
+            G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.o, n));
+        }
 
         // feed-forward
         if (fused) {
-            launch_row_tail(s, c.hidden, L.post_attn_ln, c.residual, 1.0f, L.pre_ffn_ln, nullptr,
+            launch_row_tail(s, o_out, L.post_attn_ln, c.residual, 1.0f, L.pre_ffn_ln, nullptr,
                             c.q8, c.qs, 1e-6f, n, 1, 1, 1, 1);
         } else {
             launch_rmsnorm(s, c.hidden, c.hidden, L.post_attn_ln, G4_HIDDEN, 1e-6f, n);
@@ -367,33 +409,65 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
             launch_rmsnorm(s, c.hidden, c.residual, L.pre_ffn_ln, G4_HIDDEN, 1e-6f, n);
             launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_HIDDEN / 64);
         }
-        G4_TRY(matmul(c, c.hidden, L.ffn, L.gate, n));
-        G4_TRY(matmul(c, c.aux, L.ffn, L.up, n));
-        launch_geglu(s, c.hidden, c.aux, n, L.ffn, L.ffn, c.gelu, c.gelu_size, c.gelu_lower,
-                     c.gelu_upper);
-        launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * L.ffn / 64);
-        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.down, n));
+        float *f_out = c.hidden;
+        if (one) {
+            GemvJob job = job_on(nullptr);
+            job.k = G4_HIDDEN;
+            job.m[0] = GemvMat{L.gate.data, L.gate.scales, c.hidden, L.ffn / 16};
+            job.m[1] = GemvMat{L.up.data, L.up.scales, nullptr, L.ffn / 16};
+            job.count = 2;
+            G4_TRY(launch_gemv_fused(s, job, EPI_GELU_PAIR, false));
+            job = job_on(c.hidden);
+            job.k = L.ffn;
+            job.m[0] = GemvMat{L.down.data, L.down.scales, c.aux, G4_HIDDEN / 16};
+            job.count = 1;
+            G4_TRY(launch_gemv_fused(s, job, EPI_PLAIN, true));
+            f_out = c.aux;
+        } else {
+            G4_TRY(matmul(c, c.hidden, L.ffn, L.gate, n));
+            G4_TRY(matmul(c, c.aux, L.ffn, L.up, n));
+            launch_geglu(s, c.hidden, c.aux, n, L.ffn, L.ffn, c.gelu, c.gelu_size, c.gelu_lower,
+                         c.gelu_upper);
+            launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * L.ffn / 64);
+            G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.down, n));
+        }
 
         // per-layer embedding
         if (fused) {
-            launch_row_tail(s, c.hidden, L.post_ffn_ln, c.residual, 1.0f, nullptr, nullptr, c.q8,
+            launch_row_tail(s, f_out, L.post_ffn_ln, c.residual, 1.0f, nullptr, nullptr, c.q8,
                             c.qs, 1e-6f, n, 1, 1, 0, 1);
         } else {
             launch_rmsnorm(s, c.hidden, c.hidden, L.post_ffn_ln, G4_HIDDEN, 1e-6f, n);
             launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, 1.0f);
             launch_quantize(s, c.q8, c.qs, c.residual, (size_t)n * G4_HIDDEN / 64);
         }
-        G4_TRY(matmul(c, c.hidden, G4_PLE, L.ple_gate, n));
-        launch_geglu(s, c.hidden, c.ple + (size_t)l * G4_PLE, n, G4_PLE, ple_width, c.gelu,
-                     c.gelu_size, c.gelu_lower, c.gelu_upper);
-        launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_PLE / 64);
-        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.ple_proj, n));
+        float *p_out = c.hidden;
+        if (one) {
+            GemvJob job = job_on(nullptr);
+            job.k = G4_HIDDEN;
+            job.m[0] = GemvMat{L.ple_gate.data, L.ple_gate.scales, c.hidden, G4_PLE / 16};
+            job.count = 1;
+            job.mul = c.ple + (size_t)l * G4_PLE;
+            G4_TRY(launch_gemv_fused(s, job, EPI_GELU_MUL, false));
+            job = job_on(c.hidden);
+            job.k = G4_PLE;
+            job.m[0] = GemvMat{L.ple_proj.data, L.ple_proj.scales, c.aux, G4_HIDDEN / 16};
+            job.count = 1;
+            G4_TRY(launch_gemv_fused(s, job, EPI_PLAIN, true));
+            p_out = c.aux;
+        } else {
+            G4_TRY(matmul(c, c.hidden, G4_PLE, L.ple_gate, n));
+            launch_geglu(s, c.hidden, c.ple + (size_t)l * G4_PLE, n, G4_PLE, ple_width, c.gelu,
+                         c.gelu_size, c.gelu_lower, c.gelu_upper);
+            launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_PLE / 64);
+            G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.ple_proj, n));
+        }
         if (fused) {
             if (l + 1 < G4_LAYERS)  // + the next layer's input norm and quantize
-                launch_row_tail(s, c.hidden, L.post_ple_ln, c.residual, L.layer_scalar,
+                launch_row_tail(s, p_out, L.post_ple_ln, c.residual, L.layer_scalar,
                                 c.layers[l + 1].input_ln, nullptr, c.q8, c.qs, 1e-6f, n, 1, 1, 1, 1);
             else
-                launch_row_tail(s, c.hidden, L.post_ple_ln, c.residual, L.layer_scalar, nullptr,
+                launch_row_tail(s, p_out, L.post_ple_ln, c.residual, L.layer_scalar, nullptr,
                                 nullptr, nullptr, nullptr, 1e-6f, n, 1, 1, 0, 0);
         } else {
             launch_rmsnorm(s, c.hidden, c.hidden, L.post_ple_ln, G4_HIDDEN, 1e-6f, n);
