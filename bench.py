@@ -72,21 +72,33 @@ def random_weight(torch, n: int, k: int, gen):
     return w, s.to(torch.float16)
 
 
-def timed_launches(torch, fn, launches: int) -> float:
-    """Average milliseconds per launch between HIP events on torch's stream.
-    The stream is first parked on a spin kernel long enough for the host to
-    enqueue every launch, so the events see back-to-back kernels rather than
-    the host's launch rate."""
-    fn(0)
+def graph_timed(torch, fn, count: int, replays: int) -> float:
+    """Average milliseconds per launch: `count` launches (fn(0) .. fn(count-1),
+    each on torch's current stream) captured once as a HIP graph, then the
+    graph replayed `replays` times between HIP events on the replay stream.
+    The host's launch rate drops out; what remains is each kernel's duration
+    plus the device's gap between dependent kernels."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(count):
+            fn(i)
+    graph.replay()
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(int(2.5e6 * (0.5 + launches * 0.02)))  # ~(0.5 + 0.02 * launches) ms
     start.record()
-    for i in range(launches):
-        fn(i)
+    for _ in range(replays):
+        graph.replay()
     stop.record()
     stop.synchronize()
-    return start.elapsed_time(stop) / launches
+    ms = start.elapsed_time(stop) / (replays * count)
+    del graph
+    return ms
 
 
 def gemm_roofline(pkg, lib, torch) -> dict:
@@ -110,9 +122,10 @@ def gemm_roofline(pkg, lib, torch) -> dict:
     out = torch.empty((m, n), dtype=torch.float32, device="cuda")
 
     def launch(i):
-        pkg.check(lib.g4_matmul_int8(stream, out.data_ptr(), xq.data_ptr(), xs.data_ptr(), recs[i % copies], m))
+        pkg.check(lib.g4_matmul_int8(torch.cuda.current_stream().cuda_stream, out.data_ptr(),
+                                     xq.data_ptr(), xs.data_ptr(), recs[i % copies], m))
 
-    ms = timed_launches(torch, launch, 200)
+    ms = graph_timed(torch, launch, 4 * copies, 10)
     ops = 2.0 * m * n * k
     tops = ops / (ms * 1e-3) / 1e12
     moved = n * k + n * k // 32 + m * k + m * k // 16 + 4 * m * n
@@ -180,11 +193,11 @@ def gemv_sweep(pkg, lib, torch) -> dict:
                 recs.append(r)
 
             def launch(i, recs=recs, out=out, xq=xq, xs=xs):
-                pkg.check(lib.g4_matmul_int8(stream, out.data_ptr(), xq.data_ptr(), xs.data_ptr(),
-                                             recs[i % len(recs)], 1))
+                pkg.check(lib.g4_matmul_int8(torch.cuda.current_stream().cuda_stream, out.data_ptr(),
+                                             xq.data_ptr(), xs.data_ptr(), recs[i % len(recs)], 1))
 
-            launches = max(50, min(2000, copies * 4))
-            ms = timed_launches(torch, launch, launches)
+            captured = min(copies, 256)  # one pass over >= 512 MB of copies (or 256 launches)
+            ms = graph_timed(torch, launch, captured, max(2, 1024 // captured))
             b = gemv_bytes(n, k)
             rec = {"ms": ms, "gbs": b / (ms * 1e-3) / 1e9, "bytes": b}
             per_shape[key] = rec
@@ -197,6 +210,7 @@ def gemv_sweep(pkg, lib, torch) -> dict:
         "bytes_per_token": total_bytes,
         "gemv_ms_per_token": total_time,
         "per_shape": {k: round(v["gbs"], 1) for k, v in per_shape.items()},
+        "per_shape_us": {k: round(v["ms"] * 1e3, 2) for k, v in per_shape.items()},
     }
 
 
