@@ -105,7 +105,7 @@ void launch_rope(hipStream_t s, const float *cosines, const float *sines, int pa
                  int heads, int head_dim, int start_pos, const int *pos_dev, size_t n);
 // gemma4.c:310-331
 // One token's fused products (k_gemv_fused): up to three matrices on one
-// input, fp32 input quantized in the kernel, GELU epilogues.
+// input, GELU epilogues that can also write the next product's quantized input.
 struct GemvMat {
     const int8_t *w;
     const uint16_t *ws;
@@ -115,18 +115,37 @@ struct GemvMat {
 struct GemvJob {
     GemvMat m[3];
     int count;
-    const int8_t *xq;  // quantized input and its group scales, or
+    const int8_t *xq;  // quantized input and its group scales
     const float *xs;
-    const float *xf;   // the fp32 input
     const float *mul;  // EPI_GELU_MUL
     const float *gelu_table;
     int gelu_size;
     float gelu_lower, gelu_upper;
+    int8_t *q_out;  // GELU epilogues: the output quantized (or null)
+    float *qs_out;
     int k;
 };
 enum { EPI_PLAIN = 0, EPI_GELU_PAIR = 1, EPI_GELU_MUL = 2 };
+int launch_gemv_fused(hipStream_t s, const GemvJob &job, int epi);
 
-int launch_gemv_fused(hipStream_t s, const GemvJob &job, int epi, bool xf32);
+// Prefill products with a GELU epilogue (k_gemm_dma<EPI_GELU_*>): the output
+// is written quantized only (q_out [rows][n_out], qs_out [rows][n_out / 64]).
+struct GemmEpilogue {
+    const int8_t *w2;     // EPI_GELU_PAIR: the second operand (up) and its scales
+    const uint16_t *ws2;
+    const float *mul;     // EPI_GELU_MUL: mul[m * mul_stride + n]
+    size_t mul_stride;
+    const float *gelu_table;
+    int gelu_size;
+    float gelu_lower, gelu_upper;
+    int8_t *q_out;
+    float *qs_out;
+};
+// Returns G4_ERR_ARG (and launches nothing) when the shape does not fit the
+// fused kernel (rows <= 8, K not a multiple of 512, N not of 64).
+int launch_matmul_gelu(hipStream_t s, const int8_t *xq, const float *xs, const int8_t *w,
+                       const uint16_t *ws, int n_out, int k, int rows, int epi,
+                       const GemmEpilogue &ep);
 
 void launch_geglu(hipStream_t s, float *gate, const float *up, int rows, int width,
                   int up_stride, const float *table, int table_size, float lower, float upper);
@@ -136,15 +155,18 @@ void launch_embedding(hipStream_t s, float *out, const int8_t *table, const uint
                       int width, int table_rows, const int *tokens, size_t n, float multiplier);
 // gemma4.c:443-456: attention over a ring cache; dispatches on order().
 // pos_dev requires reference order and n == 1.
+// With q8 set, the output is also written quantized (k_quantize's groups).
 int launch_attend(hipStream_t s, float *out, const float *q, const float *key_cache,
                   const float *value_cache, int cache_len, int head_dim, int heads, int full,
-                  int start_pos, const int *pos_dev, size_t n);
+                  int start_pos, const int *pos_dev, size_t n, int8_t *q8 = nullptr,
+                  float *qs = nullptr);
 int launch_attend_parallel(hipStream_t s, float *out, const float *q, const float *key_cache,
                            const float *value_cache, int cache_len, int head_dim, int heads,
                            int full, int start_pos, size_t n);
 int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
                             const float *value_cache, int cache_len, int head_dim, int heads,
-                            int full, int start_pos, const int *pos_dev, size_t n);
+                            int full, int start_pos, const int *pos_dev, size_t n,
+                            int8_t *q8 = nullptr, float *qs = nullptr);
 // Fused tail of the K/V projections (gemma4.c:437-440): rmsnorm+rope of the n
 // new keys and rmsnorm of the new values, written into the rings at
 // (start_pos + t) & (cache_len - 1).

@@ -651,16 +651,18 @@ __global__ __launch_bounds__(256) void k_gemm_bg(float *__restrict__ out, size_t
 //      (256 bytes per tile), wave 3 repeats wave 2 into padding.
 // k-slots: lane (l%16, l/16) covers k = 16 (l/16) + 0..15 -- for B that is
 // chunks 4 (l/16) .. + 3 of weight row l%16.
+template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_t out_stride,
                                                   const int8_t *__restrict__ xq,
                                                   const float *__restrict__ xs,
                                                   const int8_t *__restrict__ w,
                                                   const uint16_t *__restrict__ ws, int rows,
-                                                  int n_out, int k) {
+                                                  int n_out, int k, GemmEpilogue ep) {
     constexpr int BM = 64, BN = 64, NT = BN / 16, WN = BN / 2, NI = WN / 16;
+    constexpr int NB = EPI == EPI_GELU_PAIR ? 2 : 1;  // B operands: (gate, up) or one
     struct alignas(16) Stage {
         int8_t a[BM * 64];
-        int8_t b[NT * 1024];
+        int8_t b[NB][NT * 1024];
     };
     struct alignas(16) Scales {  // 8 groups
         float x[2][BM][4];          // [group / 4][row][group % 4]
@@ -683,21 +685,25 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
     const int8_t *a_src = xq + (size_t)min(m0 + a_row, rows - 1) * k +
                           16 * ((lane & 3) ^ ((a_row >> 2) & 3));
     const int unit = lane ^ ((lane >> 4) << 2);
-    const int8_t *b_src = w + (size_t)min(nb0 + wave, n_blocks - 1) * groups * 1024 + unit * 16;
+    const size_t b_at = (size_t)min(nb0 + wave, n_blocks - 1) * groups * 1024 + unit * 16;
+    const int8_t *b_src = w + b_at, *b2_src = NB == 2 ? ep.w2 + b_at : nullptr;
     const char *c_src;  // scales: 16 bytes a lane, advancing 8 groups per chunk
     size_t c_step;
     if (wave < 2) {
         c_src = (const char *)(xs + (size_t)min(m0 + lane, rows - 1) * groups + 4 * wave);
         c_step = 8 * sizeof(float);
-    } else {
-        c_src = (const char *)(ws + (size_t)min(nb0 + (lane >> 4), n_blocks - 1) * groups * 16 + 8 * l16);
+    } else {  // wave 2: the weight scales; wave 3: the second operand's (or again the first's)
+        const uint16_t *scales = NB == 2 && wave == 3 ? ep.ws2 : ws;
+        c_src = (const char *)(scales + (size_t)min(nb0 + (lane >> 4), n_blocks - 1) * groups * 16 + 8 * l16);
         c_step = 8 * 16 * sizeof(uint16_t);
     }
     const int c_dst = wave < 2 ? wave * (BM * 16) : 2 * BM * 16 + (wave - 2) * (NT * 8 * 16 * 2);
     auto issue = [&](int g, Stage &d) __attribute__((always_inline)) {
         g = min(g, groups - 1);  // past the end: reload the last group (never read)
         __builtin_amdgcn_global_load_lds((const void *)(a_src + g * 64), (void *)(d.a + wave * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void *)(b_src + (size_t)g * 1024), (void *)(d.b + wave * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void *)(b_src + (size_t)g * 1024), (void *)(d.b[0] + wave * 1024), 16, 0, 0);
+        if (NB == 2)
+            __builtin_amdgcn_global_load_lds((const void *)(b2_src + (size_t)g * 1024), (void *)(d.b[1] + wave * 1024), 16, 0, 0);
     };
     auto issue_scales = [&](int chunk, Scales &d) __attribute__((always_inline)) {
         chunk = min(chunk, groups / 8 - 1);
@@ -722,24 +728,26 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
             b_off[ni][i] = (wn * NI + ni) * 1024 + slot * 16 + (l16 & 3) * 4;
         }
 
-    float acc[2][NI][4];
+    float acc[NB][2][NI][4];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int o = 0; o < NB; o++)
 #pragma unroll
-        for (int j = 0; j < NI; j++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) acc[i][j][v] = 0.0f;
+            for (int j = 0; j < NI; j++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[o][i][j][v] = 0.0f;
 
     // A group's four MFMAs are issued together into their own registers and
     // folded one step later, while the next group's MFMAs run: the fold never
     // waits on a fresh MFMA result.
     struct Dots {
-        v4i d[2][NI];
+        v4i d[NB][2][NI];
         float x[2][4];
-        float w[NI];
+        float w[NB][NI];
     };
     struct Frags {
-        v4i a[2], b[NI];
+        v4i a[2], b[NB][NI];
     };
     auto fetch = [&](const Stage &d, const Scales &s, int j, Frags &f, Dots &o)
                      __attribute__((always_inline)) {
@@ -750,27 +758,34 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
             for (int v = 0; v < 4; v++) o.x[mi][v] = s.x[j >> 2][wm * 32 + mi * 16 + 4 * q + v][j & 3];
         }
 #pragma unroll
-        for (int ni = 0; ni < NI; ni++) {
+        for (int ob = 0; ob < NB; ob++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) f.b[ni][i] = *reinterpret_cast<const int *>(d.b + b_off[ni][i]);
-            o.w[ni] = half_bits_to_float(s.s[0][wn * NI + ni][j][l16]);
-        }
+            for (int ni = 0; ni < NI; ni++) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) f.b[ob][ni][i] = *reinterpret_cast<const int *>(d.b[ob] + b_off[ni][i]);
+                o.w[ob][ni] = half_bits_to_float(s.s[ob][wn * NI + ni][j][l16]);
+            }
     };
     auto multiply = [&](const Frags &f, Dots &o) __attribute__((always_inline)) {
 #pragma unroll
-        for (int ni = 0; ni < NI; ni++)
+        for (int ob = 0; ob < NB; ob++)
 #pragma unroll
-            for (int mi = 0; mi < 2; mi++)
-                o.d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[mi], f.b[ni], zero, 0, 0, 0);
+            for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+                for (int mi = 0; mi < 2; mi++)
+                    o.d[ob][mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[mi], f.b[ob][ni], zero, 0, 0, 0);
     };
     auto fold = [&](const Dots &o) __attribute__((always_inline)) {
 #pragma unroll
-        for (int ni = 0; ni < NI; ni++)
+        for (int ob = 0; ob < NB; ob++)
 #pragma unroll
-            for (int mi = 0; mi < 2; mi++)
+            for (int ni = 0; ni < NI; ni++)
 #pragma unroll
-                for (int v = 0; v < 4; v++)
-                    acc[mi][ni][v] = fmaf((float)o.d[mi][ni][v], o.w[ni] * o.x[mi][v], acc[mi][ni][v]);
+                for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        acc[ob][mi][ni][v] = fmaf((float)o.d[ob][mi][ni][v], o.w[ob][ni] * o.x[mi][v],
+                                                  acc[ob][mi][ni][v]);
     };
 
     // Step g (j = g % 8): issue group g + 2 into the stage of group g - 2
@@ -783,10 +798,12 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
                     Scales &sc_fill, Dots &cur, const Dots &prev) __attribute__((always_inline)) {
         issue(g + 2, fill);
         if (j == 6) issue_scales(g / 8 + 1, sc_fill);
+        // groups g + 1 and g + 2 (1 + NB loads each) may still be in flight,
+        // and at j = 6, 7 the next chunk's scales as well
         if (j == 6 || j == 7)
-            __builtin_amdgcn_s_waitcnt(0xF70 | 5);  // vmcnt(5): 2 + 2 + the scale chunk
+            __builtin_amdgcn_s_waitcnt(0xF70 | (2 * (1 + NB) + 1));
         else
-            __builtin_amdgcn_s_waitcnt(0xF70 | 4);  // vmcnt(4)
+            __builtin_amdgcn_s_waitcnt(0xF70 | (2 * (1 + NB)));
         __builtin_amdgcn_s_barrier();
         Frags f;
         fetch(use, sc_use, j, f, cur);  // LDS reads in flight ...
@@ -801,11 +818,13 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
 #pragma unroll
         for (int v = 0; v < 4; v++) d1.x[mi][v] = 0.0f;
 #pragma unroll
-    for (int ni = 0; ni < NI; ni++) {
-        d1.w[ni] = 0.0f;
+    for (int ob = 0; ob < NB; ob++)
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++) d1.d[mi][ni] = zero;
-    }
+        for (int ni = 0; ni < NI; ni++) {
+            d1.w[ob][ni] = 0.0f;
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++) d1.d[ob][mi][ni] = zero;
+        }
     issue(0, st0);
     issue_scales(0, sc0);
     issue(1, st1);
@@ -829,58 +848,103 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
     if (g < groups) eight(g, sc0, sc1);  // uniform: groups % 16 == 8
     fold(d1);  // the last group (groups % 8 == 0: it went to d1)
     __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): no DMA outlives the block
+    if (EPI == EPI_PLAIN) {
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+            for (int ni = 0; ni < NI; ni++) {
+                const int col = wn * WN + ni * 16;
+                if (nb0 + (col >> 4) >= n_blocks) continue;
+                const size_t n = (size_t)nb0 * 16 + col + l16;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int m = m0 + wm * 32 + mi * 16 + 4 * q + v;
+                    if (m < rows) out[(size_t)m * out_stride + n] = acc[0][mi][ni][v];
+                }
+            }
+        return;
+    }
+    // GELU epilogues: the block's 64 columns are one quantization group of
+    // each of its rows.  gelu(gate) * up (or * mul), then k_quantize's
+    // arithmetic: row absmax over the 64 columns (16 lanes x NI tiles in this
+    // wave, and the other N-half's wave through LDS), scale = absmax / 127.
+    __shared__ float s_rowmax[2][BM];  // [wn][row]
+    float val[2][NI][4], rmax[2][4];
 #pragma unroll
     for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-        for (int ni = 0; ni < NI; ni++) {
-            const int col = wn * WN + ni * 16;
-            if (nb0 + (col >> 4) >= n_blocks) continue;
-            const size_t n = (size_t)nb0 * 16 + col + l16;
+        for (int v = 0; v < 4; v++) {
+            const int m = min(m0 + wm * 32 + mi * 16 + 4 * q + v, rows - 1);
+            float mx = 0.0f;
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int m = m0 + wm * 32 + mi * 16 + 4 * q + v;
-                if (m < rows) out[(size_t)m * out_stride + n] = acc[mi][ni][v];
+            for (int ni = 0; ni < NI; ni++) {
+                const int n = nb0 * 16 + wn * WN + ni * 16 + l16;
+                const float gl = gelu_table_lookup(acc[0][mi][ni][v], ep.gelu_table, ep.gelu_size,
+                                                   ep.gelu_lower, ep.gelu_upper);
+                const float x = EPI == EPI_GELU_PAIR ? gl * acc[NB - 1][mi][ni][v]
+                                                     : gl * ep.mul[(size_t)m * ep.mul_stride + n];
+                val[mi][ni][v] = x;
+                mx = fmaxf(mx, fabsf(x));
             }
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
+            rmax[mi][v] = mx;
+            if (l16 == 0) s_rowmax[wn][wm * 32 + mi * 16 + 4 * q + v] = mx;
+        }
+    __syncthreads();
+    const int groups_out = n_out >> 6;
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int r = wm * 32 + mi * 16 + 4 * q + v, m = m0 + r;
+            const float scale = fmaxf(rmax[mi][v], s_rowmax[wn ^ 1][r]) / 127.0f;
+            const float inverse = scale > 0.0f ? 1.0f / scale : 0.0f;
+            if (m >= rows) continue;
+#pragma unroll
+            for (int ni = 0; ni < NI; ni++) {
+                const int n = nb0 * 16 + wn * WN + ni * 16 + l16;
+                ep.q_out[(size_t)m * n_out + n] = (int8_t)(int)rintf(val[mi][ni][v] * inverse);
+            }
+            if (wn == 0 && l16 == 0) ep.qs_out[(size_t)m * groups_out + blockIdx.x] = scale;
         }
 }
 
 
 // ---------------------------------------------------------------------------
 // One token's products, fused with what surrounds them in the decode step.
-// Up to three weight matrices that read the same input run in one launch
-// (q, k and v), and the block layout is k_gemv_split's: one 16-row strip per
-// block, W waves splitting its groups, exact group dots and scale products
-// folded in group order from LDS (the reference's order).
-//   XF32: the input is fp32; each wave quantizes the groups it reads exactly
-//     as k_quantize does (absmax over the group, scale = absmax / 127,
-//     rint(x / scale)), so no quantize launch precedes the product.
-//   EPI_GELU_PAIR: a block takes strip b of matrices 0 and 1 (gate, up), half
-//     of its waves each, and writes gelu(gate) * up (gemma4.c geglu).
-//   EPI_GELU_MUL: out = gelu(acc) * mul[n] (the per-layer-embedding gate).
-template <int U, bool XF32, int EPI>
+// The block layout is k_gemv_split's: S 16-row strips per block (of each of
+// NM matrices), W waves splitting the groups of each, exact group dots and
+// scale products folded in group order from LDS (the reference's order).
+//   EPI_PLAIN (S = 1): up to three weight matrices that read the same input
+//     in one launch (q, k and v), blocks taken in matrix order.
+//   EPI_GELU_PAIR (S = 4): strips of matrices 0 and 1 (gate, up); writes
+//     gelu(gate) * up (gemma4.c geglu).
+//   EPI_GELU_MUL (S = 4): writes gelu(acc) * mul[n] (the per-layer-embedding
+//     gate).
+// The GELU epilogues cover 64 outputs per block, one quantization group:
+// with job.q_out set they also write it quantized exactly as k_quantize does
+// (absmax / 127, rint(x / scale)), so the next product reads it directly.
+template <int U, int EPI>
 __global__ __launch_bounds__(1024) void k_gemv_fused(GemvJob job) {
     extern __shared__ __attribute__((aligned(16))) float s_fold[];
-    constexpr int NM = EPI == EPI_GELU_PAIR ? 2 : 1;  // matrices folded per block
+    constexpr int NM = EPI == EPI_GELU_PAIR ? 2 : 1, S = EPI == EPI_PLAIN ? 1 : 4, SM = NM * S;
     const int k = job.k, groups = k >> 6;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int waves_per = (blockDim.x >> 6) / NM;
-    // which matrix and strip this wave works on (uniform per block / wave)
-    int mi = 0, strip = blockIdx.x;
-    if (EPI == EPI_GELU_PAIR) {
-        mi = wave / waves_per;
-    } else {
+    const int W = (blockDim.x >> 6) / SM;  // waves per strip of a matrix
+    const int sm = wave / W, wv = wave % W;
+    int mi = EPI == EPI_GELU_PAIR ? sm / S : 0, strip = blockIdx.x * S + sm % S;
+    if (EPI == EPI_PLAIN)
         while (mi + 1 < job.count && strip >= job.m[mi].strips) strip -= job.m[mi++].strips;
-    }
-    const int wv = wave - (EPI == EPI_GELU_PAIR ? mi * waves_per : 0);
-    const int g_begin = (int)((long)wv * groups / waves_per);
-    const int g_end = (int)((long)(wv + 1) * groups / waves_per);
+    const int g_begin = (int)((long)wv * groups / W), g_end = (int)((long)(wv + 1) * groups / W);
     const GemvMat mat = job.m[mi];
-    float *s_d = s_fold + (size_t)(EPI == EPI_GELU_PAIR ? mi : 0) * groups * 16;  // [nm][g][r]
-    float *s_c = s_fold + (size_t)NM * groups * 16 + (size_t)(EPI == EPI_GELU_PAIR ? mi : 0) * groups * 16;
+    float *s_d = s_fold + (size_t)sm * groups * 16;  // [sm][g][r]
+    float *s_c = s_fold + (size_t)(SM + sm) * groups * 16;
     const int chunk = lane >> 2, b2 = (lane >> 2) & 1, b3 = (lane >> 3) & 1;
     const int row = 4 * (lane & 3) + 2 * b2 + b3;
     const uint4 *tiles = reinterpret_cast<const uint4 *>(mat.w + (size_t)strip * 16 * k) + lane;
     const uint16_t *wscale = mat.ws + (size_t)strip * groups * 16 + row;
+    const int *xrow = reinterpret_cast<const int *>(job.xq) + chunk;
 
     auto batch = [&](int g0, auto bsize) __attribute__((always_inline)) {
         constexpr int B = decltype(bsize)::value;
@@ -888,32 +952,15 @@ __global__ __launch_bounds__(1024) void k_gemv_fused(GemvJob job) {
         uint16_t wsr[B];
         int x4[B];
         float xsc[B];
-        float4 xf[B];
 #pragma unroll
         for (int u = 0; u < B; u++) {
             t[u] = tiles[(size_t)(g0 + u) * 64];
-            if (XF32) {
-                xf[u] = reinterpret_cast<const float4 *>(job.xf + (size_t)(g0 + u) * 64)[chunk];
-            } else {
-                x4[u] = reinterpret_cast<const int *>(job.xq)[(g0 + u) * 16 + chunk];
-                xsc[u] = job.xs[g0 + u];
-            }
+            x4[u] = xrow[(g0 + u) * 16];
+            xsc[u] = job.xs[g0 + u];
             wsr[u] = wscale[(g0 + u) * 16];
         }
 #pragma unroll
         for (int u = 0; u < B; u++) {
-            if (XF32) {  // k_quantize's arithmetic for this lane's four values
-                const float4 v = xf[u];
-                float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-#pragma unroll
-                for (int o = 4; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-                const float scale = m / 127.0f;
-                const float inverse = scale > 0.0f ? 1.0f / scale : 0.0f;
-                const int q0 = (int)rintf(v.x * inverse), q1 = (int)rintf(v.y * inverse);
-                const int q2 = (int)rintf(v.z * inverse), q3 = (int)rintf(v.w * inverse);
-                x4[u] = (q0 & 0xff) | (q1 & 0xff) << 8 | (q2 & 0xff) << 16 | (int)((unsigned)q3 << 24);
-                xsc[u] = scale;
-            }
             int d[1];
             const int xx[1] = {x4[u]};
             gemv_group_dots<1>(t[u], xx, b2, b3, d);
@@ -931,57 +978,78 @@ __global__ __launch_bounds__(1024) void k_gemv_fused(GemvJob job) {
     if (g < g_end) batch(g, std::integral_constant<int, 1>());
     __syncthreads();
     const int tid = threadIdx.x;
-    if (tid < 16 * NM) {  // wave 0
-        const int mm = tid >> 4, r = tid & 15;
-        const float *pd = s_fold + (size_t)mm * groups * 16 + r;
-        const float *pc = s_fold + (size_t)NM * groups * 16 + (size_t)mm * groups * 16 + r;
-        float acc = 0.0f;
+    float acc = 0.0f;
+    if (tid < 16 * SM) {  // strip-matrix tid / 16, row tid % 16
+        const float *pd = s_fold + (size_t)(tid >> 4) * groups * 16 + (tid & 15);
+        const float *pc = s_fold + (size_t)(SM + (tid >> 4)) * groups * 16 + (tid & 15);
         for (int gg = 0; gg < groups; gg++) acc = fmaf(pd[gg * 16], pc[gg * 16], acc);
-        const int n = strip * 16 + r;
-        if (EPI == EPI_PLAIN) {
-            mat.out[n] = acc;
-        } else if (EPI == EPI_GELU_MUL) {
-            mat.out[n] = gelu_table_lookup(acc, job.gelu_table, job.gelu_size, job.gelu_lower,
-                                           job.gelu_upper) * job.mul[n];
-        } else {
-            const float up = __shfl(acc, r + 16);  // lanes 16..31 hold matrix 1
-            if (mm == 0)
-                job.m[0].out[n] = gelu_table_lookup(acc, job.gelu_table, job.gelu_size,
-                                                    job.gelu_lower, job.gelu_upper) * up;
-        }
+    }
+    if (EPI == EPI_PLAIN) {
+        if (tid < 16) mat.out[strip * 16 + tid] = acc;
+        return;
+    }
+    float *s_e = s_fold + (size_t)2 * SM * groups * 16;  // [NM][64] folded outputs
+    if (tid < 16 * SM) s_e[tid] = acc;
+    __syncthreads();
+    if (tid >= 64) return;
+    const int n = blockIdx.x * 64 + tid;
+    const float gl = gelu_table_lookup(s_e[tid], job.gelu_table, job.gelu_size, job.gelu_lower,
+                                       job.gelu_upper);
+    const float v = EPI == EPI_GELU_PAIR ? gl * s_e[64 + tid] : gl * job.mul[n];
+    if (job.m[0].out) job.m[0].out[n] = v;
+    if (job.q_out) {  // k_quantize's arithmetic over the block's 64 outputs
+        float m = fabsf(v);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float scale = m / 127.0f;
+        const float inverse = scale > 0.0f ? 1.0f / scale : 0.0f;
+        job.q_out[n] = (int8_t)(int)rintf(v * inverse);
+        if (tid == 0) job.qs_out[blockIdx.x] = scale;
     }
 }
 
 // The decode products of one token with their fused neighbours; `epi` one of
-// EPI_*, xf32: the input is job.xf.  Waves per strip: enough for ~2048 waves
-// in all, at most 16 per block and at least 8 groups each.
-int launch_gemv_fused(hipStream_t s, const GemvJob &job, int epi, bool xf32) {
+// EPI_*.  Waves per strip: enough for ~2048 waves in all, at most 16 per
+// block, and groups spread evenly.
+int launch_gemv_fused(hipStream_t s, const GemvJob &job, int epi) {
     const int groups = job.k / 64;
+    const int S = epi == EPI_PLAIN ? 1 : 4, nm = epi == EPI_GELU_PAIR ? 2 : 1, sm = S * nm;
     int strips = 0;
     for (int i = 0; i < job.count; i++) strips += job.m[i].strips;
-    const int blocks = epi == EPI_GELU_PAIR ? job.m[0].strips : strips;
-    const int nm = epi == EPI_GELU_PAIR ? 2 : 1;
-    if (job.k % 64 || blocks <= 0 || (epi == EPI_GELU_PAIR && (job.count != 2 || job.m[1].strips != blocks)))
+    if (job.k % 64 || job.count < 1 || job.count > 3 || (epi != EPI_PLAIN && job.count != nm) ||
+        (epi != EPI_PLAIN && job.m[0].strips % 4) ||
+        (epi == EPI_GELU_PAIR && job.m[1].strips != job.m[0].strips))
         return set_error(G4_ERR_ARG, "fused product: bad shape");
-    int waves = (2048 + blocks * nm - 1) / (blocks * nm);
-    const int max_waves = groups / 8 > 0 ? groups / 8 : 1;
+    const int blocks = epi == EPI_PLAIN ? strips : job.m[0].strips / 4;
+    int waves = (2048 + blocks * sm - 1) / (blocks * sm);
+    const int max_waves = groups / 4 > 0 ? groups / 4 : 1;
     if (waves > max_waves) waves = max_waves;
-    if (waves * nm > 16) waves = 16 / nm;
+    if (waves * sm > 16) waves = 16 / sm;
     if (waves < 1) waves = 1;
-    const size_t lds = (size_t)2 * nm * groups * 16 * sizeof(float);
+    const size_t lds = ((size_t)2 * sm * groups * 16 + 128) * sizeof(float);
     if (lds > 64 * 1024) return set_error(G4_ERR_ARG, "fused product: K too large");
-    const dim3 grid((unsigned)blocks), block((unsigned)(64 * waves * nm));
-#define G4_FUSED(XF, EP) hipLaunchKernelGGL((k_gemv_fused<16, XF, EP>), grid, block, lds, s, job)
-    if (xf32) {
-        if (epi == EPI_PLAIN) G4_FUSED(true, EPI_PLAIN);
-        else if (epi == EPI_GELU_MUL) G4_FUSED(true, EPI_GELU_MUL);
-        else G4_FUSED(true, EPI_GELU_PAIR);
-    } else {
-        if (epi == EPI_PLAIN) G4_FUSED(false, EPI_PLAIN);
-        else if (epi == EPI_GELU_MUL) G4_FUSED(false, EPI_GELU_MUL);
-        else G4_FUSED(false, EPI_GELU_PAIR);
-    }
-#undef G4_FUSED
+    const dim3 grid((unsigned)blocks), block((unsigned)(64 * waves * sm));
+    if (epi == EPI_PLAIN)
+        hipLaunchKernelGGL((k_gemv_fused<16, EPI_PLAIN>), grid, block, lds, s, job);
+    else if (epi == EPI_GELU_MUL)
+        hipLaunchKernelGGL((k_gemv_fused<16, EPI_GELU_MUL>), grid, block, lds, s, job);
+    else
+        hipLaunchKernelGGL((k_gemv_fused<16, EPI_GELU_PAIR>), grid, block, lds, s, job);
+    return G4_OK;
+}
+
+int launch_matmul_gelu(hipStream_t s, const int8_t *xq, const float *xs, const int8_t *w,
+                       const uint16_t *ws, int n_out, int k, int rows, int epi,
+                       const GemmEpilogue &ep) {
+    if (rows <= 8 || k % 512 || n_out % 64 || (epi != EPI_GELU_PAIR && epi != EPI_GELU_MUL))
+        return set_error(G4_ERR_ARG, "fused GEMM: shape %d x %d x %d does not fit", rows, n_out, k);
+    const dim3 grid((unsigned)(n_out / 64), (unsigned)((rows + 63) / 64));
+    if (epi == EPI_GELU_PAIR)
+        hipLaunchKernelGGL(k_gemm_dma<EPI_GELU_PAIR>, grid, dim3(256), 0, s, nullptr, (size_t)0, xq, xs, w,
+                           ws, rows, n_out, k, ep);
+    else
+        hipLaunchKernelGGL(k_gemm_dma<EPI_GELU_MUL>, grid, dim3(256), 0, s, nullptr, (size_t)0, xq, xs, w,
+                           ws, rows, n_out, k, ep);
     return G4_OK;
 }
 
@@ -992,8 +1060,8 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
     if (rows > 8) {
         const unsigned mb = (unsigned)((rows + 63) / 64);
         if (groups % 8 == 0)
-            hipLaunchKernelGGL(k_gemm_dma, dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
-                               out, out_stride, xq, xs, w, ws, rows, n_out, k);
+            hipLaunchKernelGGL(k_gemm_dma<EPI_PLAIN>, dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0,
+                               s, out, out_stride, xq, xs, w, ws, rows, n_out, k, GemmEpilogue{});
         else
             hipLaunchKernelGGL((k_gemm<64, 1>), dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
                                out, out_stride, xq, xs, w, ws, rows, n_out, k);

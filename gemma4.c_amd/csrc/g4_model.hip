@@ -53,8 +53,8 @@ struct Context {
     float gelu_lower = 0, gelu_upper = 0;
     float *residual = nullptr, *hidden = nullptr, *aux = nullptr, *ple = nullptr;
     float *k_new = nullptr, *v_new = nullptr, *logits = nullptr, *logits_all = nullptr;
-    int8_t *q8 = nullptr;
-    float *qs = nullptr;
+    int8_t *q8 = nullptr, *q8b = nullptr;  // quantized activations; q8b: written by a
+    float *qs = nullptr, *qsb = nullptr;   // product that reads q8 (the GELU epilogues)
     float *cache[15] = {};
     int cache_len[15] = {}, cache_dim[15] = {};
     int *tokens_dev = nullptr, *argmax_dev = nullptr;
@@ -102,6 +102,8 @@ static void free_all(Context &c) {
     release(c.logits_all);
     release(c.q8);
     release(c.qs);
+    release(c.q8b);
+    release(c.qsb);
     for (int i = 0; i < 15; i++) release(c.cache[i]);
     release(c.tokens_dev);
     release(c.argmax_dev);
@@ -280,6 +282,8 @@ static int init(const g4_tensor *records, int device) {
     G4_HIP(hipMalloc(&c.logits, (size_t)G4_VOCAB * sizeof(float)));
     G4_HIP(hipMalloc(&c.q8, wide));
     G4_HIP(hipMalloc(&c.qs, wide / 64 * sizeof(float)));
+    G4_HIP(hipMalloc(&c.q8b, wide));
+    G4_HIP(hipMalloc(&c.qsb, wide / 64 * sizeof(float)));
     for (int l = 0; l < 15; l++) {
         if (!records[2 + l * 19 + 11].data) continue;
         const int full = l % 5 == 4;
@@ -304,8 +308,10 @@ static int init(const g4_tensor *records, int device) {
     return G4_OK;
 }
 
-static int matmul(Context &c, float *out, size_t stride, const Weight &w, int rows) {
-    return launch_matmul(c.stream, out, stride, c.q8, c.qs, w.data, w.scales, w.n, w.k, rows);
+static int matmul(Context &c, float *out, size_t stride, const Weight &w, int rows,
+                  bool second = false) {
+    return launch_matmul(c.stream, out, stride, second ? c.q8b : c.q8, second ? c.qsb : c.qs,
+                         w.data, w.scales, w.n, w.k, rows);
 }
 
 // The sequence of gemma4.c:463-509 (attention: 411-461) for the n tokens in
@@ -332,16 +338,14 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
         launch_row_tail(s, nullptr, nullptr, c.residual, 1.0f, c.layers[0].input_ln, nullptr, c.q8,
                         c.qs, 1e-6f, n, 0, 0, 1, 1);
     // One token in reference order: the products fused with their neighbours
-    // (k_gemv_fused): q, k and v in one launch; the quantize before o, down
-    // and ple_proj done inside those products (they read fp32 and write
-    // c.aux, so input and output never alias); geglu in the gate/up and
-    // ple_gate epilogues.
+    // (k_gemv_fused): q, k and v in one launch; geglu and the quantize that
+    // follows it in the gate/up and ple_gate epilogues (into q8b: those
+    // products read q8).
     const bool one = fused && n == 1;
-    auto job_on = [&](const float *xf) {
+    auto job_on = [&]() {
         GemvJob job{};
         job.xq = c.q8;
         job.xs = c.qs;
-        job.xf = xf;
         job.gelu_table = c.gelu;
         job.gelu_size = c.gelu_size;
         job.gelu_lower = c.gelu_lower;
@@ -361,7 +365,7 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
         const int cache_len = c.cache_len[L.owner];
         float *values = keys + (size_t)cache_len * hd;
         if (one) {
-            GemvJob job = job_on(nullptr);
+            GemvJob job = job_on();
             job.k = G4_HIDDEN;
             job.m[0] = GemvMat{L.q.data, L.q.scales, c.aux, qw / 16};
             job.count = 1;
@@ -370,7 +374,7 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
                 job.m[2] = GemvMat{L.v.data, L.v.scales, c.v_new, hd / 16};
                 job.count = 3;
             }
-            G4_TRY(launch_gemv_fused(s, job, EPI_PLAIN, false));
+            G4_TRY(launch_gemv_fused(s, job, EPI_PLAIN));
         } else {
             G4_TRY(matmul(c, c.aux, qw, L.q, n));
         }
@@ -385,23 +389,12 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
                              L.pairs, hd, cache_len, start_pos, pos_dev, n);
         }
         G4_TRY(launch_attend(s, c.hidden, c.aux, keys, values, cache_len, hd, heads, L.full,
-                             start_pos, pos_dev, n));
-        float *o_out = c.hidden;  // where the sublayer's output lands
-        if (one) {
-            GemvJob job = job_on(c.hidden);
-            job.k = qw;
-            job.m[0] = GemvMat{L.o.data, L.o.scales, c.aux, G4_HIDDEN / 16};
-            job.count = 1;
-            G4_TRY(launch_gemv_fused(s, job, EPI_PLAIN, true));
-            o_out = c.aux;
-        } else {
-            launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * qw / 64);
-            G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.o, n));
-        }
+                             start_pos, pos_dev, n, c.q8, c.qs));
+        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.o, n));
 
         // feed-forward
         if (fused) {
-            launch_row_tail(s, o_out, L.post_attn_ln, c.residual, 1.0f, L.pre_ffn_ln, nullptr,
+            launch_row_tail(s, c.hidden, L.post_attn_ln, c.residual, 1.0f, L.pre_ffn_ln, nullptr,
                             c.q8, c.qs, 1e-6f, n, 1, 1, 1, 1);
         } else {
             launch_rmsnorm(s, c.hidden, c.hidden, L.post_attn_ln, G4_HIDDEN, 1e-6f, n);
@@ -409,65 +402,80 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
             launch_rmsnorm(s, c.hidden, c.residual, L.pre_ffn_ln, G4_HIDDEN, 1e-6f, n);
             launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_HIDDEN / 64);
         }
-        float *f_out = c.hidden;
-        if (one) {
-            GemvJob job = job_on(nullptr);
+        // many rows: gate and up in one GEMM whose epilogue applies geglu and
+        // quantizes (into q8b)
+        const bool gemm_fused = n > 8;
+        auto gelu_epilogue = [&]() {
+            GemmEpilogue ep{};
+            ep.gelu_table = c.gelu;
+            ep.gelu_size = c.gelu_size;
+            ep.gelu_lower = c.gelu_lower;
+            ep.gelu_upper = c.gelu_upper;
+            ep.q_out = c.q8b;
+            ep.qs_out = c.qsb;
+            return ep;
+        };
+        if (gemm_fused) {
+            GemmEpilogue ep = gelu_epilogue();
+            ep.w2 = L.up.data;
+            ep.ws2 = L.up.scales;
+            G4_TRY(launch_matmul_gelu(s, c.q8, c.qs, L.gate.data, L.gate.scales, L.ffn, G4_HIDDEN, n,
+                                      EPI_GELU_PAIR, ep));
+        } else if (one) {
+            GemvJob job = job_on();
             job.k = G4_HIDDEN;
-            job.m[0] = GemvMat{L.gate.data, L.gate.scales, c.hidden, L.ffn / 16};
+            job.m[0] = GemvMat{L.gate.data, L.gate.scales, nullptr, L.ffn / 16};
             job.m[1] = GemvMat{L.up.data, L.up.scales, nullptr, L.ffn / 16};
             job.count = 2;
-            G4_TRY(launch_gemv_fused(s, job, EPI_GELU_PAIR, false));
-            job = job_on(c.hidden);
-            job.k = L.ffn;
-            job.m[0] = GemvMat{L.down.data, L.down.scales, c.aux, G4_HIDDEN / 16};
-            job.count = 1;
-            G4_TRY(launch_gemv_fused(s, job, EPI_PLAIN, true));
-            f_out = c.aux;
+            job.q_out = c.q8b;
+            job.qs_out = c.qsb;
+            G4_TRY(launch_gemv_fused(s, job, EPI_GELU_PAIR));
         } else {
             G4_TRY(matmul(c, c.hidden, L.ffn, L.gate, n));
             G4_TRY(matmul(c, c.aux, L.ffn, L.up, n));
             launch_geglu(s, c.hidden, c.aux, n, L.ffn, L.ffn, c.gelu, c.gelu_size, c.gelu_lower,
                          c.gelu_upper);
             launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * L.ffn / 64);
-            G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.down, n));
         }
+        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.down, n, one || gemm_fused));
 
         // per-layer embedding
         if (fused) {
-            launch_row_tail(s, f_out, L.post_ffn_ln, c.residual, 1.0f, nullptr, nullptr, c.q8,
+            launch_row_tail(s, c.hidden, L.post_ffn_ln, c.residual, 1.0f, nullptr, nullptr, c.q8,
                             c.qs, 1e-6f, n, 1, 1, 0, 1);
         } else {
             launch_rmsnorm(s, c.hidden, c.hidden, L.post_ffn_ln, G4_HIDDEN, 1e-6f, n);
             launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, 1.0f);
             launch_quantize(s, c.q8, c.qs, c.residual, (size_t)n * G4_HIDDEN / 64);
         }
-        float *p_out = c.hidden;
-        if (one) {
-            GemvJob job = job_on(nullptr);
+        if (gemm_fused) {
+            GemmEpilogue ep = gelu_epilogue();
+            ep.mul = c.ple + (size_t)l * G4_PLE;
+            ep.mul_stride = ple_width;
+            G4_TRY(launch_matmul_gelu(s, c.q8, c.qs, L.ple_gate.data, L.ple_gate.scales, G4_PLE,
+                                      G4_HIDDEN, n, EPI_GELU_MUL, ep));
+        } else if (one) {
+            GemvJob job = job_on();
             job.k = G4_HIDDEN;
-            job.m[0] = GemvMat{L.ple_gate.data, L.ple_gate.scales, c.hidden, G4_PLE / 16};
+            job.m[0] = GemvMat{L.ple_gate.data, L.ple_gate.scales, nullptr, G4_PLE / 16};
             job.count = 1;
             job.mul = c.ple + (size_t)l * G4_PLE;
-            G4_TRY(launch_gemv_fused(s, job, EPI_GELU_MUL, false));
-            job = job_on(c.hidden);
-            job.k = G4_PLE;
-            job.m[0] = GemvMat{L.ple_proj.data, L.ple_proj.scales, c.aux, G4_HIDDEN / 16};
-            job.count = 1;
-            G4_TRY(launch_gemv_fused(s, job, EPI_PLAIN, true));
-            p_out = c.aux;
+            job.q_out = c.q8b;
+            job.qs_out = c.qsb;
+            G4_TRY(launch_gemv_fused(s, job, EPI_GELU_MUL));
         } else {
             G4_TRY(matmul(c, c.hidden, G4_PLE, L.ple_gate, n));
             launch_geglu(s, c.hidden, c.ple + (size_t)l * G4_PLE, n, G4_PLE, ple_width, c.gelu,
                          c.gelu_size, c.gelu_lower, c.gelu_upper);
             launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_PLE / 64);
-            G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.ple_proj, n));
         }
+        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.ple_proj, n, one || gemm_fused));
         if (fused) {
             if (l + 1 < G4_LAYERS)  // + the next layer's input norm and quantize
-                launch_row_tail(s, p_out, L.post_ple_ln, c.residual, L.layer_scalar,
+                launch_row_tail(s, c.hidden, L.post_ple_ln, c.residual, L.layer_scalar,
                                 c.layers[l + 1].input_ln, nullptr, c.q8, c.qs, 1e-6f, n, 1, 1, 1, 1);
             else
-                launch_row_tail(s, p_out, L.post_ple_ln, c.residual, L.layer_scalar, nullptr,
+                launch_row_tail(s, c.hidden, L.post_ple_ln, c.residual, L.layer_scalar, nullptr,
                                 nullptr, nullptr, nullptr, 1e-6f, n, 1, 1, 0, 0);
         } else {
             launch_rmsnorm(s, c.hidden, c.hidden, L.post_ple_ln, G4_HIDDEN, 1e-6f, n);

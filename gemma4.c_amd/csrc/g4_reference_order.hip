@@ -1197,7 +1197,8 @@ __global__ __launch_bounds__(64) void k_attn_values_decode(float *__restrict__ o
 
 int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
                             const float *value_cache, int cache_len, int head_dim, int heads,
-                            int full, int start_pos, const int *pos_dev, size_t n) {
+                            int full, int start_pos, const int *pos_dev, size_t n, int8_t *q8,
+                            float *qs) {
     if (!n) return G4_OK;
     if (heads != 8) return set_error(G4_ERR_ARG, "reference-order attention needs 8 query heads");
     if (pos_dev && n != 1) return set_error(G4_ERR_ARG, "device-side positions are for one token");
@@ -1241,7 +1242,7 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
                            scores, heads, full, start_pos, pos_dev, stride);
     }
     const unsigned slices = (unsigned)(head_dim / 64);
-    if (n <= 4) {  // decode: one wave per (16 channels, 4 heads, token), deep prefetch
+    if (n <= 4) {  // decode: a wave per (16 channels, 4 heads, token), deep prefetch
         dim3 grid((unsigned)(head_dim / 16), 2, nn);
         if (head_dim == 256)
             hipLaunchKernelGGL((k_attn_values_decode<256, 8>), grid, dim3(64), 0, s, out, scores,
@@ -1258,18 +1259,21 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
             hipLaunchKernelGGL((k_attn_values<512, 4, 8, 2>), grid, dim3(256), 0, s, out, scores,
                                value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride);
     }
+    if (q8) launch_quantize(s, q8, qs, out, n * heads * head_dim / 64);
     return G4_OK;
 }
 
 int launch_attend(hipStream_t s, float *out, const float *q, const float *key_cache,
                   const float *value_cache, int cache_len, int head_dim, int heads, int full,
-                  int start_pos, const int *pos_dev, size_t n) {
+                  int start_pos, const int *pos_dev, size_t n, int8_t *q8, float *qs) {
     if (g_order == G4_ORDER_REFERENCE)
         return launch_attend_reference(s, out, q, key_cache, value_cache, cache_len, head_dim,
-                                       heads, full, start_pos, pos_dev, n);
+                                       heads, full, start_pos, pos_dev, n, q8, qs);
     if (pos_dev) return set_error(G4_ERR_ARG, "device-side positions need reference order");
-    return launch_attend_parallel(s, out, q, key_cache, value_cache, cache_len, head_dim, heads,
-                                  full, start_pos, n);
+    const int rc = launch_attend_parallel(s, out, q, key_cache, value_cache, cache_len, head_dim,
+                                          heads, full, start_pos, n);
+    if (!rc && q8) launch_quantize(s, q8, qs, out, n * heads * head_dim / 64);
+    return rc;
 }
 
 }  // namespace g4
