@@ -634,9 +634,10 @@ __global__ __launch_bounds__(256) void k_gemm_bg(float *__restrict__ out, size_t
 
 // Prefill W8A8 GEMM with every operand brought into LDS by the gfx950 LDS-DMA
 // loads (global_load_lds): no registers hold tiles in flight, and the number
-// of vector-memory instructions -- what bounds this kernel -- is kept low:
-// each wave issues two 1-KB loads per group, plus one 1-KB load of scales
-// every 8 groups.  64 x 64 outputs per 256-thread block (2 x 2 waves of
+// of vector-memory instructions is kept low: each wave issues two 1-KB loads
+// per group (three with a second B operand), plus one 1-KB load of scales
+// every 8 groups.  Four LDS stages: group g is read while groups g + 1 ..
+// g + 3 are in flight.  64 x 64 outputs per 256-thread block (2 x 2 waves of
 // 32 x 32), one 64-deep K step per quantization group, the group-ordered fp32
 // fold of the reference (bit-identical).  Requires groups % 8 == 0.
 //   A  64 rows x 64 B per group: wave w fetches rows 16w .. 16w + 15, lane L
@@ -648,7 +649,8 @@ __global__ __launch_bounds__(256) void k_gemm_bg(float *__restrict__ out, size_t
 //      a lane's operand are conflict free;
 //   scales, per 8 groups: waves 0, 1 fetch the activation scales of groups
 //      0-3, 4-7 (16 bytes per row), wave 2 the weight scales of the 4 tiles
-//      (256 bytes per tile), wave 3 repeats wave 2 into padding.
+//      (256 bytes per tile), wave 3 the second B operand's (or repeats
+//      wave 2's into padding).
 // k-slots: lane (l%16, l/16) covers k = 16 (l/16) + 0..15 -- for B that is
 // chunks 4 (l/16) .. + 3 of weight row l%16.
 template <int EPI>
@@ -749,13 +751,26 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
     struct Frags {
         v4i a[2], b[NB][NI];
     };
+    // activation scales of 4 groups per row, one 16-byte read per row every
+    // 4 groups
+    float4 xs4[2][4];
     auto fetch = [&](const Stage &d, const Scales &s, int j, Frags &f, Dots &o)
                      __attribute__((always_inline)) {
+        if ((j & 3) == 0) {
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    xs4[mi][v] = *reinterpret_cast<const float4 *>(&s.x[j >> 2][wm * 32 + mi * 16 + 4 * q + v][0]);
+        }
 #pragma unroll
         for (int mi = 0; mi < 2; mi++) {
             f.a[mi] = *reinterpret_cast<const v4i *>(d.a + a_off[mi]);
 #pragma unroll
-            for (int v = 0; v < 4; v++) o.x[mi][v] = s.x[j >> 2][wm * 32 + mi * 16 + 4 * q + v][j & 3];
+            for (int v = 0; v < 4; v++) {
+                const float4 x4 = xs4[mi][v];
+                o.x[mi][v] = (j & 3) == 0 ? x4.x : (j & 3) == 1 ? x4.y : (j & 3) == 2 ? x4.z : x4.w;
+            }
         }
 #pragma unroll
         for (int ob = 0; ob < NB; ob++)
@@ -788,23 +803,23 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
                                                   acc[ob][mi][ni][v]);
     };
 
-    // Step g (j = g % 8): issue group g + 2 into the stage of group g - 2
-    // (whose reads every wave finished before the previous barrier), plus the
-    // next chunk's scales when g + 2 starts one; wait until group g (and its
-    // chunk's scales) has landed -- the loads of groups g + 1, g + 2 may still
-    // be in flight -- and let the barrier publish it; then read its operands,
-    // fold group g - 1 and issue group g's MFMAs.
+    // Step g (j = g % 8): wait until group g (and its chunk's scales) has
+    // landed -- groups g + 1, g + 2 may still be in flight -- and let the
+    // barrier publish it; then issue group g + 3 into the stage of group g - 1
+    // (every wave finished reading it before the barrier), plus the next
+    // chunk's scales when g + 3 starts one; read group g's operands, fold
+    // group g - 1 and issue group g's MFMAs.
     auto step = [&](int g, int j, Stage &fill, const Stage &use, const Scales &sc_use,
                     Scales &sc_fill, Dots &cur, const Dots &prev) __attribute__((always_inline)) {
-        issue(g + 2, fill);
-        if (j == 6) issue_scales(g / 8 + 1, sc_fill);
-        // groups g + 1 and g + 2 (1 + NB loads each) may still be in flight,
-        // and at j = 6, 7 the next chunk's scales as well
+        // in flight: groups g + 1, g + 2 (1 + NB loads each), and at j = 6, 7
+        // the next chunk's scales (issued after group g + 1 or g + 2)
         if (j == 6 || j == 7)
             __builtin_amdgcn_s_waitcnt(0xF70 | (2 * (1 + NB) + 1));
         else
             __builtin_amdgcn_s_waitcnt(0xF70 | (2 * (1 + NB)));
         __builtin_amdgcn_s_barrier();
+        issue(g + 3, fill);
+        if (j == 5) issue_scales(g / 8 + 1, sc_fill);
         Frags f;
         fetch(use, sc_use, j, f, cur);  // LDS reads in flight ...
         __builtin_amdgcn_sched_barrier(0);
@@ -828,17 +843,18 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
     issue(0, st0);
     issue_scales(0, sc0);
     issue(1, st1);
+    issue(2, st2);
     // 16 groups per pass so that every stage and scale buffer is a fixed
     // object (chunk c = g / 8 lives in sc0 for even c, sc1 for odd c)
     auto eight = [&](int g, Scales &sc_use, Scales &sc_next) __attribute__((always_inline)) {
-        step(g + 0, 0, st2, st0, sc_use, sc_next, d0, d1);
-        step(g + 1, 1, st3, st1, sc_use, sc_next, d1, d0);
-        step(g + 2, 2, st0, st2, sc_use, sc_next, d0, d1);
-        step(g + 3, 3, st1, st3, sc_use, sc_next, d1, d0);
-        step(g + 4, 4, st2, st0, sc_use, sc_next, d0, d1);
-        step(g + 5, 5, st3, st1, sc_use, sc_next, d1, d0);
-        step(g + 6, 6, st0, st2, sc_use, sc_next, d0, d1);
-        step(g + 7, 7, st1, st3, sc_use, sc_next, d1, d0);
+        step(g + 0, 0, st3, st0, sc_use, sc_next, d0, d1);
+        step(g + 1, 1, st0, st1, sc_use, sc_next, d1, d0);
+        step(g + 2, 2, st1, st2, sc_use, sc_next, d0, d1);
+        step(g + 3, 3, st2, st3, sc_use, sc_next, d1, d0);
+        step(g + 4, 4, st3, st0, sc_use, sc_next, d0, d1);
+        step(g + 5, 5, st0, st1, sc_use, sc_next, d1, d0);
+        step(g + 6, 6, st1, st2, sc_use, sc_next, d0, d1);
+        step(g + 7, 7, st2, st3, sc_use, sc_next, d1, d0);
     };
     int g = 0;
     for (; g + 16 <= groups; g += 16) {
