@@ -728,50 +728,68 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     }
     __syncthreads();
     const int m = lane & 15, kg = lane >> 4;
+    // A 16-lane group takes KG keys at once, so each q value read from LDS
+    // feeds KG fmas (one key per group would make the kernel LDS-bound).
+    constexpr int KG = HD == 256 ? 4 : 2, KSTEP = 16 * KG;  // keys per block pass
     // key blocks blockIdx.x, blockIdx.x + gridDim.x, ... (one per block when
     // the grid spans the keys; a fixed grid strides when the position is read
     // from the device)
     for (int kbase = kfirst + blockIdx.x * 64; kbase <= pos_last; kbase += gridDim.x * 64)
-    for (int kk = wave * 4 + kg; kk < 64; kk += 16) {
-        const int p = kbase + kk;
-        if (p > pos_last) break;  // uniform within the 16-lane group
-        const float *kr = key_cache + (size_t)(p & mask) * HD + m;
-        float kv[S];
+    for (int k0 = (wave * 4 + kg) * KG; k0 < 64; k0 += KSTEP) {
+        if (kbase + k0 > pos_last) break;  // uniform within the 16-lane group
+        float kv[KG][S];
 #pragma unroll
-        for (int s = 0; s < S; s++) kv[s] = kr[16 * s];
-        // The 8 heads of a token are 8 independent chains: interleaving them
-        // hides the fma latency.
+        for (int i = 0; i < KG; i++) {
+            const int p = min(kbase + k0 + i, pos_last);  // past the end: a valid row, not written
+            const float *kr = key_cache + (size_t)(p & mask) * HD + m;
+#pragma unroll
+            for (int s = 0; s < S; s++) kv[i][s] = kr[16 * s];
+        }
+        // The 8 heads x KG keys of a token are independent chains:
+        // interleaving them hides the fma latency.
         for (int tt = 0; tt < tn; tt++) {
             const int t = t0 + tt, pos = start_pos + t, first = first_visible(pos, full);
-            float acc[8];
+            float acc[8][KG];
 #pragma unroll
-            for (int h = 0; h < 8; h++) acc[h] = 0.0f;
+            for (int h = 0; h < 8; h++)
+#pragma unroll
+                for (int i = 0; i < KG; i++) acc[h][i] = 0.0f;
 #pragma unroll
             for (int s4 = 0; s4 < S / 4; s4++) {
 #pragma unroll
                 for (int h = 0; h < 8; h++) {
                     const float4 qq = reinterpret_cast<const float4 *>(s_q[tt * 8 + h][m])[s4];
-                    acc[h] = fmaf(qq.x, kv[4 * s4 + 0], acc[h]);
-                    acc[h] = fmaf(qq.y, kv[4 * s4 + 1], acc[h]);
-                    acc[h] = fmaf(qq.z, kv[4 * s4 + 2], acc[h]);
-                    acc[h] = fmaf(qq.w, kv[4 * s4 + 3], acc[h]);
+#pragma unroll
+                    for (int i = 0; i < KG; i++) {
+                        acc[h][i] = fmaf(qq.x, kv[i][4 * s4 + 0], acc[h][i]);
+                        acc[h][i] = fmaf(qq.y, kv[i][4 * s4 + 1], acc[h][i]);
+                        acc[h][i] = fmaf(qq.z, kv[i][4 * s4 + 2], acc[h][i]);
+                        acc[h][i] = fmaf(qq.w, kv[i][4 * s4 + 3], acc[h][i]);
+                    }
                 }
             }
             // the reference's tree: (l, l+8), then (l, l+4), then
             // (0+2) + (1+3); DPP row shifts stay inside each 16-lane group
 #pragma unroll
-            for (int h = 0; h < 8; h++) {
-                float a = acc[h];
-                a += row_shl<8>(a);
-                a += row_shl<4>(a);
-                a += row_shl<2>(a);
-                a += row_shl<1>(a);
-                acc[h] = a;
-            }
-            if (m == 0 && p >= first && p <= pos) {
-                float *dst = scores + (size_t)t * 8 * stride + (p - first);
+            for (int h = 0; h < 8; h++)
 #pragma unroll
-                for (int h = 0; h < 8; h++) dst[(size_t)h * stride] = acc[h];
+                for (int i = 0; i < KG; i++) {
+                    float a = acc[h][i];
+                    a += row_shl<8>(a);
+                    a += row_shl<4>(a);
+                    a += row_shl<2>(a);
+                    a += row_shl<1>(a);
+                    acc[h][i] = a;
+                }
+            if (m == 0) {
+#pragma unroll
+                for (int i = 0; i < KG; i++) {
+                    const int p = kbase + k0 + i;
+                    if (p < first || p > pos) continue;
+                    float *dst = scores + (size_t)t * 8 * stride + (p - first);
+#pragma unroll
+                    for (int h = 0; h < 8; h++) dst[(size_t)h * stride] = acc[h][i];
+                }
             }
         }
     }
