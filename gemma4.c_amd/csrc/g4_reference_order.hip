@@ -706,6 +706,34 @@ __device__ __forceinline__ float row_shl(float x) {
 // 16-lane group keeps its key's channel slice in registers and reads the query
 // rows from LDS, stored [row][m][s] (padded) so a lane's chain is contiguous
 // (16-byte LDS loads, bank-conflict free).  scores[(t * 8 + h) * stride + (p - first(t))] for key position p.
+// x[0..C) in every lane of a 16-lane row; partner = lane ^ D.  Afterwards
+// x[0..C/2) holds x[j] + partner's x[j] for the half of the indices this lane
+// keeps: the lower half if bit D of the lane is clear, else the upper half.
+template <int D>
+__device__ __forceinline__ float row_xor(float v) {
+    if constexpr (D == 8) {  // row_ror:8
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+    } else if constexpr (D == 4) {  // row_ror:4 reaches l - 4, row_ror:12 reaches l + 4
+        const float down = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xf, 0xf, false));
+        const float up = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x12c, 0xf, 0xf, false));
+        return (threadIdx.x & 4) ? down : up;
+    } else if constexpr (D == 2) {  // quad_perm [2, 3, 0, 1]
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, false));
+    } else {  // quad_perm [1, 0, 3, 2]
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, false));
+    }
+}
+template <int C, int D, int N>
+__device__ __forceinline__ void butterfly_level(float (&x)[N], int lane16) {
+    const bool upper = lane16 & D;
+#pragma unroll
+    for (int j = 0; j < C / 2; j++) {
+        const float lo = x[j], hi = x[j + C / 2];
+        const float keep = upper ? hi : lo, give = upper ? lo : hi;
+        x[j] = keep + row_xor<D>(give);
+    }
+}
+
 template <int HD, int TQ>
 __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q,
                                                      const float *__restrict__ key_cache,
@@ -768,28 +796,26 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
                     }
                 }
             }
-            // the reference's tree: (l, l+8), then (l, l+4), then
-            // (0+2) + (1+3); DPP row shifts stay inside each 16-lane group
+            // The reference's tree over the 16 lanes -- (l, l+8), then
+            // (l, l+4), then (0+2) + (1+3) -- as a transposing butterfly: at
+            // each level a lane adds its partner's (lane ^ d) partial sums of
+            // one half of the scores and keeps that half, so the same pairs are
+            // added (fp addition is commutative) and lane l ends with scores
+            // V l / 16 .. of the list v = h KG + i, all lanes storing.
+            constexpr int V = 8 * KG;
+            float x[V];
 #pragma unroll
             for (int h = 0; h < 8; h++)
 #pragma unroll
-                for (int i = 0; i < KG; i++) {
-                    float a = acc[h][i];
-                    a += row_shl<8>(a);
-                    a += row_shl<4>(a);
-                    a += row_shl<2>(a);
-                    a += row_shl<1>(a);
-                    acc[h][i] = a;
-                }
-            if (m == 0) {
+                for (int i = 0; i < KG; i++) x[h * KG + i] = acc[h][i];
+            butterfly_level<V, 8>(x, m);
+            butterfly_level<V / 2, 4>(x, m);
+            butterfly_level<V / 4, 2>(x, m);
+            butterfly_level<V / 8, 1>(x, m);
 #pragma unroll
-                for (int i = 0; i < KG; i++) {
-                    const int p = kbase + k0 + i;
-                    if (p < first || p > pos) continue;
-                    float *dst = scores + (size_t)t * 8 * stride + (p - first);
-#pragma unroll
-                    for (int h = 0; h < 8; h++) dst[(size_t)h * stride] = acc[h][i];
-                }
+            for (int j = 0; j < V / 16; j++) {
+                const int v = (V / 16) * m + j, h = v / KG, p = kbase + k0 + v % KG;
+                if (p >= first && p <= pos) scores[((size_t)t * 8 + h) * stride + (p - first)] = x[j];
             }
         }
     }
