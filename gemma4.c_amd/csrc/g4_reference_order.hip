@@ -981,6 +981,22 @@ __global__ __launch_bounds__(64) void k_softmax_rows(float *values, int count, s
     softmax_row_reference(values + (size_t)blockIdx.x * stride, count);
 }
 
+// o = fma(p from lane J of this lane's 16-lane row, v, o): one VALU
+// instruction, the broadcast being the fma's DPP source operand.  The caller
+// issues s_nop 1 first when p may have been written by the VALU within the
+// two preceding instructions (the DPP source read hazard).
+#define G4_FMA_ROW_BROADCAST(J)                                                            \
+    __device__ __forceinline__ void fma_row_broadcast_##J(float &o, float p, float v) {     \
+        asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:" #J " row_mask:0xf bank_mask:0xf" \
+                     : "+v"(o)                                                              \
+                     : "v"(p), "v"(v));                                                     \
+    }
+G4_FMA_ROW_BROADCAST(0) G4_FMA_ROW_BROADCAST(1) G4_FMA_ROW_BROADCAST(2) G4_FMA_ROW_BROADCAST(3)
+G4_FMA_ROW_BROADCAST(4) G4_FMA_ROW_BROADCAST(5) G4_FMA_ROW_BROADCAST(6) G4_FMA_ROW_BROADCAST(7)
+G4_FMA_ROW_BROADCAST(8) G4_FMA_ROW_BROADCAST(9) G4_FMA_ROW_BROADCAST(10) G4_FMA_ROW_BROADCAST(11)
+G4_FMA_ROW_BROADCAST(12) G4_FMA_ROW_BROADCAST(13) G4_FMA_ROW_BROADCAST(14) G4_FMA_ROW_BROADCAST(15)
+#undef G4_FMA_ROW_BROADCAST
+
 // out[t][h][d] = fma chain over keys in order (gemma4.c:296-307): one lane
 // per output channel and (token, head) chain.  A block takes a 64-channel
 // slice for WAVES waves; wave w runs the chains of token t0 + w / (8 / HPW)
@@ -1072,19 +1088,32 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
         if (k_lo < 0) k_lo = 0;
         if (k_hi > 64) k_hi = 64;
         if (k_lo == 0 && k_hi == 64) {
-            const float4 *vr = reinterpret_cast<const float4 *>(s_v[lane]);
-#pragma unroll 4
-            for (int k4 = 0; k4 < 16; k4++) {
-                const float4 v4 = vr[k4];
+            // V of this lane's channel for the 64 keys; probabilities laid out
+            // for a DPP row broadcast: pr[e][c] in lane 16 r + j is key 16 c + j
+            // of head h0 + e, the same in every row, so the fma reads key
+            // 16 c + J of every row's lane J.  The HPW chains of a lane
+            // alternate, so consecutive fmas are independent.
+            typedef float f4 __attribute__((ext_vector_type(4)));
+            f4 v4[16];
+            const f4 *vr = reinterpret_cast<const f4 *>(s_v[lane]);
 #pragma unroll
-                for (int e = 0; e < HPW; e++) {
-                    const float4 p4 = reinterpret_cast<const float4 *>(s_p[wave][e])[k4];
-                    o[e] = fmaf(p4.x, v4.x, o[e]);
-                    o[e] = fmaf(p4.y, v4.y, o[e]);
-                    o[e] = fmaf(p4.z, v4.z, o[e]);
-                    o[e] = fmaf(p4.w, v4.w, o[e]);
-                }
+            for (int k4 = 0; k4 < 16; k4++) v4[k4] = vr[k4];
+            float pr[HPW][4];
+#pragma unroll
+            for (int e = 0; e < HPW; e++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) pr[e][c] = s_p[wave][e][16 * c + (lane & 15)];
+#define G4_KEY(J)                                                                   \
+    {                                                                               \
+        const float vv = v4[4 * c + (J) / 4][(J) % 4];                              \
+        _Pragma("unroll") for (int e = 0; e < HPW; e++) fma_row_broadcast_##J(o[e], pr[e][c], vv); \
+    }
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                G4_KEY(0) G4_KEY(1) G4_KEY(2) G4_KEY(3) G4_KEY(4) G4_KEY(5) G4_KEY(6) G4_KEY(7)
+                G4_KEY(8) G4_KEY(9) G4_KEY(10) G4_KEY(11) G4_KEY(12) G4_KEY(13) G4_KEY(14) G4_KEY(15)
             }
+#undef G4_KEY
         } else {
             for (int k = k_lo; k < k_hi; k++) {
                 const float vv = s_v[lane][k];
@@ -1117,21 +1146,6 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
 // all of them countable by vmcnt).  Keys past the row's end (in the last tile
 // and in padding steps) get probability 0 and a valid V row, and
 // fma(0, v, o) = o exactly (o is never -0), so every tile is whole.
-// o = fma(p from lane J of this lane's 16-lane row, v, o): one VALU
-// instruction, the broadcast being the fma's DPP source operand.  The caller
-// issues s_nop 1 first when p may have been written by the VALU within the
-// two preceding instructions (the DPP source read hazard).
-#define G4_FMA_ROW_BROADCAST(J)                                                            \
-    __device__ __forceinline__ void fma_row_broadcast_##J(float &o, float p, float v) {     \
-        asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:" #J " row_mask:0xf bank_mask:0xf" \
-                     : "+v"(o)                                                              \
-                     : "v"(p), "v"(v));                                                     \
-    }
-G4_FMA_ROW_BROADCAST(0) G4_FMA_ROW_BROADCAST(1) G4_FMA_ROW_BROADCAST(2) G4_FMA_ROW_BROADCAST(3)
-G4_FMA_ROW_BROADCAST(4) G4_FMA_ROW_BROADCAST(5) G4_FMA_ROW_BROADCAST(6) G4_FMA_ROW_BROADCAST(7)
-G4_FMA_ROW_BROADCAST(8) G4_FMA_ROW_BROADCAST(9) G4_FMA_ROW_BROADCAST(10) G4_FMA_ROW_BROADCAST(11)
-G4_FMA_ROW_BROADCAST(12) G4_FMA_ROW_BROADCAST(13) G4_FMA_ROW_BROADCAST(14) G4_FMA_ROW_BROADCAST(15)
-#undef G4_FMA_ROW_BROADCAST
 
 template <int HD, int DEPTH>
 __global__ __launch_bounds__(64) void k_attn_values_decode(float *__restrict__ out,
