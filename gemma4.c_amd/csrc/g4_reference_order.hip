@@ -1035,14 +1035,17 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
     const int my_keys = my_pos - my_first + 1;
     const float *prow = probs + ((size_t)ld_t * 8 + h0) * stride;
 
-    // V tile loader: thread covers float4 (key kr, channels 4 cc .. 4 cc + 3)
+    // V tile loader: thread (kq, cc) covers keys 4 kq .. 4 kq + 3 of channels
+    // d0 + 4 cc .. + 3, stored transposed as four 16-byte rows (bank-conflict
+    // free: the 8 lanes of an LDS cycle write 8 different key quads)
+    static_assert(F4 == 4 && THREADS == 256, "one key quad x channel quad per thread");
+    const int kq = tid & 15, cc = tid >> 4;
     auto load_tile = [&](int tile, float4 (&r)[F4]) {
 #pragma unroll
         for (int i = 0; i < F4; i++) {
-            const int idx = i * THREADS + tid, kr = idx >> 4, cc = idx & 15;
             // keys past the block's last position are never consumed; loading a
             // valid row instead keeps the loads unconditional (no drain)
-            const int p = min(kfirst + tile * 64 + kr, pos_last);
+            const int p = min(kfirst + tile * 64 + 4 * kq + i, pos_last);
             r[i] = *reinterpret_cast<const float4 *>(value_cache + (size_t)(p & mask) * HD + d0 + 4 * cc);
         }
     };
@@ -1069,14 +1072,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
     // DEPTH so every slot index is a compile-time constant (precise waits).
     auto step = [&](int tile, float4 (&slot)[F4], float (&pslot)[HPW]) {
         __syncthreads();  // previous tile fully consumed
-#pragma unroll
-        for (int i = 0; i < F4; i++) {
-            const int idx = i * THREADS + tid, kr = idx >> 4, cc = idx & 15;
-            s_v[4 * cc + 0][kr] = slot[i].x;
-            s_v[4 * cc + 1][kr] = slot[i].y;
-            s_v[4 * cc + 2][kr] = slot[i].z;
-            s_v[4 * cc + 3][kr] = slot[i].w;
-        }
+        *reinterpret_cast<float4 *>(&s_v[4 * cc + 0][4 * kq]) = make_float4(slot[0].x, slot[1].x, slot[2].x, slot[3].x);
+        *reinterpret_cast<float4 *>(&s_v[4 * cc + 1][4 * kq]) = make_float4(slot[0].y, slot[1].y, slot[2].y, slot[3].y);
+        *reinterpret_cast<float4 *>(&s_v[4 * cc + 2][4 * kq]) = make_float4(slot[0].z, slot[1].z, slot[2].z, slot[3].z);
+        *reinterpret_cast<float4 *>(&s_v[4 * cc + 3][4 * kq]) = make_float4(slot[0].w, slot[1].w, slot[2].w, slot[3].w);
 #pragma unroll
         for (int e = 0; e < HPW; e++) s_p[wave][e][lane] = pslot[e];
         load_tile(min(tile + DEPTH, tiles - 1), slot);  // unconditional refill
