@@ -1277,7 +1277,10 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
         const int tokens = (int)n < tq ? (int)n : tq;
         const int widest = full ? last_pos + 1 : G4_WINDOW - 1 + tokens;
         const int span = widest < last_pos + 1 ? widest : last_pos + 1;
-        return (unsigned)((span + 63) / 64);
+        const unsigned blocks = (unsigned)((span + 63) / 64);
+        // many tokens over a long context: a block strides over several key
+        // blocks, so its staged queries serve more keys
+        return n > 4 && blocks > 16 ? 16u : blocks;
     };
     const unsigned nn = (unsigned)n;
     if (head_dim == 256) {
