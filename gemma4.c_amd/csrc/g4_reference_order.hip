@@ -756,9 +756,9 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     }
     __syncthreads();
     const int m = lane & 15, kg = lane >> 4;
-    // A 16-lane group takes KG keys at once, so each q value read from LDS
-    // feeds KG fmas (one key per group would make the kernel LDS-bound).
-    constexpr int KG = HD == 256 ? 4 : 2, KSTEP = 16 * KG;  // keys per block pass
+    // A 16-lane group takes KG = 4 keys at once, so each q value read from LDS
+    // feeds 4 fmas (one key per group would make the kernel LDS-bound).
+    constexpr int KG = 4, KSTEP = 16 * KG;  // keys per block pass
     // key blocks blockIdx.x, blockIdx.x + gridDim.x, ... (one per block when
     // the grid spans the keys; a fixed grid strides when the position is read
     // from the device)
