@@ -396,8 +396,11 @@ __device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0,
         at_start = lane == i ? sv : at_start;
         sv += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(du), i));
         at_end = lane == i ? sv : at_end;
-        sv = sv * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fa), i)) +
-             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fb), i));  // two roundings
+        const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fb), i));
+        if constexpr (SPECIAL)  // s t + 1 at a new maximum, s + t (t * 1 exact) otherwise
+            sv = sv * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fa), i)) + b;
+        else
+            sv = sv + b;
     }
     const int e0 = biased_exponent(at_start), e1 = biased_exponent(at_end);
     const uint64_t bad = __ballot(lane < entries && nonempty &&
