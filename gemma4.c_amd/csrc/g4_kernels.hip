@@ -742,35 +742,24 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
 
     // A group's four MFMAs are issued together into their own registers and
     // folded one step later, while the next group's MFMAs run: the fold never
-    // waits on a fresh MFMA result.
+    // waits on a fresh MFMA result.  The fetch only issues LDS reads (scales
+    // stay raw: fp16 bits); every conversion happens in the next step's fold,
+    // so nothing in a step waits on its own reads before the fold.
     struct Dots {
         v4i d[NB][2][NI];
         float x[2][4];
-        float w[NB][NI];
+        uint16_t w[NB][NI];
     };
     struct Frags {
         v4i a[2], b[NB][NI];
     };
-    // activation scales of 4 groups per row, one 16-byte read per row every
-    // 4 groups
-    float4 xs4[2][4];
     auto fetch = [&](const Stage &d, const Scales &s, int j, Frags &f, Dots &o)
                      __attribute__((always_inline)) {
-        if ((j & 3) == 0) {
-#pragma unroll
-            for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-                for (int v = 0; v < 4; v++)
-                    xs4[mi][v] = *reinterpret_cast<const float4 *>(&s.x[j >> 2][wm * 32 + mi * 16 + 4 * q + v][0]);
-        }
 #pragma unroll
         for (int mi = 0; mi < 2; mi++) {
             f.a[mi] = *reinterpret_cast<const v4i *>(d.a + a_off[mi]);
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const float4 x4 = xs4[mi][v];
-                o.x[mi][v] = (j & 3) == 0 ? x4.x : (j & 3) == 1 ? x4.y : (j & 3) == 2 ? x4.z : x4.w;
-            }
+            for (int v = 0; v < 4; v++) o.x[mi][v] = s.x[j >> 2][wm * 32 + mi * 16 + 4 * q + v][j & 3];
         }
 #pragma unroll
         for (int ob = 0; ob < NB; ob++)
@@ -778,7 +767,7 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
             for (int ni = 0; ni < NI; ni++) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) f.b[ob][ni][i] = *reinterpret_cast<const int *>(d.b[ob] + b_off[ni][i]);
-                o.w[ob][ni] = half_bits_to_float(s.s[ob][wn * NI + ni][j][l16]);
+                o.w[ob][ni] = s.s[ob][wn * NI + ni][j][l16];
             }
     };
     auto multiply = [&](const Frags &f, Dots &o) __attribute__((always_inline)) {
@@ -799,7 +788,8 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
                 for (int mi = 0; mi < 2; mi++)
 #pragma unroll
                     for (int v = 0; v < 4; v++)
-                        acc[ob][mi][ni][v] = fmaf((float)o.d[ob][mi][ni][v], o.w[ob][ni] * o.x[mi][v],
+                        acc[ob][mi][ni][v] = fmaf((float)o.d[ob][mi][ni][v],
+                                                  half_bits_to_float(o.w[ob][ni]) * o.x[mi][v],
                                                   acc[ob][mi][ni][v]);
     };
 
@@ -836,7 +826,7 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
     for (int ob = 0; ob < NB; ob++)
 #pragma unroll
         for (int ni = 0; ni < NI; ni++) {
-            d1.w[ob][ni] = 0.0f;
+            d1.w[ob][ni] = 0;
 #pragma unroll
             for (int mi = 0; mi < 2; mi++) d1.d[ob][mi][ni] = zero;
         }
