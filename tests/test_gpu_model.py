@@ -122,6 +122,30 @@ def test_long_prefill_ring_wrap(pkg, model, image, oracle_lib):
     cpu.close()
 
 
+def test_teacher_forced_dump_2388(pkg, model, image, oracle_lib):
+    """The teacher-forced logit dump (gemma4.c:563-573 with dump on): 2388
+    random ids in 512-token chunks, every position's 262144 logits
+    (g4_logits_all, one batched lm_head per chunk) within 1e-3 of the
+    oracle's logits() for that row."""
+    cpu = oracle_lib.Model(image)
+    tokens = rng(67).integers(0, pkg.VOCAB, 2388).astype(np.int32)
+    worst, rows = 0.0, 0
+    for pos in range(0, len(tokens), 512):
+        chunk = tokens[pos:pos + 512]
+        gpu_forward(pkg, model, chunk, pos)
+        cpu.forward(chunk, pos)
+        dump = np.empty((len(chunk), pkg.VOCAB), np.float32)
+        pkg.check(model.g4_logits_all(dump.ctypes.data))
+        for r in range(len(chunk)):
+            err = float(np.abs(dump[r] - cpu.logits(r)).max())
+            assert err <= TOL, (pos + r, err)
+            worst = max(worst, err)
+            rows += 1
+    print(f"{rows} dumped rows within {worst:.3g} of the oracle")
+    assert rows == 2388
+    cpu.close()
+
+
 def test_logits_all_matches_rows(pkg, model):
     tokens = rng(61).integers(0, pkg.VOCAB, 24).astype(np.int32)
     gpu_forward(pkg, model, tokens, 0)
