@@ -258,6 +258,19 @@ def model_benchmarks(pkg, lib, np, steps: int, warmup: int) -> dict:
         pkg.check(lib.g4_logits(0, out.ctypes.data))
     res["decode16k_tok_s"] = 128 / (time.perf_counter() - s)
     log(f"decode @16K: {res['decode16k_tok_s']:.1f} tok/s")
+
+    # teacher-forced logit dump (gemma4.c:563-573 with dump on): 2388 ids in
+    # 512-token chunks, every position's logits to host memory (one batched
+    # lm_head per chunk)
+    t_dump = rng.integers(0, pkg.VOCAB, 2388).astype(np.int32)
+    dump = np.empty((512, pkg.VOCAB), np.float32)
+    s = time.perf_counter()
+    for pos in range(0, t_dump.size, 512):
+        chunk = t_dump[pos:pos + 512]
+        forward(chunk, pos)
+        pkg.check(lib.g4_logits_all(dump.ctypes.data))
+    res["dump2388_rows_s"] = t_dump.size / (time.perf_counter() - s)
+    log(f"teacher-forced dump of 2388 positions: {res['dump2388_rows_s']:.0f} rows/s")
     return res
 
 
@@ -363,6 +376,7 @@ def main() -> int:
         },
         "prefill8192_tok_s": round(res["prefill8192_tok_s"], 1),
         "decode16k_tok_s": round(res["decode16k_tok_s"], 2),
+        "dump2388_rows_s": round(res["dump2388_rows_s"], 1),
         "roofline": {
             "bound": "mfma",
             "kernel": "k_gemm (prefill W8A8 GEMM, X[512x1536] x W[6144x1536])",
