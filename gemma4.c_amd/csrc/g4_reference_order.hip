@@ -899,10 +899,13 @@ __device__ void softmax_row_reference(float *v, int count) {
 // one-wave kernel's bit for bit.
 
 // Which values a row holds: a fixed count, or an attention row (t, head)
-// whose visible keys follow from the position.
+// whose visible keys follow from the position.  pad64: the row's stride
+// leaves room to round the count up to a multiple of 64, and the values
+// between are written as 0 (the decode P.V kernel reads whole 64-key tiles).
 struct SoftmaxRows {
     int heads, full, start_pos, fixed_count;
     const int *pos_dev;
+    int pad64;
     __device__ __forceinline__ int count(int row) const {
         if (fixed_count > 0) return fixed_count;
         const int pos = (pos_dev ? *pos_dev : start_pos) + row / heads;
@@ -953,7 +956,8 @@ __global__ __launch_bounds__(64 * NW) void k_softmax_block(float *__restrict__ v
         sum = exact_sum_events<NW, J, true>(t, fresh, sum, sh);
         run_max = chunk_max;
     }
-    for (int i = T; i < count; i += 64 * NW) x[i] = expf_libm(x[i] - run_max) / sum;
+    const int end = spec.pad64 ? (count + 63) & ~63 : count;
+    for (int i = T; i < end; i += 64 * NW) x[i] = i < count ? expf_libm(x[i] - run_max) / sum : 0.0f;
 }
 
 // Softmax of `rows` rows (attention rows (t, head) or rows of a fixed count)
@@ -1137,122 +1141,155 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
 // P.V for one token (decode): one wave per block, four heads per wave.  Lane
 // 16 r + j runs the fma chain of head 4 g + r over channel c0 + j (block
 // (c0 / 16, g, token)), keys in order (gemma4.c:296-307).  Per 64-key tile
-// the wave stages V[64 keys][16 channels] in its own LDS, transposed to
-// [channel][key], so a lane reads four keys of its channel with one 16-byte
-// load; the four heads share it (the four lanes of a channel read the same
-// address).  Lane 16 r + j holds head 4 g + r's probabilities of keys
-// 4 j .. 4 j + 3 (one 16-byte load); key 4 J + e reaches every lane of row r
-// as the DPP source of its fma (component e, row_newbcast:J).  Per key a wave
-// spends one fma and a quarter of a 16-byte LDS read, with no barrier: tiles
-// are prefetched DEPTH ahead in registers by unconditional loads (5 per tile,
-// all of them countable by vmcnt).  Keys past the row's end (in the last tile
-// and in padding steps) get probability 0 and a valid V row, and
-// fma(0, v, o) = o exactly (o is never -0), so every tile is whole.
+// the wave stages V[64 keys][16 channels] in its own LDS as [channel][key]
+// rows, so a lane reads its channel with 16-byte loads; the four heads share
+// them (the four lanes of a channel read the same address).  Within a row
+// key 4 kq + i sits at position 16 i + kq: the loading lane's sixteen values
+// then go out as eight two-address writes with no register shuffling, and
+// column register m component u holds key 16 (m % 4) + 4 u + m / 4.  Lane
+// 16 r + j holds head 4 g + r's probabilities of keys 4 j .. 4 j + 3 (one
+// 16-byte load); key 4 J + e reaches every lane of row r as the DPP source of
+// its fma (component e, row_newbcast:J).  A tile's 64 fmas are one asm block:
+// nothing inside writes a DPP source, so they issue back to back.  With one
+// wave per SIMD every instruction costs the chain its issue slot, so loads
+// take at most one add of per-lane address arithmetic: V and the
+// probabilities are read through buffer descriptors.
+//   FULL (a global layer: keys 0 .. pos are cache rows 0 .. pos, no wrap):
+//   the V descriptor ends at row `keys`, so rows past the end read as 0.
+//   Sliding windows wrap around the ring; their keys are clamped to the last
+//   one (a valid row).
+// V is prefetched DEPTH tiles ahead, the probabilities DEPTH - 1, in register
+// rings by unconditional loads (5 per tile, all countable by vmcnt; past the
+// end the probability loads reread the last tile).  The softmax writes 0 for
+// the keys between the row's end and its last whole tile, fma(0, v, o) = o
+// exactly (o is never -0, v finite or 0), and steps past the last tile skip
+// the chain.
 
-template <int HD, int DEPTH>
+template <int HD, int DEPTH, bool FULL>
 __global__ __launch_bounds__(64) void k_attn_values_decode(float *__restrict__ out,
                                                            const float *__restrict__ probs,
                                                            const float *__restrict__ value_cache,
                                                            int cache_len, int full, int start_pos,
                                                            const int *__restrict__ pos_dev,
                                                            size_t stride) {
-    __shared__ __attribute__((aligned(16))) float s_v[2][16][68];  // [slot][channel][key]
+    __shared__ __attribute__((aligned(16))) float s_v[2][16][68];  // [slot][channel][position]
     if (pos_dev) start_pos = *pos_dev;
     const int lane = threadIdx.x, r = lane >> 4, j = lane & 15;
-    const int c0 = blockIdx.x * 16, head = 4 * blockIdx.y + r, t = blockIdx.z;
-    const int pos = start_pos + t, first = first_visible(pos, full);
+    const int c0 = blockIdx.x * 16, t = blockIdx.z;
+    const int pos = start_pos + t, first = FULL ? 0 : first_visible(pos, full);
     const int keys = pos - first + 1, tiles = (keys + 63) / 64, mask = cache_len - 1;
-    const float *prow = probs + ((size_t)t * 8 + head) * stride;
-    const int last4 = (int)stride - 4;  // the row holds `stride` floats
+    constexpr uint32_t ROW = HD * 4, TILE = 64 * ROW;  // bytes
     // V loads: lane (kq, cc) = (lane >> 2, lane & 3) takes keys 4 kq .. 4 kq + 3
     // of channels c0 + 4 cc .. + 3
     const int kq = lane >> 2, cc = lane & 3;
+    const uint32_t chan = (uint32_t)(c0 + 4 * cc) * 4;
+    const int v_rows = FULL ? min(keys, cache_len) : cache_len;
+    const __amdgpu_buffer_rsrc_t v_desc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(value_cache), 0, (int)((uint32_t)v_rows * ROW), 0x00020000);
+    // probabilities of heads 4 g .. 4 g + 3 (rows `stride` floats apart), up
+    // to the last tile of the fourth
+    const float *prows = probs + ((size_t)t * 8 + 4 * blockIdx.y) * stride;
+    const __amdgpu_buffer_rsrc_t p_desc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(prows), 0, (int)((3 * stride + (size_t)tiles * 64) * 4), 0x00020000);
+    const uint32_t p_lane = (uint32_t)((r * stride + 4 * j) * 4);
     typedef float f4 __attribute__((ext_vector_type(4)));  // SROA-friendly (HIP's float4 is not)
-    struct Stage {
+    struct VTile {
         f4 v[4];
-        f4 p;
     };
-    auto load_tile = [&](int tile, Stage &st) __attribute__((always_inline)) {
+    auto load16 = [](__amdgpu_buffer_rsrc_t d, uint32_t offset) __attribute__((always_inline)) {
+        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(d, offset, 0, 0));
+    };
+    auto load_v = [&](int tile, VTile &st) __attribute__((always_inline)) {
+        if constexpr (FULL) {
+            const uint32_t base = (uint32_t)(4 * kq) * ROW + chan + (uint32_t)tile * TILE;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int key = min(tile * 64 + 4 * kq + i, keys - 1);  // past the end: a valid row
-            st.v[i] = *reinterpret_cast<const f4 *>(value_cache + (size_t)((first + key) & mask) * HD +
-                                                    c0 + 4 * cc);
+            for (int i = 0; i < 4; i++) st.v[i] = load16(v_desc, base + i * ROW);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int key = min(tile * 64 + 4 * kq + i, keys - 1);
+                st.v[i] = load16(v_desc, (uint32_t)((first + key) & mask) * ROW + chan);
+            }
         }
-        st.p = *reinterpret_cast<const f4 *>(prow + min(tile * 64 + 4 * j, last4));  // masked at use
     };
-    auto masked = [&](int tile, f4 p) __attribute__((always_inline)) {
-        const int kb = tile * 64 + 4 * j;
-#pragma unroll
-        for (int e = 0; e < 4; e++) p[e] = kb + e < keys ? p[e] : 0.0f;
-        return p;
+    auto load_p = [&](int tile) __attribute__((always_inline)) {
+        return load16(p_desc, p_lane + (uint32_t)min(tile, tiles - 1) * 256);
     };
-    auto store_tile = [&](int slot, const Stage &st) __attribute__((always_inline)) {
+    auto store_v = [&](int slot, const VTile &st) __attribute__((always_inline)) {
+        float *row = &s_v[slot][4 * cc][kq];
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-            *reinterpret_cast<f4 *>(&s_v[slot][4 * cc + e][4 * kq]) =
-                f4{st.v[0][e], st.v[1][e], st.v[2][e], st.v[3][e]};
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) row[e * 68 + 16 * i] = st.v[i][e];
     };
     float o = 0.0f;
-    // keys 4 J .. 4 J + 3 of a tile: V column quad a, probabilities in row lane J
-#define G4_KEYS4(J)                                   \
-    {                                                 \
-        const f4 a = col[J];                          \
-        fma_row_broadcast_##J(o, p.x, a.x);           \
-        fma_row_broadcast_##J(o, p.y, a.y);           \
-        fma_row_broadcast_##J(o, p.z, a.z);           \
-        fma_row_broadcast_##J(o, p.w, a.w);           \
-    }
+    // The tile's 64 fmas, keys in order: key 4 J + e is p component e of row
+    // lane J times column register 4 e + J / 4, component J % 4 (asm operand
+    // 5 + 16 e + J).  s_nop 1 first: p may have been written by the VALU just
+    // before (the DPP source read hazard).
+#define G4_PV_FMA(J, E, C) \
+    "v_fmac_f32_dpp %0, %" #E ", %" #C " row_newbcast:" #J " row_mask:0xf bank_mask:0xf\n"
+#define G4_PV_KEYS(J, A, B, C, D) G4_PV_FMA(J, 1, A) G4_PV_FMA(J, 2, B) G4_PV_FMA(J, 3, C) G4_PV_FMA(J, 4, D)
+#define G4_PV_COL(M) "v"(col[M].x), "v"(col[M].y), "v"(col[M].z), "v"(col[M].w)
     auto chain64 = [&](const f4 (&col)[16], f4 p) __attribute__((always_inline)) {
-        // p is final before the nop: no VALU write of it within two instructions
-        // of a DPP read (the hazard is not checked across inline asm)
-        asm volatile("" : "+v"(p.x), "+v"(p.y), "+v"(p.z), "+v"(p.w));
-        asm volatile("s_nop 1");
-        G4_KEYS4(0) G4_KEYS4(1) G4_KEYS4(2) G4_KEYS4(3) G4_KEYS4(4) G4_KEYS4(5) G4_KEYS4(6)
-        G4_KEYS4(7) G4_KEYS4(8) G4_KEYS4(9) G4_KEYS4(10) G4_KEYS4(11) G4_KEYS4(12) G4_KEYS4(13)
-        G4_KEYS4(14) G4_KEYS4(15)
+        asm volatile("s_nop 1\n"
+                     G4_PV_KEYS(0, 5, 21, 37, 53) G4_PV_KEYS(1, 6, 22, 38, 54)
+                     G4_PV_KEYS(2, 7, 23, 39, 55) G4_PV_KEYS(3, 8, 24, 40, 56)
+                     G4_PV_KEYS(4, 9, 25, 41, 57) G4_PV_KEYS(5, 10, 26, 42, 58)
+                     G4_PV_KEYS(6, 11, 27, 43, 59) G4_PV_KEYS(7, 12, 28, 44, 60)
+                     G4_PV_KEYS(8, 13, 29, 45, 61) G4_PV_KEYS(9, 14, 30, 46, 62)
+                     G4_PV_KEYS(10, 15, 31, 47, 63) G4_PV_KEYS(11, 16, 32, 48, 64)
+                     G4_PV_KEYS(12, 17, 33, 49, 65) G4_PV_KEYS(13, 18, 34, 50, 66)
+                     G4_PV_KEYS(14, 19, 35, 51, 67) G4_PV_KEYS(15, 20, 36, 52, 68)
+                     : "+v"(o)
+                     : "v"(p.x), "v"(p.y), "v"(p.z), "v"(p.w), G4_PV_COL(0), G4_PV_COL(1),
+                       G4_PV_COL(2), G4_PV_COL(3), G4_PV_COL(4), G4_PV_COL(5), G4_PV_COL(6),
+                       G4_PV_COL(7), G4_PV_COL(8), G4_PV_COL(9), G4_PV_COL(10), G4_PV_COL(11),
+                       G4_PV_COL(12), G4_PV_COL(13), G4_PV_COL(14), G4_PV_COL(15));
     };
-#undef G4_KEYS4
-    Stage ring[DEPTH];
-    f4 p_cur;  // probabilities of the tile in LDS
-    {
-        Stage first_tile;
-        load_tile(0, first_tile);
+#undef G4_PV_COL
+#undef G4_PV_KEYS
+#undef G4_PV_FMA
+    // V of tile u in v_ring[u % DEPTH], its probabilities in p_ring[u % DEPTH]
+    VTile v_ring[DEPTH];
+    f4 p_ring[DEPTH];
 #pragma unroll
-        for (int s = 0; s < DEPTH; s++) load_tile(s + 1, ring[s]);
-        store_tile(0, first_tile);
-        p_cur = masked(0, first_tile.p);
+    for (int s = 0; s < DEPTH; s++) {
+        load_v(s, v_ring[s]);
+        p_ring[s] = load_p(s);
     }
-    // step: tile `tile` is in LDS slot tile & 1 (its probabilities in p_cur);
-    // its column is read, then the ring slot's tile + 1 goes to the other LDS
-    // slot (last read by tile - 1: a wave's LDS accesses complete in order) and
-    // the ring slot is refilled with tile + 1 + DEPTH.  always_inline: the
-    // ring must stay in registers.
-    auto step = [&](int tile, Stage &slot) __attribute__((always_inline)) {
+    store_v(0, v_ring[0]);
+    load_v(DEPTH, v_ring[0]);
+    // step s of a round (tile u = base + s, u % DEPTH = s): tile u is in LDS
+    // slot u & 1; its column is read, then tile u + 1 goes to the other slot
+    // (last read by tile u - 1: a wave's LDS accesses complete in order) and
+    // its ring slot is refilled with tile u + 1 + DEPTH; after the chain, p_ring[s]
+    // is refilled with tile u + DEPTH's probabilities.  always_inline: the
+    // rings must stay in registers.
+    auto step = [&](int tile, VTile &next, f4 &p) __attribute__((always_inline)) {
         f4 col[16];  // this lane's channel, the tile's 64 keys: all reads issued first
         const f4 *src = reinterpret_cast<const f4 *>(&s_v[tile & 1][j][0]);
 #pragma unroll
         for (int i = 0; i < 16; i++) col[i] = src[i];
-        store_tile((tile + 1) & 1, slot);
-        const f4 p_next = slot.p;
-        load_tile(tile + 1 + DEPTH, slot);  // unconditional: past the end, whole no-op tiles
-        chain64(col, p_cur);
-        p_cur = masked(tile + 1, p_next);
+        store_v((tile + 1) & 1, next);
+        load_v(tile + 1 + DEPTH, next);  // unconditional: past the end, valid memory
+        if (tile < tiles) chain64(col, p);
+        p = load_p(tile + DEPTH);
     };
     // The steps are written out (a dynamically indexed ring would live in
-    // scratch memory); steps past the last tile add nothing.
+    // scratch memory).
     static_assert(DEPTH == 8, "the steps below are written out for 8 ring slots");
     for (int tile = 0; tile < tiles; tile += DEPTH) {
-        step(tile + 0, ring[0]);
-        step(tile + 1, ring[1]);
-        step(tile + 2, ring[2]);
-        step(tile + 3, ring[3]);
-        step(tile + 4, ring[4]);
-        step(tile + 5, ring[5]);
-        step(tile + 6, ring[6]);
-        step(tile + 7, ring[7]);
+        step(tile + 0, v_ring[1], p_ring[0]);
+        step(tile + 1, v_ring[2], p_ring[1]);
+        step(tile + 2, v_ring[3], p_ring[2]);
+        step(tile + 3, v_ring[4], p_ring[3]);
+        step(tile + 4, v_ring[5], p_ring[4]);
+        step(tile + 5, v_ring[6], p_ring[5]);
+        step(tile + 6, v_ring[7], p_ring[6]);
+        step(tile + 7, v_ring[0], p_ring[7]);
     }
-    out[((size_t)t * 8 + head) * HD + c0 + j] = o;
+    out[((size_t)t * 8 + 4 * blockIdx.y + r) * HD + c0 + j] = o;
 }
 
 int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
@@ -1298,7 +1335,7 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
                            full, start_pos, (int)n, pos_dev, stride, scores);
     }
     if (n <= 4) {  // decode: few rows, a block per row
-        const SoftmaxRows spec{heads, full, start_pos, 0, pos_dev};
+        const SoftmaxRows spec{heads, full, start_pos, 0, pos_dev, 1};
         launch_softmax_block(s, scores, stride, max_keys, spec, (unsigned)(n * heads));
     } else {
         hipLaunchKernelGGL(k_attn_softmax_reference, dim3((unsigned)heads, nn), dim3(64), 0, s,
@@ -1307,12 +1344,17 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
     const unsigned slices = (unsigned)(head_dim / 64);
     if (n <= 4) {  // decode: a wave per (16 channels, 4 heads, token), deep prefetch
         dim3 grid((unsigned)(head_dim / 16), 2, nn);
-        if (head_dim == 256)
-            hipLaunchKernelGGL((k_attn_values_decode<256, 8>), grid, dim3(64), 0, s, out, scores,
-                               value_cache, cache_len, full, start_pos, pos_dev, stride);
-        else
-            hipLaunchKernelGGL((k_attn_values_decode<512, 8>), grid, dim3(64), 0, s, out, scores,
-                               value_cache, cache_len, full, start_pos, pos_dev, stride);
+#define G4_PV_DECODE(HD, FULL)                                                                    \
+    hipLaunchKernelGGL((k_attn_values_decode<HD, 8, FULL>), grid, dim3(64), 0, s, out, scores,     \
+                       value_cache, cache_len, full, start_pos, pos_dev, stride)
+        if (head_dim == 256) {
+            if (full) G4_PV_DECODE(256, true);
+            else G4_PV_DECODE(256, false);
+        } else {
+            if (full) G4_PV_DECODE(512, true);
+            else G4_PV_DECODE(512, false);
+        }
+#undef G4_PV_DECODE
     } else {  // prefill: 4 tokens x 8 heads per block share each V tile
         dim3 grid(slices, (nn + 3) / 4);
         if (head_dim == 256)
@@ -1355,7 +1397,7 @@ extern "C" int g4_softmax(void *stream, float *values, int count, size_t rows) {
     G4_CHECK(values && count > 0, "g4_softmax: bad arguments");
     if (!rows) return G4_OK;
     if (count > 1024 && rows <= 64) {  // few long rows: a block per row
-        const g4::SoftmaxRows spec{1, 1, 0, count, nullptr};
+        const g4::SoftmaxRows spec{1, 1, 0, count, nullptr, 0};
         g4::launch_softmax_block((hipStream_t)stream, values, (size_t)count, count, spec,
                                  (unsigned)rows);
     } else {

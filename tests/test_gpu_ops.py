@@ -300,6 +300,12 @@ ATTN_CASES = [
     (512, 4096, 1, 0, 16),
     (512, 4096, 1, 3000, 1),
     (512, 4096, 1, 1000, 64),
+    # decode (one to four tokens)
+    (512, 4096, 1, 63, 1),        # the row ends on a tile edge
+    (512, 4096, 1, 4, 3),         # under one tile, three tokens
+    (512, 4096, 1, 4095, 1),      # every cache row; prefetches run past the end of the cache
+    (256, 1024, 0, 100, 2),       # sliding window before it fills
+    (256, 1024, 0, 1019, 4),      # four tokens whose windows wrap the ring
 ]
 
 
