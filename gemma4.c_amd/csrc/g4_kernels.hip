@@ -18,6 +18,7 @@
 namespace g4 {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 // ---------------------------------------------------------------------------
 // Scratch
@@ -653,6 +654,15 @@ __global__ __launch_bounds__(256) void k_gemm_bg(float *__restrict__ out, size_t
 //      wave 2's into padding).
 // k-slots: lane (l%16, l/16) covers k = 16 (l/16) + 0..15 -- for B that is
 // chunks 4 (l/16) .. + 3 of weight row l%16.
+// The fold takes two VALU operations per output: the int8 MFMAs accumulate
+// onto the bits of 1.5 * 2^23, so the sum read as a float is 1.5 * 2^23 + dot
+// exactly (|dot| <= 64 * 127 * 127 < 2^22) and one subtraction recovers the
+// dot (half the cost of an int-to-float conversion); the scale products
+// xs[m] * ws[n] of the wave's four 16 x 16 tiles come from one fp32 MFMA with
+// K = 1 (16x16x1, four blocks), whose products are rounded exactly as a VALU
+// multiply, subnormals included.  Block b = 2 mi + ni takes its 16 row
+// scales and 16 column scales from lanes 16 b .. 16 b + 15, and its result
+// lands in the int8 MFMA's output layout (outputs 4 b .. 4 b + 3).
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_t out_stride,
                                                   const int8_t *__restrict__ xq,
@@ -680,7 +690,9 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1, q = lane >> 4, l16 = lane & 15;
-    const v4i zero = {0, 0, 0, 0};
+    constexpr int MAGIC = 0x4B400000;  // 1.5 * 2^23
+    const v4i magic = {MAGIC, MAGIC, MAGIC, MAGIC};
+    const v16f zero16 = {};
 
     // DMA sources (group 0, chunk 0); the builtin wants plain void pointers
     const int a_row = 16 * wave + (lane >> 2);
@@ -740,44 +752,44 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
 #pragma unroll
                 for (int v = 0; v < 4; v++) acc[o][i][j][v] = 0.0f;
 
-    // A group's four MFMAs are issued together into their own registers and
+    // A group's MFMAs are issued together into their own registers and
     // folded one step later, while the next group's MFMAs run: the fold never
-    // waits on a fresh MFMA result.  The fetch only issues LDS reads (scales
-    // stay raw: fp16 bits); every conversion happens in the next step's fold,
-    // so nothing in a step waits on its own reads before the fold.
+    // waits on a fresh MFMA result.  The fetch only issues LDS reads (the
+    // weight scale stays raw fp16 bits until the multiply step converts it).
+    static_assert(NI == 2, "the scale-product MFMA covers 2 x 2 tiles");
     struct Dots {
-        v4i d[NB][2][NI];
-        float x[2][4];
-        uint16_t w[NB][NI];
+        v4i d[NB][2][NI];  // 1.5 * 2^23 + dot, as int bits
+        v16f c[NB];        // xs * ws, tile (mi, ni) at outputs 4 (2 mi + ni) ..
     };
     struct Frags {
         v4i a[2], b[NB][NI];
+        float xs;          // row scale of lane l's block (tile row l / 32)
+        uint16_t ws[NB];   // column scale of lane l's block (tile column (l / 16) % 2)
     };
-    auto fetch = [&](const Stage &d, const Scales &s, int j, Frags &f, Dots &o)
-                     __attribute__((always_inline)) {
+    const int xs_row = wm * 32 + (lane >> 5) * 16 + l16, ws_tile = wn * NI + ((lane >> 4) & 1);
+    auto fetch = [&](const Stage &d, const Scales &s, int j, Frags &f) __attribute__((always_inline)) {
 #pragma unroll
-        for (int mi = 0; mi < 2; mi++) {
-            f.a[mi] = *reinterpret_cast<const v4i *>(d.a + a_off[mi]);
+        for (int mi = 0; mi < 2; mi++) f.a[mi] = *reinterpret_cast<const v4i *>(d.a + a_off[mi]);
+        f.xs = s.x[j >> 2][xs_row][j & 3];
 #pragma unroll
-            for (int v = 0; v < 4; v++) o.x[mi][v] = s.x[j >> 2][wm * 32 + mi * 16 + 4 * q + v][j & 3];
-        }
+        for (int ob = 0; ob < NB; ob++) {
 #pragma unroll
-        for (int ob = 0; ob < NB; ob++)
-#pragma unroll
-            for (int ni = 0; ni < NI; ni++) {
+            for (int ni = 0; ni < NI; ni++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) f.b[ob][ni][i] = *reinterpret_cast<const int *>(d.b[ob] + b_off[ni][i]);
-                o.w[ob][ni] = s.s[ob][wn * NI + ni][j][l16];
-            }
+            f.ws[ob] = s.s[ob][ws_tile][j][l16];
+        }
     };
     auto multiply = [&](const Frags &f, Dots &o) __attribute__((always_inline)) {
 #pragma unroll
-        for (int ob = 0; ob < NB; ob++)
+        for (int ob = 0; ob < NB; ob++) {
 #pragma unroll
             for (int ni = 0; ni < NI; ni++)
 #pragma unroll
                 for (int mi = 0; mi < 2; mi++)
-                    o.d[ob][mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[mi], f.b[ob][ni], zero, 0, 0, 0);
+                    o.d[ob][mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[mi], f.b[ob][ni], magic, 0, 0, 0);
+            o.c[ob] = __builtin_amdgcn_mfma_f32_16x16x1f32(f.xs, half_bits_to_float(f.ws[ob]), zero16, 0, 0, 0);
+        }
     };
     auto fold = [&](const Dots &o) __attribute__((always_inline)) {
 #pragma unroll
@@ -788,9 +800,8 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
                 for (int mi = 0; mi < 2; mi++)
 #pragma unroll
                     for (int v = 0; v < 4; v++)
-                        acc[ob][mi][ni][v] = fmaf((float)o.d[ob][mi][ni][v],
-                                                  half_bits_to_float(o.w[ob][ni]) * o.x[mi][v],
-                                                  acc[ob][mi][ni][v]);
+                        acc[ob][mi][ni][v] = fmaf(__int_as_float(o.d[ob][mi][ni][v]) - 12582912.0f,
+                                                  o.c[ob][4 * (2 * mi + ni) + v], acc[ob][mi][ni][v]);
     };
 
     // Step g (j = g % 8): wait until group g (and its chunk's scales) has
@@ -811,25 +822,24 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
         issue(g + 3, fill);
         if (j == 5) issue_scales(g / 8 + 1, sc_fill);
         Frags f;
-        fetch(use, sc_use, j, f, cur);  // LDS reads in flight ...
+        fetch(use, sc_use, j, f);       // LDS reads in flight ...
         __builtin_amdgcn_sched_barrier(0);
         fold(prev);                     // ... while group g - 1 is folded
         __builtin_amdgcn_sched_barrier(0);
         multiply(f, cur);               // results are folded one step later
+        // (kept here: moved past the next barrier, the MFMAs would sit right
+        // before the fold that reads them)
+        __builtin_amdgcn_sched_barrier(0);
     };
-    Dots d0, d1;  // d1 starts as zeros: fmaf(0, 0, acc) = acc
+    Dots d0, d1;  // d1 starts as dots 0, products 0: fmaf(0, 0, acc) = acc
 #pragma unroll
-    for (int mi = 0; mi < 2; mi++)
+    for (int ob = 0; ob < NB; ob++) {
+        d1.c[ob] = zero16;
 #pragma unroll
-        for (int v = 0; v < 4; v++) d1.x[mi][v] = 0.0f;
+        for (int ni = 0; ni < NI; ni++)
 #pragma unroll
-    for (int ob = 0; ob < NB; ob++)
-#pragma unroll
-        for (int ni = 0; ni < NI; ni++) {
-            d1.w[ob][ni] = 0;
-#pragma unroll
-            for (int mi = 0; mi < 2; mi++) d1.d[ob][mi][ni] = zero;
-        }
+            for (int mi = 0; mi < 2; mi++) d1.d[ob][mi][ni] = magic;
+    }
     issue(0, st0);
     issue_scales(0, sc0);
     issue(1, st1);
