@@ -132,6 +132,28 @@ def gemm_roofline(pkg, lib, torch) -> dict:
     return {"kernel": "k_gemm", "ms_per_launch": ms, "tops": tops, "bytes": moved, "ops": ops}
 
 
+def vendor_int8_gemm(torch, m: int = 512, n: int = 6144, k: int = 1536) -> dict:
+    """The vendor library's plain int8 GEMM on the same shape (hipBLASLt through
+    torch._int_mm: int32 output, no scales, no fold), timed the same way: a
+    reference point for what a 512-row GEMM reaches on this chip."""
+    copies = 8
+    try:
+        gen = torch.Generator(device="cuda").manual_seed(3)
+        a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device="cuda", generator=gen)
+        bs = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=gen)
+              for _ in range(copies)]
+
+        def launch(i):
+            torch._int_mm(a, bs[i % copies].t())
+
+        ms = graph_timed(torch, launch, 4 * copies, 10)
+    except Exception as ex:  # the comparison is optional
+        return {"error": str(ex)[:160]}
+    tops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    return {"library": "hipBLASLt via torch._int_mm (int32 out, no scales)", "us": round(ms * 1e3, 2),
+            "tops": round(tops, 1), "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4)}
+
+
 def probe(pkg, lib, torch, what: str, launches: int = 20) -> None:
     """Launch one kernel alone, for hardware-counter runs under rocprofv3 --pmc:
     `gemm` = the prefill GEMM above, `gemv` = the lm_head GEMV (262144 x 1536,
@@ -341,6 +363,8 @@ def main() -> int:
 
     gemm = gemm_roofline(pkg, lib, torch)
     log(f"prefill GEMM 512x6144x1536: {gemm['ms_per_launch'] * 1e3:.1f} us, {gemm['tops']:.0f} TOPS")
+    vendor = vendor_int8_gemm(torch)
+    log(f"vendor int8 GEMM, same shape: {vendor}")
     sweep = gemv_sweep(pkg, lib, torch)
     log(f"decode GEMV sweep: {sweep['byte_weighted_gbs']:.0f} GB/s byte-weighted; {sweep['per_shape']}")
     torch.cuda.empty_cache()
@@ -387,6 +411,8 @@ def main() -> int:
             "traffic": pmc_traffic("k_gemm_512x6144x1536_pmc.txt"),
             "algorithmic_bytes": gemm["bytes"],
             "traffic_source": "profiles/k_gemm_512x6144x1536_pmc.txt (HBM bytes per launch)",
+            "us_per_launch": round(gemm["ms_per_launch"] * 1e3, 2),
+            "vendor_int8_gemm_same_shape": vendor,
         },
         "roofline_decode": {
             "bound": "hbm",
