@@ -174,6 +174,14 @@ void launch_kv_finish(hipStream_t s, float *key_cache, float *value_cache, const
                       const float *v_new, const float *k_norm, const float *cosines,
                       const float *sines, int pairs, int head_dim, int cache_len, int start_pos,
                       const int *pos_dev, size_t n);
+// Reference order, one launch for the row-local tail of the attention
+// projections (gemma4.c:427-428, 437-440): rmsnorm + RoPE of every query head
+// in place, and, when k_new is set, launch_kv_finish's work on the new key and
+// value.  head_dim 256 or 512.
+void launch_qkv_finish(hipStream_t s, float *q, int heads, const float *q_norm, const float *k_new,
+                       const float *v_new, const float *k_norm, float *key_cache, float *value_cache,
+                       const float *cosines, const float *sines, int pairs, int head_dim,
+                       int cache_len, int start_pos, const int *pos_dev, size_t n);
 // gemma4.c:518-519: 30 * tanh(x / 30) in place.
 void launch_softcap(hipStream_t s, float *x, size_t n);
 // First index of the maximum (gemma4.c:537-541) of each of `rows` rows.

@@ -378,15 +378,20 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
         } else {
             G4_TRY(matmul(c, c.aux, qw, L.q, n));
         }
-        launch_rmsnorm(s, c.aux, c.aux, L.q_norm, hd, 1e-6f, (size_t)n * heads);
-        launch_rope(s, L.rope_cos, L.rope_sin, L.pairs, c.aux, heads, hd, start_pos, pos_dev, n);
-        if (L.k.data) {
-            if (!one) {
-                G4_TRY(matmul(c, c.k_new, hd, L.k, n));
-                G4_TRY(matmul(c, c.v_new, hd, L.v, n));
-            }
-            launch_kv_finish(s, keys, values, c.k_new, c.v_new, L.k_norm, L.rope_cos, L.rope_sin,
-                             L.pairs, hd, cache_len, start_pos, pos_dev, n);
+        if (L.k.data && !one) {
+            G4_TRY(matmul(c, c.k_new, hd, L.k, n));
+            G4_TRY(matmul(c, c.v_new, hd, L.v, n));
+        }
+        if (fused) {  // query norms + RoPE and the new key/value rows: one launch
+            launch_qkv_finish(s, c.aux, heads, L.q_norm, L.k.data ? c.k_new : nullptr, c.v_new,
+                              L.k_norm, keys, values, L.rope_cos, L.rope_sin, L.pairs, hd, cache_len,
+                              start_pos, pos_dev, n);
+        } else {
+            launch_rmsnorm(s, c.aux, c.aux, L.q_norm, hd, 1e-6f, (size_t)n * heads);
+            launch_rope(s, L.rope_cos, L.rope_sin, L.pairs, c.aux, heads, hd, start_pos, pos_dev, n);
+            if (L.k.data)
+                launch_kv_finish(s, keys, values, c.k_new, c.v_new, L.k_norm, L.rope_cos, L.rope_sin,
+                                 L.pairs, hd, cache_len, start_pos, pos_dev, n);
         }
         G4_TRY(launch_attend(s, c.hidden, c.aux, keys, values, cache_len, hd, heads, L.full,
                              start_pos, pos_dev, n, c.q8, c.qs));

@@ -1138,6 +1138,83 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
     }
 }
 
+// The row-local tail of the attention projections, one wave per row, in
+// reference order (gemma4.c:427-428 for the queries, 437-440 for a new key and
+// value): rmsnorm of each query head (q_norm) then RoPE in place; rmsnorm of
+// the new key (k_norm) then RoPE, and the weightless rmsnorm of the new value,
+// both written into the rings at (start_pos + t) & (cache_len - 1).  Block
+// (r, t): r < heads a query head of token t, r = heads its key, heads + 1 its
+// value.  Lane l holds elements J l .. J l + J - 1 (J = HD / 64); the sum of
+// squares is the sequential one (exact_sum_events on one wave), and element
+// e's RoPE partner e + HD / 2 sits in lane l + 32, same register.
+template <int HD>
+__global__ __launch_bounds__(64) void k_qkv_finish(float *q, int heads, const float *__restrict__ q_norm,
+                                                   const float *__restrict__ k_new,
+                                                   const float *__restrict__ v_new,
+                                                   const float *__restrict__ k_norm, float *key_cache,
+                                                   float *value_cache, const float *__restrict__ cosines,
+                                                   const float *__restrict__ sines, int pairs,
+                                                   int cache_len, int start_pos,
+                                                   const int *__restrict__ pos_dev) {
+    constexpr int J = HD / 64;
+    __shared__ EsumShared sh;
+    if (pos_dev) start_pos = *pos_dev;
+    const int r = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int pos = start_pos + t;
+    const bool is_q = r < heads, is_v = r == heads + 1;
+    const float *src = is_q ? q + ((size_t)t * heads + r) * HD : (is_v ? v_new : k_new) + (size_t)t * HD;
+    const float *weight = is_q ? q_norm : is_v ? nullptr : k_norm;
+    float x[J], w[J], sq[J];
+#pragma unroll
+    for (int i = 0; i < J; i += 4) {
+        const float4 a = *reinterpret_cast<const float4 *>(src + J * lane + i);
+        const float4 b = weight ? *reinterpret_cast<const float4 *>(weight + J * lane + i)
+                                : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        x[i] = a.x, x[i + 1] = a.y, x[i + 2] = a.z, x[i + 3] = a.w;
+        w[i] = b.x, w[i + 1] = b.y, w[i + 2] = b.z, w[i + 3] = b.w;
+    }
+#pragma unroll
+    for (int i = 0; i < J; i++) sq[i] = x[i] * x[i];
+    const float inverse = 1.0f / sqrtf(exact_sum_events<1, J, false>(sq, 0u, 0.0f, sh) / (float)HD + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < J; i++) x[i] = w[i] * (inverse * x[i]);
+    if (!is_v) {
+        const bool upper = lane >= 32;
+        const float *c = cosines + (size_t)pos * pairs, *sn = sines + (size_t)pos * pairs;
+#pragma unroll
+        for (int i = 0; i < J; i++) {
+            const float other = __shfl_xor(x[i], 32);
+            const int jj = J * (lane & 31) + i;  // the pair index
+            if (jj < pairs) {
+                const float cj = c[jj], sj = sn[jj];
+                // first = element jj (lower lane), second = jj + HD / 2 (upper lane)
+                x[i] = upper ? x[i] * cj + other * sj : x[i] * cj - other * sj;
+            }
+        }
+    }
+    float *dst = is_q ? q + ((size_t)t * heads + r) * HD
+                      : (is_v ? value_cache : key_cache) + (size_t)(pos & (cache_len - 1)) * HD;
+#pragma unroll
+    for (int i = 0; i < J; i += 4)
+        *reinterpret_cast<float4 *>(dst + J * lane + i) = make_float4(x[i], x[i + 1], x[i + 2], x[i + 3]);
+}
+
+void launch_qkv_finish(hipStream_t s, float *q, int heads, const float *q_norm, const float *k_new,
+                       const float *v_new, const float *k_norm, float *key_cache, float *value_cache,
+                       const float *cosines, const float *sines, int pairs, int head_dim,
+                       int cache_len, int start_pos, const int *pos_dev, size_t n) {
+    if (!n) return;
+    const dim3 grid((unsigned)(heads + (k_new ? 2 : 0)), (unsigned)n);
+    if (head_dim == 256)
+        hipLaunchKernelGGL(k_qkv_finish<256>, grid, dim3(64), 0, s, q, heads, q_norm, k_new, v_new,
+                           k_norm, key_cache, value_cache, cosines, sines, pairs, cache_len, start_pos,
+                           pos_dev);
+    else
+        hipLaunchKernelGGL(k_qkv_finish<512>, grid, dim3(64), 0, s, q, heads, q_norm, k_new, v_new,
+                           k_norm, key_cache, value_cache, cosines, sines, pairs, cache_len, start_pos,
+                           pos_dev);
+}
+
 // P.V for one token (decode): one wave per block, four heads per wave.  Lane
 // 16 r + j runs the fma chain of head 4 g + r over channel c0 + j (block
 // (c0 / 16, g, token)), keys in order (gemma4.c:296-307).  Per 64-key tile
