@@ -923,12 +923,23 @@ __global__ __launch_bounds__(64 * NW) void k_softmax_block(float *__restrict__ v
     const int T = threadIdx.x, lane = T & 63, wave = T >> 6;
     float *x = v + (size_t)row * stride;
     float run_max = x[0], sum = 1.0f;  // gemma4.c:401
+    // 16-byte loads of a thread's J consecutive values when the row allows it
+    // (each lane then touches a quarter of the cache lines)
+    const bool wide = J % 4 == 0 && (((uintptr_t)x | stride * sizeof(float)) & 15) == 0;
     for (int base = 0; base < count; base += C) {
         float val[J];
 #pragma unroll
-        for (int j = 0; j < J; j++) {
+        for (int j = 0; j < J; j += 4) {
             const int i = base + J * T + j;
-            val[j] = i > 0 && i < count ? x[i] : -INFINITY;  // -inf: a zero term
+            if (J % 4 == 0 && wide && i + 3 < count) {
+                const float4 f = *reinterpret_cast<const float4 *>(x + i);
+                val[j] = f.x, val[j + 1] = f.y, val[j + 2] = f.z, val[j + 3] = f.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4 && j + e < J; e++)
+                    val[j + e] = i + e < count ? x[i + e] : -INFINITY;  // -inf: a zero term
+            }
+            if (i == 0) val[j] = -INFINITY;  // v_0 is the starting maximum, not a term
         }
         float m = -INFINITY;
 #pragma unroll
