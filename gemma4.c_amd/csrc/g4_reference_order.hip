@@ -737,7 +737,7 @@ __device__ __forceinline__ void butterfly_level(float (&x)[N], int lane16) {
     }
 }
 
-template <int HD, int TQ>
+template <int HD, int TQ, int KG>
 __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q,
                                                      const float *__restrict__ key_cache,
                                                      int cache_len, int full, int start_pos, int n,
@@ -749,8 +749,9 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     const int tn = n - t0 < TQ ? n - t0 : TQ;
     if (pos_dev) start_pos = *pos_dev;
     const int pos_last = start_pos + t0 + tn - 1;
+    constexpr int KB = 16 * KG;  // keys per block pass: 16 groups of KG
     const int kfirst = first_visible(start_pos + t0, full);
-    if (kfirst + (int)blockIdx.x * 64 > pos_last) return;
+    if (kfirst + (int)blockIdx.x * KB > pos_last) return;
     const int mask = cache_len - 1, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *qt = q + (size_t)t0 * 8 * HD;
     for (int i = tid; i < tn * 8 * HD; i += 256) {
@@ -759,15 +760,14 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     }
     __syncthreads();
     const int m = lane & 15, kg = lane >> 4;
-    // A 16-lane group takes KG = 4 keys at once, so each q value read from LDS
-    // feeds 4 fmas (one key per group would make the kernel LDS-bound).
-    constexpr int KG = 4, KSTEP = 16 * KG;  // keys per block pass
-    // key blocks blockIdx.x, blockIdx.x + gridDim.x, ... (one per block when
+    // A 16-lane group takes KG keys at once, so each q value read from LDS
+    // feeds KG fmas (one key per group would make the kernel LDS-bound).
+    // Key blocks blockIdx.x, blockIdx.x + gridDim.x, ... (one per block when
     // the grid spans the keys; a fixed grid strides when the position is read
     // from the device)
-    for (int kbase = kfirst + blockIdx.x * 64; kbase <= pos_last; kbase += gridDim.x * 64)
-    for (int k0 = (wave * 4 + kg) * KG; k0 < 64; k0 += KSTEP) {
-        if (kbase + k0 > pos_last) break;  // uniform within the 16-lane group
+    for (int kbase = kfirst + blockIdx.x * KB; kbase <= pos_last; kbase += gridDim.x * KB) {
+        const int k0 = (wave * 4 + kg) * KG;
+        if (kbase + k0 > pos_last) continue;  // uniform within the 16-lane group
         float kv[KG][S];
 #pragma unroll
         for (int i = 0; i < KG; i++) {
@@ -1400,28 +1400,33 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
     // key blocks spanned by one block of tokens: its first token's window
     // start to its last token (a fixed count with a device-side position:
     // the kernel then strides over the blocks it needs)
-    auto key_blocks = [&](int tq) -> unsigned {
-        if (pos_dev) return full ? 512u : (unsigned)((G4_WINDOW + 63) / 64);
+    // blocks of kb keys
+    auto key_blocks = [&](int tq, int kb) -> unsigned {
+        if (pos_dev) return full ? 512u : (unsigned)((G4_WINDOW + kb - 1) / kb);
         const int tokens = (int)n < tq ? (int)n : tq;
         const int widest = full ? last_pos + 1 : G4_WINDOW - 1 + tokens;
         const int span = widest < last_pos + 1 ? widest : last_pos + 1;
-        const unsigned blocks = (unsigned)((span + 63) / 64);
+        const unsigned blocks = (unsigned)((span + kb - 1) / kb);
         // many tokens over a long context: a block strides over several key
         // blocks, so its staged queries serve more keys
-        return n > 4 && blocks > 16 ? 16u : blocks;
+        const unsigned cap = (unsigned)(1024 / kb);
+        return n > 4 && blocks > cap ? cap : blocks;
     };
     const unsigned nn = (unsigned)n;
+    // decode: 4 keys per 16-lane group; many tokens at head_dim 256: 8 (twice
+    // the fmas per query value read from LDS; at 512 the 8 keys' channel
+    // slices would not fit in registers)
+#define G4_SCORES(HD, TQ, KG)                                                                     \
+    hipLaunchKernelGGL((k_attn_scores<HD, TQ, KG>), dim3(key_blocks(TQ, 16 * KG), (nn + TQ - 1) / TQ), \
+                       dim3(256), 0, s, q, key_cache, cache_len, full, start_pos, (int)n, pos_dev,  \
+                       stride, scores)
     if (head_dim == 256) {
-        constexpr int TQ = 6;
-        dim3 grid(key_blocks(TQ), (nn + TQ - 1) / TQ);
-        hipLaunchKernelGGL((k_attn_scores<256, TQ>), grid, dim3(256), 0, s, q, key_cache, cache_len,
-                           full, start_pos, (int)n, pos_dev, stride, scores);
+        if (n <= 4) G4_SCORES(256, 6, 4);
+        else G4_SCORES(256, 6, 8);
     } else {
-        constexpr int TQ = 3;
-        dim3 grid(key_blocks(TQ), (nn + TQ - 1) / TQ);
-        hipLaunchKernelGGL((k_attn_scores<512, TQ>), grid, dim3(256), 0, s, q, key_cache, cache_len,
-                           full, start_pos, (int)n, pos_dev, stride, scores);
+        G4_SCORES(512, 3, 4);
     }
+#undef G4_SCORES
     if (n <= 4) {  // decode: few rows, a block per row
         const SoftmaxRows spec{heads, full, start_pos, 0, pos_dev, 1};
         launch_softmax_block(s, scores, stride, max_keys, spec, (unsigned)(n * heads));
