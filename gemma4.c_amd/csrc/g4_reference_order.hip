@@ -1120,17 +1120,34 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
             for (int e = 0; e < HPW; e++)
 #pragma unroll
                 for (int c = 0; c < 4; c++) pr[e][c] = s_p[wave][e][16 * c + (lane & 15)];
-#define G4_KEY(J)                                                                   \
-    {                                                                               \
-        const float vv = v4[4 * c + (J) / 4][(J) % 4];                              \
-        _Pragma("unroll") for (int e = 0; e < HPW; e++) fma_row_broadcast_##J(o[e], pr[e][c], vv); \
-    }
+            // Keys 16 c .. 16 c + 15 for the 8 heads: 128 fmas in one asm block
+            // (nothing inside writes a DPP source, so they issue back to back;
+            // s_nop 1 first for probabilities just written by the VALU).
+            static_assert(HPW == 8, "the asm block below is written for 8 heads per wave");
+#define G4_PVE(E, P, V, J) \
+    "v_fmac_f32_dpp %" #E ", %" #P ", %" #V " row_newbcast:" #J " row_mask:0xf bank_mask:0xf\n"
+#define G4_PV8(J, V)                                                                               \
+    G4_PVE(0, 8, V, J) G4_PVE(1, 9, V, J) G4_PVE(2, 10, V, J) G4_PVE(3, 11, V, J) G4_PVE(4, 12, V, J) \
+    G4_PVE(5, 13, V, J) G4_PVE(6, 14, V, J) G4_PVE(7, 15, V, J)
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                G4_KEY(0) G4_KEY(1) G4_KEY(2) G4_KEY(3) G4_KEY(4) G4_KEY(5) G4_KEY(6) G4_KEY(7)
-                G4_KEY(8) G4_KEY(9) G4_KEY(10) G4_KEY(11) G4_KEY(12) G4_KEY(13) G4_KEY(14) G4_KEY(15)
+                asm volatile("s_nop 1\n"
+                             G4_PV8(0, 16) G4_PV8(1, 17) G4_PV8(2, 18) G4_PV8(3, 19) G4_PV8(4, 20)
+                             G4_PV8(5, 21) G4_PV8(6, 22) G4_PV8(7, 23) G4_PV8(8, 24) G4_PV8(9, 25)
+                             G4_PV8(10, 26) G4_PV8(11, 27) G4_PV8(12, 28) G4_PV8(13, 29) G4_PV8(14, 30)
+                             G4_PV8(15, 31)
+                             : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(o[4]), "+v"(o[5]),
+                               "+v"(o[6]), "+v"(o[7])
+                             : "v"(pr[0][c]), "v"(pr[1][c]), "v"(pr[2][c]), "v"(pr[3][c]), "v"(pr[4][c]),
+                               "v"(pr[5][c]), "v"(pr[6][c]), "v"(pr[7][c]), "v"(v4[4 * c][0]),
+                               "v"(v4[4 * c][1]), "v"(v4[4 * c][2]), "v"(v4[4 * c][3]),
+                               "v"(v4[4 * c + 1][0]), "v"(v4[4 * c + 1][1]), "v"(v4[4 * c + 1][2]),
+                               "v"(v4[4 * c + 1][3]), "v"(v4[4 * c + 2][0]), "v"(v4[4 * c + 2][1]),
+                               "v"(v4[4 * c + 2][2]), "v"(v4[4 * c + 2][3]), "v"(v4[4 * c + 3][0]),
+                               "v"(v4[4 * c + 3][1]), "v"(v4[4 * c + 3][2]), "v"(v4[4 * c + 3][3]));
             }
-#undef G4_KEY
+#undef G4_PV8
+#undef G4_PVE
         } else {
             for (int k = k_lo; k < k_hi; k++) {
                 const float vv = s_v[lane][k];
