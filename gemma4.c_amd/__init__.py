@@ -79,6 +79,9 @@ _G4_SIGNATURES = {
     "g4_logits": (_c_i, [_c_sz, _c_p]),
     "g4_logits_all": (_c_i, [_c_p]),
     "g4_argmax": (_c_i, [_c_sz, ctypes.POINTER(_c_i)]),
+    "g4_sample": (_c_i, [_c_sz, ctypes.c_float, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(_c_i)]),
+    "g4_sample_logits": (_c_i, [_c_p, _c_p, _c_i, ctypes.c_float, ctypes.POINTER(ctypes.c_uint64),
+                                ctypes.POINTER(_c_i)]),
     "g4_shutdown": (None, []),
     "g4_stream": (_c_p, []),
     "g4_set_order": (_c_i, [_c_i]),

@@ -186,5 +186,13 @@ void launch_qkv_finish(hipStream_t s, float *q, int heads, const float *q_norm, 
 void launch_softcap(hipStream_t s, float *x, size_t n);
 // First index of the maximum (gemma4.c:537-541) of each of `rows` rows.
 void launch_argmax(hipStream_t s, int *out, const float *x, size_t rows, size_t width);
+// sample() (gemma4.c:536-561) over `vocab` device logits; *result points into
+// the scratch buffer: [0] the token, [1] the advanced generator state.
+int launch_sample(hipStream_t s, const float *logits, int vocab, float temperature, uint64_t state,
+                  uint64_t **result);
+// Copies that result back (synchronizing the stream); the state only when
+// temperature > 0 (the reference draws only then).
+int finish_sample(hipStream_t s, const uint64_t *result, float temperature, uint64_t *rng_state,
+                  int *out_token);
 
 }  // namespace g4

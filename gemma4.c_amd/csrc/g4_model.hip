@@ -623,6 +623,18 @@ extern "C" int g4_argmax(size_t token, int *out_token) {
     return G4_OK;
 }
 
+extern "C" int g4_sample(size_t token, float temperature, uint64_t *rng_state, int *out_token) {
+    Context &c = g_ctx;
+    if (!c.ready || !c.last_n) return set_error(G4_ERR_STATE, "g4_sample: no forward pass yet");
+    G4_CHECK(out_token && rng_state, "g4_sample: null output");
+    G4_CHECK(token < (size_t)c.last_n, "g4_sample: row %zu not in the last forward", token);
+    G4_HIP(hipSetDevice(c.device));
+    G4_TRY(logits_rows(c, c.logits, token, 1));
+    uint64_t *result = nullptr;
+    G4_TRY(launch_sample(c.stream, c.logits, G4_VOCAB, temperature, *rng_state, &result));
+    return finish_sample(c.stream, result, temperature, rng_state, out_token);
+}
+
 extern "C" void g4_shutdown(void) {
     if (g_ctx.ready || g_ctx.arena) free_all(g_ctx);
 }

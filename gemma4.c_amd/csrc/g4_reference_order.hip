@@ -1491,6 +1491,180 @@ int launch_attend(hipStream_t s, float *out, const float *q, const float *key_ca
     return rc;
 }
 
+// ---------------------------------------------------------------------------
+// Sampling (gemma4.c:527-561) on the device.
+//
+// The reference keeps the 64 highest logits in a list sorted by score: a
+// later equal score goes after an earlier one, and a score equal to the 64th
+// does not enter.  That list is the first 64 of the order (score descending,
+// index ascending) over the logits above -inf.  Each logit becomes a 64-bit
+// key that sorts that way: its bits made monotone in the high word (-0 taken
+// as +0, which the reference's comparisons treat as equal), the complemented
+// index in the low word; -inf and NaN get key 0 and never lead.  Blocks keep
+// the 64 largest keys of every 1024 (a bitonic sort in LDS), twice, and one
+// block sorts the last 1024 and runs the reference's arithmetic on the 64 in
+// one lane, in its order (glibc's expf through expf_libm).  A NaN logit makes
+// the list depend on where it falls, so then that lane runs the reference's
+// own insertion loop over the whole row.
+
+__device__ __forceinline__ uint64_t sample_key(float x, int index) {
+    if (!(x > -INFINITY)) return 0;
+    if (x == 0.0f) x = 0.0f;  // -0 -> +0
+    const uint32_t b = __float_as_uint(x);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return (uint64_t)o << 32 | (uint32_t)(0xFFFFFFFFu - (uint32_t)index);
+}
+
+// Bitonic sort of s[0 .. 1024) into descending order, by a block of 256
+// threads (the caller has published s with a barrier).
+__device__ void sort1024_descending(uint64_t *s) {
+    for (int k = 2; k <= 1024; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < 1024; i += 256) {
+                const int p = i ^ j;
+                if (p > i) {
+                    const uint64_t a = s[i], b = s[p];
+                    if ((i & k) == 0 ? a < b : a > b) {
+                        s[i] = b;
+                        s[p] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+}
+
+// Block b: the 64 largest keys of logits [1024 b, 1024 b + 1024) (LOGITS) or
+// of keys [1024 b, ...) of a previous pass; flags[b] = a NaN logit was seen.
+template <bool LOGITS>
+__global__ __launch_bounds__(256) void k_sample_top(uint64_t *__restrict__ top,
+                                                    int *__restrict__ flags,
+                                                    const void *__restrict__ in, int n) {
+    __shared__ uint64_t s[1024];
+    const int base = blockIdx.x * 1024;
+    bool nan = false;
+    for (int i = threadIdx.x; i < 1024; i += 256) {
+        const int g = base + i;
+        if (LOGITS) {
+            const float v = g < n ? static_cast<const float *>(in)[g] : -INFINITY;
+            nan |= v != v;
+            s[i] = sample_key(v, g);
+        } else {
+            s[i] = g < n ? static_cast<const uint64_t *>(in)[g] : 0;
+        }
+    }
+    nan = __syncthreads_or(nan);
+    sort1024_descending(s);
+    if (threadIdx.x < 64) top[blockIdx.x * 64 + threadIdx.x] = s[threadIdx.x];
+    if (LOGITS && threadIdx.x == 0) flags[blockIdx.x] = nan;
+}
+
+// The last 1024 candidates (n of them), then sample() on lane 0:
+// result[0] = the token, result[1] = the advanced generator state.
+__global__ __launch_bounds__(256) void k_sample_draw(uint64_t *__restrict__ result,
+                                                     const uint64_t *__restrict__ keys, int n,
+                                                     const int *__restrict__ flags, int flag_count,
+                                                     const float *__restrict__ logits, int vocab,
+                                                     float temperature, uint64_t state) {
+    __shared__ uint64_t s[1024];
+    for (int i = threadIdx.x; i < 1024; i += 256) s[i] = i < n ? keys[i] : 0;
+    __syncthreads();
+    sort1024_descending(s);
+    if (threadIdx.x != 0) return;
+    bool nan = false;
+    for (int i = 0; i < flag_count; i++) nan |= flags[i] != 0;
+    float score[64];
+    int token[64];
+    if (!nan) {
+        for (int i = 0; i < 64; i++) {
+            const uint32_t o = (uint32_t)(s[i] >> 32);
+            score[i] = s[i] ? __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o) : -INFINITY;
+            token[i] = s[i] ? (int)(0xFFFFFFFFu - (uint32_t)s[i]) : 0;
+        }
+    } else {  // gemma4.c:546-550 as written
+        for (int i = 0; i < 64; i++) {
+            score[i] = -INFINITY;
+            token[i] = 0;
+        }
+        for (int t = 0; t < vocab; t++) {
+            const float x = logits[t];
+            if (x <= score[63]) continue;
+            int i = 63;
+            for (; i > 0 && x > score[i - 1]; i--) {
+                score[i] = score[i - 1];
+                token[i] = token[i - 1];
+            }
+            score[i] = x;
+            token[i] = t;
+        }
+    }
+    // gemma4.c:552-560
+    const float max = score[0] / temperature;
+    float sum = 0.0f;
+    for (int i = 0; i < 64; i++) {
+        score[i] = expf_libm(score[i] / temperature - max);
+        sum += score[i];
+    }
+    float mass = 0.0f;
+    int count = 0;
+    while (count < 64 && mass < 0.95f * sum) mass += score[count++];
+    // gemma4.c:529-533: xorshift64*
+    state ^= state >> 12;
+    state ^= state << 25;
+    state ^= state >> 27;
+    float threshold = (float)((state * 0x2545F4914F6CDD1DULL) >> 40) / 16777216.0f * mass;
+    int chosen = token[count > 0 ? count - 1 : 0];
+    for (int i = 0; i < count; i++)
+        if ((threshold -= score[i]) <= 0.0f) {
+            chosen = token[i];
+            break;
+        }
+    result[0] = (uint64_t)(uint32_t)chosen;
+    result[1] = state;
+}
+
+// sample() over `vocab` device logits; *result (device, in the scratch
+// buffer): [0] the token, [1] the advanced generator state (temperature > 0).
+int launch_sample(hipStream_t s, const float *logits, int vocab, float temperature, uint64_t state,
+                  uint64_t **result) {
+    if (vocab < 64 || vocab > G4_VOCAB)
+        return set_error(G4_ERR_ARG, "sample: vocabulary %d not in [64, %d]", vocab, G4_VOCAB);
+    const int blocks1 = (vocab + 1023) / 1024, n1 = blocks1 * 64;
+    const int blocks2 = (n1 + 1023) / 1024, n2 = blocks2 * 64;  // <= 1024
+    const size_t flag_words = ((size_t)blocks1 + 1) / 2;        // ints, in 8-byte words
+    const size_t need = ((size_t)n1 + n2 + flag_words + 2) * sizeof(uint64_t);
+    int rc = scratch_reserve(need, 0);
+    if (rc) return rc;
+    uint64_t *top1 = reinterpret_cast<uint64_t *>(scratch().dots), *top2 = top1 + n1;
+    int *flags = reinterpret_cast<int *>(top2 + n2);
+    uint64_t *out = top2 + n2 + flag_words;
+    *result = out;
+    if (temperature <= 0.0f) {  // gemma4.c:537-541: the first maximum
+        launch_argmax(s, reinterpret_cast<int *>(out), logits, 1, (size_t)vocab);
+    } else {
+        hipLaunchKernelGGL(k_sample_top<true>, dim3((unsigned)blocks1), dim3(256), 0, s, top1, flags,
+                           static_cast<const void *>(logits), vocab);
+        hipLaunchKernelGGL(k_sample_top<false>, dim3((unsigned)blocks2), dim3(256), 0, s, top2,
+                           static_cast<int *>(nullptr), static_cast<const void *>(top1), n1);
+        hipLaunchKernelGGL(k_sample_draw, dim3(1), dim3(256), 0, s, out, top2, n2, flags, blocks1,
+                           logits, vocab, temperature, state);
+    }
+    G4_HIP(hipGetLastError());
+    return G4_OK;
+}
+
+// Copies a launch_sample result back (synchronizing the stream): the token,
+// and the generator state when temperature > 0.
+int finish_sample(hipStream_t s, const uint64_t *result, float temperature, uint64_t *rng_state,
+                  int *out_token) {
+    uint64_t host[2] = {0, 0};
+    G4_HIP(hipMemcpyAsync(host, result, sizeof(host), hipMemcpyDeviceToHost, s));
+    G4_HIP(hipStreamSynchronize(s));
+    *out_token = (int)(uint32_t)host[0];
+    if (temperature > 0.0f) *rng_state = host[1];
+    return G4_OK;
+}
+
 }  // namespace g4
 
 extern "C" int g4_set_order(int order) {
@@ -1516,4 +1690,13 @@ extern "C" int g4_softmax(void *stream, float *values, int count, size_t rows) {
     }
     G4_HIP(hipGetLastError());
     return G4_OK;
+}
+
+extern "C" int g4_sample_logits(void *stream, const float *logits, int vocab, float temperature,
+                                uint64_t *rng_state, int *out_token) {
+    G4_CHECK(logits && rng_state && out_token, "g4_sample_logits: null argument");
+    uint64_t *result = nullptr;
+    const int rc = g4::launch_sample((hipStream_t)stream, logits, vocab, temperature, *rng_state, &result);
+    if (rc) return rc;
+    return g4::finish_sample((hipStream_t)stream, result, temperature, rng_state, out_token);
 }

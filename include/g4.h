@@ -88,6 +88,16 @@ int g4_logits_all(float *out);
  * computed on the device so only one int crosses the bus. */
 int g4_argmax(size_t token, int *out_token);
 
+/* sample() (gemma4.c:536-561) of row `token` of the last forward pass, on the
+ * device: temperature <= 0 is the first maximum; otherwise the 64 highest
+ * logits, the smallest prefix holding 95% of their softmax at `temperature`,
+ * and one xorshift64* draw (random_uniform, gemma4.c:529-534) from
+ * *rng_state -- the reference's global rng_state (gemma4.c:527), passed in
+ * and advanced in place exactly as the reference advances it.  Replaces
+ * logits() + sample() in generate() (gemma4.c:600): only the token and the
+ * state cross the bus. */
+int g4_sample(size_t token, float temperature, uint64_t *rng_state, int *out_token);
+
 /* Free every device resource of the model context. */
 void g4_shutdown(void);
 
@@ -139,6 +149,12 @@ int g4_embedding(void *stream, float *out, const g4_tensor *table, const int *to
 /* gemma4.c:400-408: softmax of `rows` independent rows of `count` values in
  * place, in the reference's order with its libm expf (bit-identical). */
 int g4_softmax(void *stream, float *values, int count, size_t rows);
+
+/* gemma4.c:536-561: sample() over `vocab` (64 .. G4_VOCAB) device logits with
+ * the generator state in *rng_state (advanced in place when temperature > 0).
+ * Synchronizes `stream`. */
+int g4_sample_logits(void *stream, const float *logits, int vocab, float temperature,
+                     uint64_t *rng_state, int *out_token);
 
 /* gemma4.c:443-456: causal attention of n query tokens (heads x head_dim each,
  * row-major) at positions start_pos.. over a ring KV cache of cache_len rows;

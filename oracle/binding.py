@@ -54,6 +54,7 @@ _ORACLE_EXTRA = {
     "orc_fast_available": (_i, []),
     "orc_f16_to_f32": (_f, [ctypes.c_uint16]),
     "orc_attend": (None, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _sz]),
+    "orc_sample": (_i, [_p, _i, _f, ctypes.POINTER(ctypes.c_uint64)]),
 }
 
 _REF_EXTRA = {
@@ -64,6 +65,7 @@ _REF_EXTRA = {
     "ref_off_full": (_sz, []),
     "ref_model_weights_offset": (_sz, []),
     "ref_thread_count": (_i, []),
+    "sample": (_i, [_p, _i, _f]),
 }
 
 _cache: dict[str, ctypes.CDLL] = {}

@@ -598,3 +598,62 @@ float *orc_logits(const orc_weights *w, orc_state *s, size_t row) {
     }
     return s->hidden;
 }
+
+/* ------------------------------------------------------------------------- */
+/* Sampling (gemma4.c:527-561), the generator state passed explicitly.        */
+
+/* gemma4.c:529-534: one xorshift64* step; the top 24 bits of the scrambled
+ * state as a float in [0, 1). */
+static float orc_uniform(uint64_t *state) {
+    uint64_t x = *state;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    *state = x;
+    return (float)((x * 0x2545F4914F6CDD1DULL) >> 40) / 16777216.0f;
+}
+
+/* gemma4.c:536-561.  temperature <= 0: the first maximum.  Otherwise the 64
+ * highest logits kept in a list sorted by score (a later equal score goes
+ * after an earlier one; a score equal to the 64th does not enter), softmax
+ * over them at the temperature (sum accumulated in list order), the smallest
+ * prefix holding 95% of that sum, one uniform draw scaled by the prefix mass
+ * and walked down the prefix. */
+int orc_sample(const float *logits, int vocab, float temperature, uint64_t *rng_state) {
+    if (temperature <= 0.0f) {
+        int best = 0;
+        for (int i = 1; i < vocab; i++)
+            if (logits[i] > logits[best]) best = i;
+        return best;
+    }
+    float score[64];
+    int token[64];
+    for (int i = 0; i < 64; i++) {
+        score[i] = -INFINITY;
+        token[i] = 0;
+    }
+    for (int t = 0; t < vocab; t++) {
+        const float x = logits[t];
+        if (x <= score[63]) continue;
+        int i = 63;
+        for (; i > 0 && x > score[i - 1]; i--) {
+            score[i] = score[i - 1];
+            token[i] = token[i - 1];
+        }
+        score[i] = x;
+        token[i] = t;
+    }
+    const float max = score[0] / temperature;
+    float sum = 0.0f;
+    for (int i = 0; i < 64; i++) {
+        score[i] = expf(score[i] / temperature - max);
+        sum += score[i];
+    }
+    float mass = 0.0f;
+    int count = 0;
+    while (count < 64 && mass < 0.95f * sum) mass += score[count++];
+    float threshold = orc_uniform(rng_state) * mass;
+    for (int i = 0; i < count; i++)
+        if ((threshold -= score[i]) <= 0.0f) return token[i];
+    return token[count > 0 ? count - 1 : 0];
+}

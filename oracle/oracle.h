@@ -110,6 +110,10 @@ void orc_forward(const orc_weights *w, orc_state *s, const int *tokens, size_t n
 /* Returns a pointer to VOCAB floats inside the state, valid until the next call. */
 float *orc_logits(const orc_weights *w, orc_state *s, size_t row);
 
+/* gemma4.c:527-561: sample() with the generator state (the reference's global
+ * rng_state) passed in and advanced in place. */
+int orc_sample(const float *logits, int vocab, float temperature, uint64_t *rng_state);
+
 #ifdef __cplusplus
 }
 #endif

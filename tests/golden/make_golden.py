@@ -4,6 +4,10 @@ sources by oracle/Makefile) on seeded inputs.
 
     python tests/golden/make_golden.py
 
+    python tests/golden/make_golden.py sample   # sample.npz only
+
+sample.npz the sampler (gemma4.c:527-561): logits rows, temperatures, the
+           generator state before each call, and the token and state after
 ops.npz    per-kernel inputs and outputs (quantize, matmul_int8,
            attention_scores, softmax, weighted_value_sum, geglu, embedding,
            rmsnorm, add_and_scale, apply_rope)
@@ -144,9 +148,40 @@ def make_model(pkg, image) -> dict[str, np.ndarray]:
     )
 
 
+def make_sample() -> dict[str, np.ndarray]:
+    """The reference's sample() over SAMPLE_CASES (tests/helpers.py): for each
+    logits row and temperature, DRAWS consecutive calls from a recorded
+    generator state."""
+    import ctypes
+
+    from helpers import sample_cases
+
+    lib = binding.ref()
+    state = ctypes.c_ulonglong.in_dll(lib, "rng_state")
+    rows, temps, states = sample_cases()
+    tokens = np.zeros((len(rows), len(temps), len(states), SAMPLE_DRAWS), np.int32)
+    after = np.zeros(tokens.shape, np.uint64)
+    for r, row in enumerate(rows):
+        for t, temp in enumerate(temps):
+            for s0, start in enumerate(states):
+                state.value = int(start)
+                for d in range(SAMPLE_DRAWS):
+                    tokens[r, t, s0, d] = lib.sample(row.ctypes.data, row.size, float(temp))
+                    after[r, t, s0, d] = state.value
+    return dict(rows=np.stack(rows), temps=np.array(temps, np.float32),
+                states=np.array(states, np.uint64), tokens=tokens, states_after=after)
+
+
+SAMPLE_DRAWS = 6
+
+
 def main() -> None:
     if not binding.ref_available():
         sys.exit("oracle/_ref/libgemma4ref.so is not built (needs the reference checkout)")
+    if sys.argv[1:] == ["sample"]:
+        np.savez_compressed(os.path.join(HERE, "sample.npz"), **make_sample())
+        print("sample.npz", os.path.getsize(os.path.join(HERE, "sample.npz")), "bytes")
+        return
     pkg = __graft_entry__.load_package()
     ops = make_ops(pkg, binding.Kernels(use_ref=True))
     np.savez_compressed(os.path.join(HERE, "ops.npz"), **ops)

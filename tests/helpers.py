@@ -127,3 +127,28 @@ def image_digest(image) -> np.ndarray:
             h.update(np.int64(p - image.base).tobytes())
             h.update(ctypes.string_at(p, min(size, 4096)))
     return np.frombuffer(h.digest(), dtype=np.uint8)
+
+
+def sample_cases(vocab: int = 4096):
+    """Logits rows, temperatures and generator states for the sampler
+    (gemma4.c:527-561): rows chosen to exercise the top-64 list's ordering
+    (ties at and around the 64th place, +0 against -0), the soft-capped
+    range, one dominant logit, a flat top, and a row whose 64 highest are
+    all equal."""
+    g = np.random.default_rng(42)
+    rows = []
+    rows.append((g.standard_normal(vocab) * 3.0).astype(np.float32))
+    rows.append(g.integers(-20, 21, vocab).astype(np.float32))                      # many ties
+    z = np.where(g.random(vocab) < 0.5, np.float32(0.0), np.float32(-0.0))
+    z[g.choice(vocab, 40, replace=False)] = g.standard_normal(40).astype(np.float32)
+    rows.append(z.astype(np.float32))                                               # +0 / -0
+    rows.append((30.0 * np.tanh(g.standard_normal(vocab) * 10.0 / 30.0)).astype(np.float32))
+    d = (g.standard_normal(vocab)).astype(np.float32)
+    d[1234] = 40.0
+    rows.append(d)                                                                  # dominant
+    f = (g.standard_normal(vocab) - 10.0).astype(np.float32)
+    f[g.choice(vocab, 100, replace=False)] = np.float32(5.0)
+    rows.append(f)                                                                  # 100-way tie
+    temps = [0.0, 0.3, 1.0, 2.5]
+    states = [42, 0x9E3779B97F4A7C15]
+    return rows, temps, states

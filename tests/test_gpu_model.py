@@ -165,3 +165,22 @@ def test_errors(pkg, model):
     out = np.empty(pkg.VOCAB, np.float32)
     assert model.g4_logits(1, out.ctypes.data) == 1  # only one row
     assert model.g4_init(None, 0) == 1
+
+
+def test_sample_model_row(pkg, model, oracle_lib):
+    """g4_sample on the model's own logits row matches the oracle's sample()
+    over the same row (copied out with g4_logits), token and generator state."""
+    import ctypes
+
+    tokens = rng(62).integers(0, pkg.VOCAB, 6).astype(np.int32)
+    gpu_forward(pkg, model, tokens, 0)
+    row = gpu_logits(pkg, model, 5)
+    state = 42
+    for temp in (0.0, 0.8, 1.0, 1.3, 1.0):
+        st = ctypes.c_uint64(state)
+        tok = ctypes.c_int(-1)
+        pkg.check(model.g4_sample(5, temp, ctypes.byref(st), ctypes.byref(tok)))
+        ost = ctypes.c_uint64(state)
+        want = oracle_lib.oracle().orc_sample(row.ctypes.data, row.size, temp, ctypes.byref(ost))
+        assert tok.value == want and st.value == ost.value, temp
+        state = st.value

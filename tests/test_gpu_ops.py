@@ -339,3 +339,70 @@ def test_attention_parallel_order(pkg, g4lib, torch_gpu, oracle_lib, order, hd, 
     o, ref = run_attention(pkg, g4lib, torch_gpu, oracle_lib, hd, ring, full, start, n)
     scale = np.abs(ref).max()
     assert np.abs(o - ref).max() <= 2e-5 * scale, float(np.abs(o - ref).max() / scale)
+
+
+# --- the sampler (gemma4.c:527-561) -------------------------------------------
+
+def gpu_sample(pkg, lib, torch, row: np.ndarray, temp: float, state: int) -> tuple[int, int]:
+    import ctypes
+
+    d = dev(torch, row)
+    st = ctypes.c_uint64(state)
+    tok = ctypes.c_int(-1)
+    pkg.check(lib.g4_sample_logits(None, d.data_ptr(), row.size, float(temp), ctypes.byref(st),
+                                   ctypes.byref(tok)))
+    return tok.value, st.value
+
+
+def orc_sample(oracle_lib, row: np.ndarray, temp: float, state: int) -> tuple[int, int]:
+    import ctypes
+
+    st = ctypes.c_uint64(state)
+    tok = oracle_lib.oracle().orc_sample(row.ctypes.data, row.size, float(temp), ctypes.byref(st))
+    return int(tok), st.value
+
+
+def test_sample_golden(pkg, g4lib, torch_gpu):
+    """The reference's own sample() outputs (tests/golden/sample.npz): the
+    token and the generator state after each of several consecutive draws."""
+    d = load_golden("sample.npz")
+    for r in range(d["rows"].shape[0]):
+        row = np.ascontiguousarray(d["rows"][r])
+        for t, temp in enumerate(d["temps"]):
+            for s0, start in enumerate(d["states"]):
+                state = int(start)
+                for k in range(d["tokens"].shape[3]):
+                    tok, after = gpu_sample(pkg, g4lib, torch_gpu, row, float(temp), state)
+                    if temp > 0:
+                        state = after
+                    assert tok == d["tokens"][r, t, s0, k], (r, float(temp), s0, k)
+                    assert state == int(d["states_after"][r, t, s0, k]), (r, float(temp), s0, k)
+
+
+def test_sample_full_vocab(pkg, g4lib, torch_gpu, oracle_lib):
+    """Model-sized rows against the oracle: soft-capped logits with ties
+    planted at the 64th place, a row with a NaN (the reference's insertion
+    loop then decides), and a row that is -inf outside 70 entries."""
+    g = rng(77)
+    rows = []
+    for _ in range(3):
+        row = (30.0 * np.tanh(g.standard_normal(pkg.VOCAB) * 8.0 / 30.0)).astype(np.float32)
+        row[g.choice(pkg.VOCAB, 12, replace=False)] = np.sort(row)[::-1][63]
+        rows.append(row)
+    nan_row = rows[0].copy()
+    nan_row[g.integers(0, pkg.VOCAB)] = np.nan
+    rows.append(nan_row)
+    sparse = np.full(pkg.VOCAB, -np.inf, np.float32)
+    sparse[g.choice(pkg.VOCAB, 70, replace=False)] = g.standard_normal(70).astype(np.float32)
+    rows.append(sparse)
+    for i, row in enumerate(rows):
+        for temp in (0.0, 0.5, 1.0, 1.7):
+            state = int(g.integers(1, 2**63))
+            for _ in range(3):
+                want = orc_sample(oracle_lib, row, temp, state)
+                got = gpu_sample(pkg, g4lib, torch_gpu, row, temp, state)
+                if temp > 0:
+                    assert got == want, (i, temp)
+                    state = want[1]
+                else:
+                    assert got[0] == want[0], (i, temp)

@@ -269,3 +269,88 @@ def test_oracle_thread_count_independent(image, oracle_lib):
         m.close()
     lib.orc_set_threads(0)
     assert np.array_equal(rows[0], rows[1])
+
+
+# --- the sampler (gemma4.c:527-561) -------------------------------------------
+
+def _orc_sample(oracle_lib, row: np.ndarray, temp: float, state: int) -> tuple[int, int]:
+    import ctypes
+
+    st = ctypes.c_uint64(state)
+    tok = oracle_lib.oracle().orc_sample(row.ctypes.data, row.size, float(temp), ctypes.byref(st))
+    return int(tok), int(st.value)
+
+
+def test_sample_golden(oracle_lib):
+    """orc_sample against the reference's own sample() (tests/golden/sample.npz):
+    tokens and generator states over consecutive draws."""
+    d = load_golden("sample.npz")
+    rows, temps, states = d["rows"], d["temps"], d["states"]
+    for r in range(rows.shape[0]):
+        row = np.ascontiguousarray(rows[r])
+        for t, temp in enumerate(temps):
+            for s0, start in enumerate(states):
+                state = int(start)
+                for k in range(d["tokens"].shape[3]):
+                    tok, state = _orc_sample(oracle_lib, row, float(temp), state)
+                    assert tok == d["tokens"][r, t, s0, k], (r, t, s0, k)
+                    assert state == int(d["states_after"][r, t, s0, k]), (r, t, s0, k)
+
+
+def test_sample_reference_full_vocab(oracle_lib):
+    """orc_sample against the compiled reference at the model's vocabulary,
+    soft-capped logits with ties planted at the 64th place."""
+    import ctypes
+
+    if not oracle_lib.ref_available():
+        pytest.skip("reference library not built here")
+    lib = oracle_lib.ref()
+    state = ctypes.c_ulonglong.in_dll(lib, "rng_state")
+    g = np.random.default_rng(5)
+    for case in range(3):
+        row = (30.0 * np.tanh(g.standard_normal(262144) * 8.0 / 30.0)).astype(np.float32)
+        top = np.sort(row)[::-1]
+        row[g.choice(262144, 12, replace=False)] = top[63]  # equal to the 64th
+        for temp in (0.0, 0.7, 1.0):
+            s = int(g.integers(1, 2**63))
+            state.value = s
+            want = lib.sample(row.ctypes.data, row.size, temp)
+            tok, after = _orc_sample(oracle_lib, row, temp, s)
+            assert tok == want and after == state.value, (case, temp)
+
+
+def _uniform(state: int) -> tuple[float, int]:
+    """xorshift64* as published (Vigna): shifts 12, 25, 27, multiplier
+    0x2545F4914F6CDD1D; the top 24 bits of the product over 2^24."""
+    m = (1 << 64) - 1
+    x = state
+    x ^= x >> 12
+    x = (x ^ (x << 25)) & m
+    x ^= x >> 27
+    return ((x * 0x2545F4914F6CDD1D) & m) >> 40, x
+
+
+def test_sample_closed_forms(oracle_lib):
+    """Cases whose answer follows from the definition alone: temperature 0
+    is the first maximum; one logit 40 above the rest is always drawn; a row
+    whose 64 highest are equal has p = 1/64 each (weights exactly 1), a 95%
+    prefix of ceil(0.95 * 64) = 61 entries, and draws entry ceil(x) - 1 of
+    the 64 lowest-indexed maxima, x = u * 61 in float32 (x = 0: the first),
+    for the generator's next u."""
+    g = np.random.default_rng(9)
+    row = g.standard_normal(5000).astype(np.float32)
+    row[[77, 3000]] = 9.0
+    assert _orc_sample(oracle_lib, row, 0.0, 1)[0] == 77
+    row[1234] = 49.0
+    assert all(_orc_sample(oracle_lib, row, 1.0, s)[0] == 1234 for s in (1, 42, 2**40 + 7))
+    flat = np.full(5000, -3.0, np.float32)
+    idx = np.sort(g.choice(5000, 90, replace=False))
+    flat[idx] = 2.5  # 90 equal maxima: the list holds the 64 with the lowest indices
+    state = 42
+    for _ in range(20):
+        top24, nxt = _uniform(state)
+        x = float(np.float32(np.float32(top24) / np.float32(16777216.0)) * np.float32(61.0))
+        want = idx[max(0, min(60, int(np.ceil(x)) - 1))]
+        tok, state = _orc_sample(oracle_lib, flat, 1.0, state)
+        assert state == nxt
+        assert tok == want, (tok, want)
