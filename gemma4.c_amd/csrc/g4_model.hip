@@ -2,10 +2,11 @@
 // g4_forward / g4_logits (include/g4.h).
 //
 // Weights are uploaded once into one HBM arena in the exporter's packed layout
-// (the same bytes as the .bin); the fp32 KV rings (3 global owners x 131072 x
-// 512, 12 sliding owners x 1024 x 256, keys then values) and every activation
-// live on the device, so a token step moves only token ids in and one logits
-// row (or one argmax) out.
+// (the same bytes as the .bin); the fp32 KV rings (3 global owners x 512
+// channels, growing from 4096 to at most 131072 positions with the context;
+// 12 sliding owners x 1024 x 256; keys then values) and every activation live
+// on the device, so a token step moves only token ids in and one logits row
+// (or one sampled token) out.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -67,9 +68,16 @@ struct Context {
     hipGraphExec_t decode_graph = nullptr;
     unsigned graph_generation = 0;
     int graph_order = -1;
+    // The global layers' rings grow with the context (ensure_kv): a move bumps
+    // kv_generation, and the captured graph (which holds the old pointers and
+    // lengths) is captured again.
+    unsigned kv_generation = 0, graph_kv_generation = 0;
 };
 
 static Context g_ctx;
+
+// Initial positions of a global-attention ring (a power of two).
+constexpr int kGlobalStart = 4096;
 
 static size_t record_bytes(const g4_tensor &t, int index, size_t *scale_bytes) {
     *scale_bytes = 0;
@@ -287,7 +295,8 @@ static int init(const g4_tensor *records, int device) {
     for (int l = 0; l < 15; l++) {
         if (!records[2 + l * 19 + 11].data) continue;
         const int full = l % 5 == 4;
-        c.cache_len[l] = full ? G4_MAX_CONTEXT : G4_WINDOW + G4_BATCH;
+        // global rings start at kGlobalStart positions and grow on demand
+        c.cache_len[l] = full ? kGlobalStart : G4_WINDOW + G4_BATCH;
         c.cache_dim[l] = full ? 512 : 256;
         const size_t bytes = 2 * (size_t)c.cache_len[l] * c.cache_dim[l] * sizeof(float);
         G4_HIP(hipMalloc(&c.cache[l], bytes));
@@ -511,18 +520,56 @@ static int capture_decode(Context &c) {
     G4_HIP(inst);
     c.graph_generation = scratch().generation;
     c.graph_order = order();
+    c.graph_kv_generation = c.kv_generation;
+    return G4_OK;
+}
+
+// Global-attention rings hold every position from 0, so they must cover the
+// last position of a forward pass.  They start at kGlobalStart positions and
+// double (to G4_MAX_CONTEXT at most), keys and values copied to the new
+// buffer, the new rows zeroed: a short context does not pay for 131072
+// positions of fp32 keys and values per ring (gemma4.c:164-165 allocates
+// them all).  Runs between forward passes, outside any graph capture.
+static int ensure_kv(Context &c, int last_pos) {
+    for (int l = 0; l < 15; l++) {
+        if (!c.cache[l] || c.cache_dim[l] != 512 || last_pos < c.cache_len[l]) continue;
+        int len = c.cache_len[l];
+        while (len <= last_pos && len < G4_MAX_CONTEXT) len *= 2;
+        const size_t hd = (size_t)c.cache_dim[l], old_len = (size_t)c.cache_len[l];
+        float *grown = nullptr;
+        G4_HIP(hipMalloc(&grown, 2 * (size_t)len * hd * sizeof(float)));
+        const size_t old_bytes = old_len * hd * sizeof(float), new_bytes = (size_t)len * hd * sizeof(float);
+        hipError_t e = hipMemcpyAsync(grown, c.cache[l], old_bytes, hipMemcpyDeviceToDevice, c.stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(grown + (size_t)len * hd, c.cache[l] + old_len * hd, old_bytes,
+                               hipMemcpyDeviceToDevice, c.stream);
+        if (e == hipSuccess) e = hipMemsetAsync((char *)grown + old_bytes, 0, new_bytes - old_bytes, c.stream);
+        if (e == hipSuccess)
+            e = hipMemsetAsync((char *)(grown + (size_t)len * hd) + old_bytes, 0, new_bytes - old_bytes, c.stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c.stream);
+        if (e != hipSuccess) {
+            (void)hipFree(grown);
+            return set_error(G4_ERR_DEVICE, "growing the KV ring of layer %d: %s", l, hipGetErrorString(e));
+        }
+        G4_HIP(hipFree(c.cache[l]));
+        c.cache[l] = grown;
+        c.cache_len[l] = len;
+        c.kv_generation++;
+    }
     return G4_OK;
 }
 
 static int forward(Context &c, const int *tokens, int n, int start_pos) {
     hipStream_t s = c.stream;
+    G4_TRY(ensure_kv(c, start_pos + n - 1));
     memcpy(c.tokens_pinned, tokens, (size_t)n * sizeof(int));
     G4_HIP(hipMemcpyAsync(c.tokens_dev, c.tokens_pinned, (size_t)n * sizeof(int),
                           hipMemcpyHostToDevice, s));
     if (n == 1 && order() == G4_ORDER_REFERENCE) {
         *c.pos_pinned = start_pos;
         G4_HIP(hipMemcpyAsync(c.pos_dev, c.pos_pinned, sizeof(int), hipMemcpyHostToDevice, s));
-        if (!c.decode_graph || c.graph_generation != scratch().generation || c.graph_order != order())
+        if (!c.decode_graph || c.graph_generation != scratch().generation || c.graph_order != order() ||
+            c.graph_kv_generation != c.kv_generation)
             G4_TRY(capture_decode(c));
         G4_HIP(hipGraphLaunch(c.decode_graph, s));
     } else {

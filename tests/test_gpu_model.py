@@ -122,6 +122,38 @@ def test_long_prefill_ring_wrap(pkg, model, image, oracle_lib):
     cpu.close()
 
 
+def test_global_ring_grows(pkg, model, image, oracle_lib):
+    """A 4096-token prefill, then decode steps past position 4096: the global
+    layers' rings start at 4096 positions and grow (keys and values copied,
+    the captured decode graph taken again) -- logits and greedy tokens still
+    follow the oracle."""
+    cpu = oracle_lib.Model(image)
+    tokens = rng(71).integers(0, pkg.VOCAB, 4096).astype(np.int32)
+    row = prefill(pkg, model, cpu, tokens)
+    pos = len(tokens)
+    for step in range(4):
+        c_lg = cpu.logits(row)
+        g_lg = gpu_logits(pkg, model, row)
+        err = float(np.abs(g_lg - c_lg).max())
+        assert err <= TOL, (step, err)
+        tok = int(np.argmax(c_lg))
+        assert int(np.argmax(g_lg)) == tok, step
+        gpu_forward(pkg, model, [tok], pos)
+        cpu.forward(np.array([tok], np.int32), pos)
+        pos += 1
+        row = 0
+    cpu.close()
+    # a new sequence whose 512-token prefill (the reference's chunking, from
+    # position 0) crosses the next doubling at 8192 inside a chunk
+    cpu = oracle_lib.Model(image)
+    tokens = rng(72).integers(0, pkg.VOCAB, 8400).astype(np.int32)
+    row = prefill(pkg, model, cpu, tokens)
+    for r in (0, row):
+        err = float(np.abs(gpu_logits(pkg, model, r) - cpu.logits(r)).max())
+        assert err <= TOL, (r, err)
+    cpu.close()
+
+
 def test_teacher_forced_dump_2388(pkg, model, image, oracle_lib):
     """The teacher-forced logit dump (gemma4.c:563-573 with dump on): 2388
     random ids in 512-token chunks, every position's 262144 logits
