@@ -298,34 +298,47 @@ def model_benchmarks(pkg, lib, np, steps: int, warmup: int) -> dict:
 
 def cpu_baseline(pkg, image, np) -> dict:
     """The oracle (CPU restatement of the same path, bit-identical to the
-    reference) on this host: 512-token prefill + logits, 1 warmup + 2 timed."""
+    reference) on this host: 512-token prefill + logits, 1 discarded warmup +
+    the mean of 3 (the reference README's protocol), at the host's thread
+    count (OMP_NUM_THREADS when set, else the oracle's default, at most 16)
+    and at 8 threads for comparability with the reference's published setup;
+    then decode at 512 tokens of context (4 steps of forward + logits)."""
+    import psutil
+
     from oracle import binding
     lib = binding.oracle()
     threads = min(lib.orc_threads(), 16)
-    lib.orc_set_threads(threads)
     model = binding.Model(image)
     tokens = np.random.default_rng(3).integers(0, pkg.VOCAB, 512).astype(np.int32)
-    model.forward(tokens, 0)
-    model.logits(511)
-    times = []
-    for _ in range(2):
-        s = time.perf_counter()
+
+    def prefill_rate(n_threads: int) -> float:
+        lib.orc_set_threads(n_threads)
         model.forward(tokens, 0)
         model.logits(511)
-        times.append(time.perf_counter() - s)
-    prefill = 512 / (sum(times) / len(times))
-    # decode at 512 tokens of context: 4 steps of forward + logits
+        times = []
+        for _ in range(3):
+            s = time.perf_counter()
+            model.forward(tokens, 0)
+            model.logits(511)
+            times.append(time.perf_counter() - s)
+        return 512 / (sum(times) / len(times))
+
+    prefill8 = prefill_rate(8)
+    prefill = prefill_rate(threads)
     s = time.perf_counter()
     for i in range(4):
         model.forward(np.array([2], np.int32), 512 + i)
         model.logits(0)
     decode = 4 / (time.perf_counter() - s)
     model.close()
-    log(f"cpu oracle ({threads} threads): prefill 512 {prefill:.1f} tok/s, decode@512 {decode:.2f} tok/s")
+    nproc, physical = os.cpu_count(), psutil.cpu_count(logical=False)
+    log(f"cpu oracle ({threads} threads; nproc {nproc}, {physical} physical cores): prefill 512 "
+        f"{prefill:.1f} tok/s ({prefill8:.1f} at 8 threads), decode@512 {decode:.2f} tok/s")
     return {"value": prefill, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": "512-token prefill + logits of the same synthetic model, 1 warmup + mean of 2; "
-                      f"decode@512 ctx {decode:.2f} tok/s over 4 steps",
-            "decode512_tok_s": decode}
+            "sample": "512-token prefill + logits of the same synthetic model, 1 discarded warmup + "
+                      f"mean of 3; decode@512 ctx {decode:.2f} tok/s over 4 steps",
+            "prefill512_tok_s_8_threads": prefill8, "decode512_tok_s": decode,
+            "host": {"nproc": nproc, "physical_cores": physical, "threads": threads}}
 
 
 def main() -> int:
