@@ -392,7 +392,11 @@ __device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0,
     const bool sp = e.meta & 1;
     const float fa = sp ? e.t : 1.0f, fb = sp ? 1.0f : e.t;
     float sv = s, at_start = 0.0f, at_end = 0.0f;
-    for (int i = 0; i < entries; i++) {
+    // entries is the same in every lane (a count read back from LDS, which the
+    // compiler cannot see): made scalar, the loop runs on scalar branches
+    // instead of as a divergent loop with exec-mask updates per step
+    const int n_entries = __builtin_amdgcn_readfirstlane(entries);
+    auto chain_step = [&](int i) __attribute__((always_inline)) {
         at_start = lane == i ? sv : at_start;
         sv += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(du), i));
         at_end = lane == i ? sv : at_end;
@@ -401,7 +405,15 @@ __device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0,
             sv = sv * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fa), i)) + b;
         else
             sv = sv + b;
+    };
+    int i_chain = 0;
+    for (; i_chain + 4 <= n_entries; i_chain += 4) {  // the readlanes of four steps issue ahead
+        chain_step(i_chain);
+        chain_step(i_chain + 1);
+        chain_step(i_chain + 2);
+        chain_step(i_chain + 3);
     }
+    for (; i_chain < n_entries; i_chain++) chain_step(i_chain);
     const int e0 = biased_exponent(at_start), e1 = biased_exponent(at_end);
     const uint64_t bad = __ballot(lane < entries && nonempty &&
                                   (e0 != e_run || (unsigned)(e0 - 27) > 200u || e1 != e_run));
