@@ -33,22 +33,25 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     return __half2float(__ushort_as_half(h));  // exact
 }
 
-// The reference's table GELU (gemma4.c:243-262): linear interpolation inside
-// [lower, upper), table[0] below, identity above.
+// The reference's table GELU (gemma4.c:319-327): linear interpolation inside
+// (lower, upper), table[0] at or below lower, identity at or above upper (and
+// NaN for NaN).  Branch-free: both table loads are issued for every x, at an
+// index clamped into the table, so that the loads of many lookups go out
+// together instead of one branch -- and one wait -- per lookup.
 __device__ __forceinline__ float gelu_table_lookup(float x, const float *table, int size,
                                                    float lower, float upper) {
     const float scale = (float)(size - 1) / (upper - lower);
-    if (x <= lower) return table[0];
-    if (!(x >= upper)) {
-        const float position = (x - lower) * scale;
-        const int index = (int)position;
-        // x just below `upper` can round to position == size - 1 (x + 8 -> 16);
-        // the fraction is then 0 and the reference's result is table[size - 1].
-        if (index >= size - 1) return table[size - 1];
-        const float fraction = position - (float)index;
-        return table[index] + fraction * (table[index + 1] - table[index]);
-    }
-    return x;
+    // inside (lower, upper) xc == x: the position and index are the reference's
+    const float xc = fminf(fmaxf(x, lower), upper);  // NaN -> lower
+    const float position = (xc - lower) * scale;     // 0 .. size - 1
+    const int index = (int)position;
+    const int at = min(index, size - 2);
+    const float t0 = table[at], t1 = table[at + 1];  // t0 = table[0] for x <= lower
+    const float fraction = position - (float)index;
+    // x just below `upper` can round to position == size - 1 (x + 8 -> 16);
+    // the fraction is then 0 and the reference's result is table[size - 1]
+    const float inside = index >= size - 1 ? t1 : t0 + fraction * (t1 - t0);
+    return x <= lower ? t0 : (x >= upper || x != x) ? x : inside;
 }
 
 // ---- scratch owned by the library ------------------------------------------

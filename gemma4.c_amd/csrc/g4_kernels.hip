@@ -633,14 +633,21 @@ __global__ __launch_bounds__(256) void k_gemm_bg(float *__restrict__ out, size_t
         }
 }
 
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector-memory
+// operations are outstanding and leaves the LDS and export counters alone:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4 = 7, lgkmcnt 11:8 = 15.
+constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
 // Prefill W8A8 GEMM with every operand brought into LDS by the gfx950 LDS-DMA
 // loads (global_load_lds): no registers hold tiles in flight, and the number
 // of vector-memory instructions is kept low: each wave issues two 1-KB loads
 // per group (three with a second B operand), plus one 1-KB load of scales
 // every 8 groups.  Four LDS stages: group g is read while groups g + 1 ..
-// g + 3 are in flight.  64 x 64 outputs per 256-thread block (2 x 2 waves of
-// 32 x 32), one 64-deep K step per quantization group, the group-ordered fp32
-// fold of the reference (bit-identical).  Requires groups % 8 == 0.
+// g + 3 are in flight.  64 x 64 outputs per block of 4 waves (2 x 2 waves of
+// 32 x 32), or of 8 waves (2 x 4 waves of 32 x 16; waves 0-3 then fetch A,
+// waves 4-7 the B tiles, one load each per group), one 64-deep K step per
+// quantization group, the group-ordered fp32 fold of the reference
+// (bit-identical).  Requires groups % 8 == 0.
 //   A  64 rows x 64 B per group: wave w fetches rows 16w .. 16w + 15, lane L
 //      the 16-byte part (L & 3) ^ ((row >> 2) & 3) of row 16w + L / 4, so the
 //      parts of a row are stored XOR-swizzled and a lane's 16-byte operand
@@ -662,16 +669,23 @@ __global__ __launch_bounds__(256) void k_gemm_bg(float *__restrict__ out, size_t
 // K = 1 (16x16x1, four blocks), whose products are rounded exactly as a VALU
 // multiply, subnormals included.  Block b = 2 mi + ni takes its 16 row
 // scales and 16 column scales from lanes 16 b .. 16 b + 15, and its result
-// lands in the int8 MFMA's output layout (outputs 4 b .. 4 b + 3).
-template <int EPI>
-__global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_t out_stride,
-                                                  const int8_t *__restrict__ xq,
-                                                  const float *__restrict__ xs,
-                                                  const int8_t *__restrict__ w,
-                                                  const uint16_t *__restrict__ ws, int rows,
-                                                  int n_out, int k, GemmEpilogue ep) {
-    constexpr int BM = 64, BN = 64, NT = BN / 16, WN = BN / 2, NI = WN / 16;
+// lands in the int8 MFMA's output layout (outputs 4 b .. 4 b + 3); a wave of
+// 32 x 16 uses blocks 0 and 2.
+template <int EPI, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out, size_t out_stride,
+                                                         const int8_t *__restrict__ xq,
+                                                         const float *__restrict__ xs,
+                                                         const int8_t *__restrict__ w,
+                                                         const uint16_t *__restrict__ ws, int rows,
+                                                         int n_out, int k, GemmEpilogue ep) {
+    // WAVES = 4: 2 x 2 waves of 32 x 32 outputs; WAVES = 8: 2 x 4 waves of
+    // 32 x 16 (two waves a SIMD from one block, for grids of one block a CU)
+    constexpr int NWN = WAVES / 2, BM = 64, BN = 64, NT = BN / 16, WN = BN / NWN, NI = WN / 16;
     constexpr int NB = EPI == EPI_GELU_PAIR ? 2 : 1;  // B operands: (gate, up) or one
+    static_assert(WAVES == 4 || (WAVES == 8 && NB == 1), "8 waves: one B operand");
+    // vector-memory loads a wave issues per group: A and B (and B2) parts
+    // with 4 waves, one of A or B with 8
+    constexpr int LOADS = WAVES == 4 ? 1 + NB : 1;
     struct alignas(16) Stage {
         int8_t a[BM * 64];
         int8_t b[NB][NT * 1024];
@@ -683,37 +697,53 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
     // One __shared__ object per stage: the compiler then tells a read of one
     // stage from the DMA writes still landing in the others (with one array
     // it would wait for every DMA before every LDS read).
+    constexpr int S = 4;  // LDS stages
     __shared__ Stage st0, st1, st2, st3;
     __shared__ Scales sc0, sc1;
+    auto stage = [&](int i) __attribute__((always_inline)) -> Stage & {
+        return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3;
+    };
     const int groups = k >> 6;
     const int m0 = blockIdx.y * BM, nb0 = blockIdx.x * NT, n_blocks = n_out >> 4;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1, q = lane >> 4, l16 = lane & 15;
+    const int wm = wave / NWN, wn = wave % NWN, q = lane >> 4, l16 = lane & 15;
     constexpr int MAGIC = 0x4B400000;  // 1.5 * 2^23
     const v4i magic = {MAGIC, MAGIC, MAGIC, MAGIC};
     const v16f zero16 = {};
 
     // DMA sources (group 0, chunk 0); the builtin wants plain void pointers
-    const int a_row = 16 * wave + (lane >> 2);
+    // (8 waves: waves 0-3 fetch A, waves 4-7 B)
+    const int part = wave & 3;
+    const int a_row = 16 * part + (lane >> 2);
     const int8_t *a_src = xq + (size_t)min(m0 + a_row, rows - 1) * k +
                           16 * ((lane & 3) ^ ((a_row >> 2) & 3));
     const int unit = lane ^ ((lane >> 4) << 2);
-    const size_t b_at = (size_t)min(nb0 + wave, n_blocks - 1) * groups * 1024 + unit * 16;
+    const size_t b_at = (size_t)min(nb0 + part, n_blocks - 1) * groups * 1024 + unit * 16;
     const int8_t *b_src = w + b_at, *b2_src = NB == 2 ? ep.w2 + b_at : nullptr;
     const char *c_src;  // scales: 16 bytes a lane, advancing 8 groups per chunk
     size_t c_step;
     if (wave < 2) {
         c_src = (const char *)(xs + (size_t)min(m0 + lane, rows - 1) * groups + 4 * wave);
         c_step = 8 * sizeof(float);
-    } else {  // wave 2: the weight scales; wave 3: the second operand's (or again the first's)
+    } else {  // wave 2: the weight scales; wave 3: the second operand's (or
+              // again the first's into the padding, as do waves 4-7)
         const uint16_t *scales = NB == 2 && wave == 3 ? ep.ws2 : ws;
         c_src = (const char *)(scales + (size_t)min(nb0 + (lane >> 4), n_blocks - 1) * groups * 16 + 8 * l16);
         c_step = 8 * 16 * sizeof(uint16_t);
     }
-    const int c_dst = wave < 2 ? wave * (BM * 16) : 2 * BM * 16 + (wave - 2) * (NT * 8 * 16 * 2);
+    const int c_dst = wave < 2 ? wave * (BM * 16) : 2 * BM * 16 + min(wave - 2, 1) * (NT * 8 * 16 * 2);
+    // 8 waves: one source, step and stage offset per wave, chosen once
+    const int8_t *dma_src = wave < 4 ? a_src : b_src;
+    const int dma_step = wave < 4 ? 64 : 1024;
+    const int dma_dst = (wave < 4 ? 0 : (int)offsetof(Stage, b)) + part * 1024;
     auto issue = [&](int g, Stage &d) __attribute__((always_inline)) {
         g = min(g, groups - 1);  // past the end: reload the last group (never read)
+        if (WAVES == 8) {
+            __builtin_amdgcn_global_load_lds((const void *)(dma_src + (size_t)g * dma_step),
+                                             (void *)((char *)&d + dma_dst), 16, 0, 0);
+            return;
+        }
         __builtin_amdgcn_global_load_lds((const void *)(a_src + g * 64), (void *)(d.a + wave * 1024), 16, 0, 0);
         __builtin_amdgcn_global_load_lds((const void *)(b_src + (size_t)g * 1024), (void *)(d.b[0] + wave * 1024), 16, 0, 0);
         if (NB == 2)
@@ -756,7 +786,7 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
     // folded one step later, while the next group's MFMAs run: the fold never
     // waits on a fresh MFMA result.  The fetch only issues LDS reads (the
     // weight scale stays raw fp16 bits until the multiply step converts it).
-    static_assert(NI == 2, "the scale-product MFMA covers 2 x 2 tiles");
+    // (with NI = 1 only its blocks 0 and 2 are used)
     struct Dots {
         v4i d[NB][2][NI];  // 1.5 * 2^23 + dot, as int bits
         v16f c[NB];        // xs * ws, tile (mi, ni) at outputs 4 (2 mi + ni) ..
@@ -766,7 +796,8 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
         float xs;          // row scale of lane l's block (tile row l / 32)
         uint16_t ws[NB];   // column scale of lane l's block (tile column (l / 16) % 2)
     };
-    const int xs_row = wm * 32 + (lane >> 5) * 16 + l16, ws_tile = wn * NI + ((lane >> 4) & 1);
+    const int xs_row = wm * 32 + (lane >> 5) * 16 + l16;
+    const int ws_tile = NI == 2 ? wn * NI + ((lane >> 4) & 1) : wn;
     auto fetch = [&](const Stage &d, const Scales &s, int j, Frags &f) __attribute__((always_inline)) {
 #pragma unroll
         for (int mi = 0; mi < 2; mi++) f.a[mi] = *reinterpret_cast<const v4i *>(d.a + a_off[mi]);
@@ -805,22 +836,23 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
     };
 
     // Step g (j = g % 8): wait until group g (and its chunk's scales) has
-    // landed -- groups g + 1, g + 2 may still be in flight -- and let the
-    // barrier publish it; then issue group g + 3 into the stage of group g - 1
-    // (every wave finished reading it before the barrier), plus the next
-    // chunk's scales when g + 3 starts one; read group g's operands, fold
-    // group g - 1 and issue group g's MFMAs.
+    // landed -- groups g + 1 .. g + S - 2 may still be in flight -- and let
+    // the barrier publish it; then issue group g + S - 1 into the stage of
+    // group g - 1 (every wave finished reading it before the barrier), plus
+    // the next chunk's scales when g + S - 1 starts one; read group g's
+    // operands, fold group g - 1 and issue group g's MFMAs.
+    constexpr int in_flight = (S - 2) * LOADS;  // loads of groups g + 1 .. g + S - 2
     auto step = [&](int g, int j, Stage &fill, const Stage &use, const Scales &sc_use,
                     Scales &sc_fill, Dots &cur, const Dots &prev) __attribute__((always_inline)) {
-        // in flight: groups g + 1, g + 2 (1 + NB loads each), and at j = 6, 7
-        // the next chunk's scales (issued after group g + 1 or g + 2)
-        if (j == 6 || j == 7)
-            __builtin_amdgcn_s_waitcnt(0xF70 | (2 * (1 + NB) + 1));
+        // the next chunk's scales (issued right after its first group) are
+        // also in flight once that group is among g + 1 .. g + S - 2
+        if (j + S - 2 >= 8)
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(in_flight + 1));
         else
-            __builtin_amdgcn_s_waitcnt(0xF70 | (2 * (1 + NB)));
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(in_flight));
         __builtin_amdgcn_s_barrier();
-        issue(g + 3, fill);
-        if (j == 5) issue_scales(g / 8 + 1, sc_fill);
+        issue(g + S - 1, fill);
+        if (j == (9 - S) % 8) issue_scales(g / 8 + 1, sc_fill);
         Frags f;
         fetch(use, sc_use, j, f);       // LDS reads in flight ...
         __builtin_amdgcn_sched_barrier(0);
@@ -842,19 +874,20 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
     }
     issue(0, st0);
     issue_scales(0, sc0);
-    issue(1, st1);
-    issue(2, st2);
+#pragma unroll
+    for (int i = 1; i < S - 1; i++) issue(i, stage(i));
     // 16 groups per pass so that every stage and scale buffer is a fixed
-    // object (chunk c = g / 8 lives in sc0 for even c, sc1 for odd c)
+    // object (group g in stage g % S; chunk c = g / 8 in sc0 for even c, sc1
+    // for odd c)
     auto eight = [&](int g, Scales &sc_use, Scales &sc_next) __attribute__((always_inline)) {
-        step(g + 0, 0, st3, st0, sc_use, sc_next, d0, d1);
-        step(g + 1, 1, st0, st1, sc_use, sc_next, d1, d0);
-        step(g + 2, 2, st1, st2, sc_use, sc_next, d0, d1);
-        step(g + 3, 3, st2, st3, sc_use, sc_next, d1, d0);
-        step(g + 4, 4, st3, st0, sc_use, sc_next, d0, d1);
-        step(g + 5, 5, st0, st1, sc_use, sc_next, d1, d0);
-        step(g + 6, 6, st1, st2, sc_use, sc_next, d0, d1);
-        step(g + 7, 7, st2, st3, sc_use, sc_next, d1, d0);
+        step(g + 0, 0, stage((S - 1) % S), stage(0 % S), sc_use, sc_next, d0, d1);
+        step(g + 1, 1, stage((S + 0) % S), stage(1 % S), sc_use, sc_next, d1, d0);
+        step(g + 2, 2, stage((S + 1) % S), stage(2 % S), sc_use, sc_next, d0, d1);
+        step(g + 3, 3, stage((S + 2) % S), stage(3 % S), sc_use, sc_next, d1, d0);
+        step(g + 4, 4, stage((S + 3) % S), stage(4 % S), sc_use, sc_next, d0, d1);
+        step(g + 5, 5, stage((S + 4) % S), stage(5 % S), sc_use, sc_next, d1, d0);
+        step(g + 6, 6, stage((S + 5) % S), stage(6 % S), sc_use, sc_next, d0, d1);
+        step(g + 7, 7, stage((S + 6) % S), stage(7 % S), sc_use, sc_next, d1, d0);
     };
     int g = 0;
     for (; g + 16 <= groups; g += 16) {
@@ -884,24 +917,30 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
     // each of its rows.  gelu(gate) * up (or * mul), then k_quantize's
     // arithmetic: row absmax over the 64 columns (16 lanes x NI tiles in this
     // wave, and the other N-half's wave through LDS), scale = absmax / 127.
-    __shared__ float s_rowmax[2][BM];  // [wn][row]
+    __shared__ float s_rowmax[NWN][BM];  // [wn][row]
     float val[2][NI][4], rmax[2][4];
+    // every lookup (and multiplier) first, so that their loads go out together
 #pragma unroll
     for (int mi = 0; mi < 2; mi++)
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int m = min(m0 + wm * 32 + mi * 16 + 4 * q + v, rows - 1);
-            float mx = 0.0f;
 #pragma unroll
             for (int ni = 0; ni < NI; ni++) {
                 const int n = nb0 * 16 + wn * WN + ni * 16 + l16;
                 const float gl = gelu_table_lookup(acc[0][mi][ni][v], ep.gelu_table, ep.gelu_size,
                                                    ep.gelu_lower, ep.gelu_upper);
-                const float x = EPI == EPI_GELU_PAIR ? gl * acc[NB - 1][mi][ni][v]
-                                                     : gl * ep.mul[(size_t)m * ep.mul_stride + n];
-                val[mi][ni][v] = x;
-                mx = fmaxf(mx, fabsf(x));
+                val[mi][ni][v] = EPI == EPI_GELU_PAIR ? gl * acc[NB - 1][mi][ni][v]
+                                                      : gl * ep.mul[(size_t)m * ep.mul_stride + n];
             }
+        }
+#pragma unroll
+    for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            float mx = 0.0f;
+#pragma unroll
+            for (int ni = 0; ni < NI; ni++) mx = fmaxf(mx, fabsf(val[mi][ni][v]));
 #pragma unroll
             for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
             rmax[mi][v] = mx;
@@ -914,7 +953,10 @@ __global__ __launch_bounds__(256) void k_gemm_dma(float *__restrict__ out, size_
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int r = wm * 32 + mi * 16 + 4 * q + v, m = m0 + r;
-            const float scale = fmaxf(rmax[mi][v], s_rowmax[wn ^ 1][r]) / 127.0f;
+            float mx = rmax[mi][v];
+#pragma unroll
+            for (int o = 1; o < NWN; o++) mx = fmaxf(mx, s_rowmax[(wn + o) % NWN][r]);
+            const float scale = mx / 127.0f;
             const float inverse = scale > 0.0f ? 1.0f / scale : 0.0f;
             if (m >= rows) continue;
 #pragma unroll
@@ -1054,18 +1096,26 @@ int launch_gemv_fused(hipStream_t s, const GemvJob &job, int epi) {
     return G4_OK;
 }
 
+// Grids of at most one block a CU (256 CUs) take 8-wave blocks: a lone
+// block's step is bound by latency, which two waves a SIMD partly hide.
+static bool small_grid(unsigned blocks) { return blocks <= 256; }
+
 int launch_matmul_gelu(hipStream_t s, const int8_t *xq, const float *xs, const int8_t *w,
                        const uint16_t *ws, int n_out, int k, int rows, int epi,
                        const GemmEpilogue &ep) {
     if (rows <= 8 || k % 512 || n_out % 64 || (epi != EPI_GELU_PAIR && epi != EPI_GELU_MUL))
         return set_error(G4_ERR_ARG, "fused GEMM: shape %d x %d x %d does not fit", rows, n_out, k);
     const dim3 grid((unsigned)(n_out / 64), (unsigned)((rows + 63) / 64));
+    // the pair variant's 8 stages would take 104 KB: one block per CU
     if (epi == EPI_GELU_PAIR)
-        hipLaunchKernelGGL(k_gemm_dma<EPI_GELU_PAIR>, grid, dim3(256), 0, s, nullptr, (size_t)0, xq, xs, w,
-                           ws, rows, n_out, k, ep);
+        hipLaunchKernelGGL((k_gemm_dma<EPI_GELU_PAIR, 4>), grid, dim3(256), 0, s, nullptr, (size_t)0,
+                           xq, xs, w, ws, rows, n_out, k, ep);
+    else if (small_grid(grid.x * grid.y))
+        hipLaunchKernelGGL((k_gemm_dma<EPI_GELU_MUL, 8>), grid, dim3(512), 0, s, nullptr,
+                           (size_t)0, xq, xs, w, ws, rows, n_out, k, ep);
     else
-        hipLaunchKernelGGL(k_gemm_dma<EPI_GELU_MUL>, grid, dim3(256), 0, s, nullptr, (size_t)0, xq, xs, w,
-                           ws, rows, n_out, k, ep);
+        hipLaunchKernelGGL((k_gemm_dma<EPI_GELU_MUL, 4>), grid, dim3(256), 0, s, nullptr, (size_t)0,
+                           xq, xs, w, ws, rows, n_out, k, ep);
     return G4_OK;
 }
 
@@ -1075,9 +1125,13 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
     const int blocks = n_out / 16, groups = k / 64;
     if (rows > 8) {
         const unsigned mb = (unsigned)((rows + 63) / 64);
-        if (groups % 8 == 0)
-            hipLaunchKernelGGL(k_gemm_dma<EPI_PLAIN>, dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0,
-                               s, out, out_stride, xq, xs, w, ws, rows, n_out, k, GemmEpilogue{});
+        const dim3 grid((unsigned)((blocks + 3) / 4), mb);
+        if (groups % 8 == 0 && small_grid(grid.x * grid.y))
+            hipLaunchKernelGGL((k_gemm_dma<EPI_PLAIN, 8>), grid, dim3(512), 0, s, out,
+                               out_stride, xq, xs, w, ws, rows, n_out, k, GemmEpilogue{});
+        else if (groups % 8 == 0)
+            hipLaunchKernelGGL((k_gemm_dma<EPI_PLAIN, 4>), grid, dim3(256), 0, s, out, out_stride, xq,
+                               xs, w, ws, rows, n_out, k, GemmEpilogue{});
         else
             hipLaunchKernelGGL((k_gemm<64, 1>), dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
                                out, out_stride, xq, xs, w, ws, rows, n_out, k);

@@ -103,6 +103,19 @@ def test_matmul_row_counts_bitexact(pkg, g4lib, torch_gpu, ok, rows):
     assert np.array_equal(y, ok.matmul(xq, xs, hw.record, n))
 
 
+# Prefill products of a layer: grids of 16 to 256 blocks take the 8-stage
+# pipeline, larger ones the 4-stage one (launch_matmul).
+@pytest.mark.parametrize("rows,n,k", [(512, 256, 1536), (512, 2048, 1536), (200, 1536, 6144),
+                                      (64, 1536, 12288), (1000, 512, 1536)])
+def test_matmul_prefill_shapes_bitexact(pkg, g4lib, torch_gpu, ok, rows, n, k):
+    g = rng(rows * 7 + n + k)
+    w, s = random_weight(g, n, k)
+    hw = HostWeight(pkg, w, s)
+    xq, xs = ok.quantize(g.standard_normal((rows, k)).astype(np.float32))
+    y = gpu_matmul(pkg, g4lib, torch_gpu, DeviceWeight(pkg, torch_gpu, hw), xq, xs)
+    assert np.array_equal(y, ok.matmul(xq, xs, hw.record, n))
+
+
 def test_matmul_prefill_config_bitexact(pkg, g4lib, torch_gpu, ok):
     """The prefill GEMM workload: X [512 x 1536] N(0,1), W [6144 x 1536]."""
     g = rng(2026)
