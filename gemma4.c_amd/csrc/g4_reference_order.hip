@@ -766,9 +766,29 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     if (kfirst + (int)blockIdx.x * KB > pos_last) return;
     const int mask = cache_len - 1, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *qt = q + (size_t)t0 * 8 * HD;
-    for (int i = tid; i < tn * 8 * HD; i += 256) {
-        const int row = i / HD, j = i % HD;
-        s_q[row][j & 15][j >> 4] = qt[i];
+    {
+        // every thread's 16-byte query loads go out before its first LDS
+        // write (one load, wait and write at a time would cost a memory
+        // latency per float)
+        constexpr int QV = TQ * 8 * HD / 4 / 256;
+        static_assert(TQ * 8 * HD % 1024 == 0, "whole float4s per thread");
+        const int count = tn * 8 * HD;
+        float4 qv[QV];
+#pragma unroll
+        for (int u = 0; u < QV; u++) {
+            const int i = 4 * (tid + 256 * u);
+            qv[u] = i < count ? *reinterpret_cast<const float4 *>(qt + i) : make_float4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < QV; u++) {
+            const int i = 4 * (tid + 256 * u), row = i / HD, j = i % HD;
+            if (i < count) {
+                s_q[row][(j + 0) & 15][(j + 0) >> 4] = qv[u].x;
+                s_q[row][(j + 1) & 15][(j + 1) >> 4] = qv[u].y;
+                s_q[row][(j + 2) & 15][(j + 2) >> 4] = qv[u].z;
+                s_q[row][(j + 3) & 15][(j + 3) >> 4] = qv[u].w;
+            }
+        }
     }
     __syncthreads();
     const int m = lane & 15, kg = lane >> 4;
