@@ -247,7 +247,7 @@ def gemv_sweep(pkg, lib, torch) -> dict:
     }
 
 
-def model_benchmarks(pkg, lib, np, steps: int, warmup: int) -> dict:
+def model_benchmarks(pkg, lib, np, steps: int, warmup: int, prefill_only: bool = False) -> dict:
     rng = np.random.default_rng(3)
     out = np.empty(pkg.VOCAB, np.float32)
 
@@ -269,6 +269,8 @@ def model_benchmarks(pkg, lib, np, steps: int, warmup: int) -> dict:
     elapsed = time.perf_counter() - start
     res = {"prefill512_s": elapsed, "prefill512_tok_s": 512 * steps / elapsed}
     log(f"prefill 512: {res['prefill512_tok_s']:.0f} tok/s ({elapsed / steps * 1e3:.2f} ms/step)")
+    if prefill_only:
+        return res
 
     # prefill 8192 in 512-token chunks: 1 warmup + mean of 3
     t8k = rng.integers(0, pkg.VOCAB, 8192).astype(np.int32)
@@ -359,8 +361,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--order", choices=["reference", "parallel"], default="reference")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--probe", choices=["gemm", "gemv", "copy"],
-                    help="only launch one kernel 20 times (for rocprofv3 --pmc runs); no JSON")
+    ap.add_argument("--probe", choices=["gemm", "gemv", "copy", "prefill"],
+                    help="only launch one kernel 20 times (for rocprofv3 --pmc runs), or run "
+                         "3 + 10 prefill-512 steps of the model (prefill); no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -377,6 +380,15 @@ def main() -> int:
     pkg = __graft_entry__.load_package()
     lib = pkg.lib()
     lib.g4_set_order(pkg.ORDER_REFERENCE if args.order == "reference" else pkg.ORDER_PARALLEL)
+    if args.probe == "prefill":
+        # the headline step alone, for a kernel trace of one 512-token prefill
+        image = pkg.Image.synthetic(seed=MODEL_SEED)
+        pkg.check(lib.g4_init(image.records, 0))
+        try:
+            model_benchmarks(pkg, lib, np, 10, 3, prefill_only=True)
+        finally:
+            lib.g4_shutdown()
+        return 0
     if args.probe:
         probe(pkg, lib, torch, args.probe)
         return 0
