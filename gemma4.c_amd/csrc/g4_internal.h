@@ -143,9 +143,24 @@ struct GemmEpilogue {
     float gelu_lower, gelu_upper;
     int8_t *q_out;
     float *qs_out;
+    // EPI_PLAIN with up to two more products of the same input (q, k, v):
+    // column blocks [0, cols[0]) are the launch's own matrix, the next
+    // cols[1] matrix 1, the next cols[2] matrix 2
+    int cols[3];
+    const int8_t *gw[2];
+    const uint16_t *gws[2];
+    float *gout[2];
+    size_t gstride[2];
+    int gn[2];
 };
 // Returns G4_ERR_ARG (and launches nothing) when the shape does not fit the
 // fused kernel (rows <= 8, K not a multiple of 512, N not of 64).
+// Up to three products of the same many-row input in one launch (K equal,
+// groups % 8 == 0, rows > 8): out[i] = x W[i]^T at out_stride[i].  Returns
+// G4_ERR_ARG (and launches nothing) when they do not fit.
+int launch_matmul_group(hipStream_t s, const int8_t *xq, const float *xs, int rows, int k, int count,
+                        const int8_t *const *w, const uint16_t *const *ws, float *const *out,
+                        const size_t *out_stride, const int *n_out);
 int launch_matmul_gelu(hipStream_t s, const int8_t *xq, const float *xs, const int8_t *w,
                        const uint16_t *ws, int n_out, int k, int rows, int epi,
                        const GemmEpilogue &ep);

@@ -704,7 +704,17 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
         return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3;
     };
     const int groups = k >> 6;
-    const int m0 = blockIdx.y * BM, nb0 = blockIdx.x * NT, n_blocks = n_out >> 4;
+    int bx = blockIdx.x;
+    if (EPI == EPI_PLAIN && bx >= ep.cols[0]) {  // a grouped launch's matrix 1 or 2 (uniform)
+        const int i = bx - ep.cols[0] < ep.cols[1] ? 0 : 1;
+        bx -= ep.cols[0] + (i ? ep.cols[1] : 0);
+        w = ep.gw[i];
+        ws = ep.gws[i];
+        out = ep.gout[i];
+        out_stride = ep.gstride[i];
+        n_out = ep.gn[i];
+    }
+    const int m0 = blockIdx.y * BM, nb0 = bx * NT, n_blocks = n_out >> 4;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / NWN, wn = wave % NWN, q = lane >> 4, l16 = lane & 15;
@@ -964,7 +974,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
                 const int n = nb0 * 16 + wn * WN + ni * 16 + l16;
                 ep.q_out[(size_t)m * n_out + n] = (int8_t)(int)rintf(val[mi][ni][v] * inverse);
             }
-            if (wn == 0 && l16 == 0) ep.qs_out[(size_t)m * groups_out + blockIdx.x] = scale;
+            if (wn == 0 && l16 == 0) ep.qs_out[(size_t)m * groups_out + bx] = scale;
         }
 }
 
@@ -1119,6 +1129,36 @@ int launch_matmul_gelu(hipStream_t s, const int8_t *xq, const float *xs, const i
     return G4_OK;
 }
 
+int launch_matmul_group(hipStream_t s, const int8_t *xq, const float *xs, int rows, int k, int count,
+                        const int8_t *const *w, const uint16_t *const *ws, float *const *out,
+                        const size_t *out_stride, const int *n_out) {
+    if (rows <= 8 || k % 512 || count < 1 || count > 3)
+        return set_error(G4_ERR_ARG, "grouped GEMM: %d products of %d rows x K %d do not fit", count, rows, k);
+    GemmEpilogue ep{};
+    unsigned cols = 0;
+    for (int i = 0; i < count; i++) {
+        if (n_out[i] <= 0 || n_out[i] % 16)
+            return set_error(G4_ERR_ARG, "grouped GEMM: N %d is not a multiple of 16", n_out[i]);
+        ep.cols[i] = (n_out[i] / 16 + 3) / 4;
+        cols += (unsigned)ep.cols[i];
+        if (i) {
+            ep.gw[i - 1] = w[i];
+            ep.gws[i - 1] = ws[i];
+            ep.gout[i - 1] = out[i];
+            ep.gstride[i - 1] = out_stride[i];
+            ep.gn[i - 1] = n_out[i];
+        }
+    }
+    const dim3 grid(cols, (unsigned)((rows + 63) / 64));
+    if (small_grid(grid.x * grid.y))
+        hipLaunchKernelGGL((k_gemm_dma<EPI_PLAIN, 8>), grid, dim3(512), 0, s, out[0], out_stride[0], xq, xs,
+                           w[0], ws[0], rows, n_out[0], k, ep);
+    else
+        hipLaunchKernelGGL((k_gemm_dma<EPI_PLAIN, 4>), grid, dim3(256), 0, s, out[0], out_stride[0], xq, xs,
+                           w[0], ws[0], rows, n_out[0], k, ep);
+    return G4_OK;
+}
+
 int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq, const float *xs,
                   const int8_t *w, const uint16_t *ws, int n_out, int k, int rows) {
     if (rows <= 0) return G4_OK;
@@ -1126,12 +1166,14 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
     if (rows > 8) {
         const unsigned mb = (unsigned)((rows + 63) / 64);
         const dim3 grid((unsigned)((blocks + 3) / 4), mb);
+        GemmEpilogue ep{};
+        ep.cols[0] = (int)grid.x;
         if (groups % 8 == 0 && small_grid(grid.x * grid.y))
             hipLaunchKernelGGL((k_gemm_dma<EPI_PLAIN, 8>), grid, dim3(512), 0, s, out,
-                               out_stride, xq, xs, w, ws, rows, n_out, k, GemmEpilogue{});
+                               out_stride, xq, xs, w, ws, rows, n_out, k, ep);
         else if (groups % 8 == 0)
             hipLaunchKernelGGL((k_gemm_dma<EPI_PLAIN, 4>), grid, dim3(256), 0, s, out, out_stride, xq,
-                               xs, w, ws, rows, n_out, k, GemmEpilogue{});
+                               xs, w, ws, rows, n_out, k, ep);
         else
             hipLaunchKernelGGL((k_gemm<64, 1>), dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
                                out, out_stride, xq, xs, w, ws, rows, n_out, k);

@@ -384,12 +384,20 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
                 job.count = 3;
             }
             G4_TRY(launch_gemv_fused(s, job, EPI_PLAIN));
+        } else if (L.k.data && n > 8 && G4_HIDDEN % 512 == 0) {
+            // q, k and v read the same rows: one launch fills the chip
+            const int8_t *w[3] = {L.q.data, L.k.data, L.v.data};
+            const uint16_t *ws[3] = {L.q.scales, L.k.scales, L.v.scales};
+            float *out[3] = {c.aux, c.k_new, c.v_new};
+            const size_t strides[3] = {(size_t)qw, (size_t)hd, (size_t)hd};
+            const int ns[3] = {L.q.n, L.k.n, L.v.n};
+            G4_TRY(launch_matmul_group(s, c.q8, c.qs, n, G4_HIDDEN, 3, w, ws, out, strides, ns));
         } else {
             G4_TRY(matmul(c, c.aux, qw, L.q, n));
-        }
-        if (L.k.data && !one) {
-            G4_TRY(matmul(c, c.k_new, hd, L.k, n));
-            G4_TRY(matmul(c, c.v_new, hd, L.v, n));
+            if (L.k.data) {
+                G4_TRY(matmul(c, c.k_new, hd, L.k, n));
+                G4_TRY(matmul(c, c.v_new, hd, L.v, n));
+            }
         }
         if (fused) {  // query norms + RoPE and the new key/value rows: one launch
             launch_qkv_finish(s, c.aux, heads, L.q_norm, L.k.data ? c.k_new : nullptr, c.v_new,
