@@ -1062,7 +1062,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
                                                             const float *__restrict__ value_cache,
                                                             int cache_len, int full, int start_pos,
                                                             int n, const int *__restrict__ pos_dev,
-                                                            size_t stride) {
+                                                            size_t stride, int8_t *__restrict__ q8,
+                                                            float *__restrict__ qs) {
     constexpr int THREADS = WAVES * 64;
     if (pos_dev) start_pos = *pos_dev;
     constexpr int TOKENS = WAVES * HPW / 8;     // tokens per block
@@ -1192,9 +1193,24 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
 #pragma unroll
         for (int s = 0; s < DEPTH; s++) step(tile + s, ring[s], pring[s]);
     }
-    if (active) {
+    if (!active) return;
+    if (!q8) {
 #pragma unroll
         for (int e = 0; e < HPW; e++) out[((size_t)my_t * 8 + h0 + e) * HD + d0 + lane] = o[e];
+        return;
+    }
+    // the o projection's input quantized here (k_quantize's arithmetic): the
+    // wave's 64 lanes of head h0 + e are one 64-channel group of the row
+#pragma unroll
+    for (int e = 0; e < HPW; e++) {
+        float m = fabsf(o[e]);
+#pragma unroll
+        for (int x = 32; x > 0; x >>= 1) m = fmaxf(m, __shfl_xor(m, x));
+        const float gscale = m / 127.0f;
+        const float inverse = gscale > 0.0f ? 1.0f / gscale : 0.0f;
+        const size_t at = ((size_t)my_t * 8 + h0 + e) * HD + d0;
+        q8[at + lane] = (int8_t)(int)rintf(o[e] * inverse);
+        if (lane == 0) qs[at / 64] = gscale;
     }
 }
 
@@ -1502,12 +1518,14 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
 #undef G4_PV_DECODE
     } else {  // prefill: 4 tokens x 8 heads per block share each V tile
         dim3 grid(slices, (nn + 3) / 4);
+        // with q8 the kernel writes the quantized rows (and no fp32 ones)
         if (head_dim == 256)
             hipLaunchKernelGGL((k_attn_values<256, 4, 8, 2>), grid, dim3(256), 0, s, out, scores,
-                               value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride);
+                               value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride, q8, qs);
         else
             hipLaunchKernelGGL((k_attn_values<512, 4, 8, 2>), grid, dim3(256), 0, s, out, scores,
-                               value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride);
+                               value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride, q8, qs);
+        return G4_OK;
     }
     if (q8) launch_quantize(s, q8, qs, out, n * heads * head_dim / 64);
     return G4_OK;
