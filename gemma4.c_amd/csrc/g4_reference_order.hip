@@ -1021,7 +1021,9 @@ __global__ __launch_bounds__(64) void k_attn_softmax_reference(float *__restrict
                                                                const int *__restrict__ pos_dev,
                                                                size_t stride) {
     if (pos_dev) start_pos = *pos_dev;
-    const int h = blockIdx.x, t = blockIdx.y;
+    // last token first: rows grow with the token (causal), so the longest
+    // start first and the short ones fill in behind them
+    const int h = blockIdx.x, t = gridDim.y - 1 - blockIdx.y;
     const int pos = start_pos + t, keys = pos + 1 - first_visible(pos, full);
     softmax_row_reference(scores + ((size_t)t * heads + h) * stride, keys);
 }
