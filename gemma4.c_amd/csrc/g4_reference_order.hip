@@ -1074,7 +1074,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
     __shared__ __attribute__((aligned(16))) float s_p[WAVES][HPW][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int d0 = blockIdx.x * 64, t0 = blockIdx.y * TOKENS;
+    // last tokens first: their windows hold the most tiles
+    const int d0 = blockIdx.x * 64, t0 = (gridDim.y - 1 - blockIdx.y) * TOKENS;
     const int tn = n - t0 < TOKENS ? n - t0 : TOKENS;
     const int mask = cache_len - 1;
     const int pos_last = start_pos + t0 + tn - 1;
