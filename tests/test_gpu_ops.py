@@ -282,6 +282,37 @@ def test_elementwise_golden_bitexact(pkg, g4lib, torch_gpu):
     assert np.array_equal(host(a), gold["add_out"])
 
 
+def test_geglu_table_edges_bitexact(pkg, g4lib, torch_gpu, image, ok):
+    """The GELU table's boundaries (gemma4.c:319-327): at and around lower and
+    upper, the top interpolation cell (x just below upper, whose position can
+    round to the last entry), +-inf, signed zeros and tiny values."""
+    torch = torch_gpu
+    below_upper = np.nextafter(np.float32(8.0), np.float32(0.0))
+    edges = np.array([-8.0, np.nextafter(np.float32(-8.0), np.float32(0.0)),
+                      np.nextafter(np.float32(-8.0), np.float32(-9.0)), 8.0, below_upper,
+                      np.nextafter(below_upper, np.float32(0.0)), 7.9999, 7.998, -7.998,
+                      0.0, -0.0, 1e-30, -1e-30, np.inf, -np.inf, 100.0, -100.0, 3.0e38], np.float32)
+    gate = np.tile(edges, (3, 1))
+    up = np.random.default_rng(5).standard_normal(gate.shape).astype(np.float32)
+    width = gate.shape[1]
+    table = image.array(pkg.GELU_TABLE)
+    gd, ud, td = dev(torch, gate), dev(torch, up), dev(torch, table)
+    pkg.check(g4lib.g4_geglu(None, gd.data_ptr(), ud.data_ptr(), 3, width, width, td.data_ptr(), 4096, -8.0, 8.0))
+    torch.cuda.synchronize()
+    want = ok.geglu(gate, up, width, image.records[pkg.GELU_TABLE])
+    # where x + 8 rounds to 16 the position is the last entry and the fraction
+    # 0: the reference reads one float past the table and multiplies it by 0,
+    # which gives table[4095] for a finite neighbour (the oracle reads whatever
+    # follows its copy of the table, so that case is stated directly)
+    with np.errstate(over="ignore", invalid="ignore"):  # 3e38 and inf overflow: outside anyway
+        position = (gate - np.float32(-8.0)) * np.float32(4095.0 / 16.0)
+    last = (gate < np.float32(8.0)) & (gate > np.float32(-8.0)) & (position >= np.float32(4095.0))
+    assert last.any()  # the case is exercised
+    want = np.where(last, np.float32(table[4095]) * up, want).astype(np.float32)
+    got = host(gd)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (edges, got[0], want[0])
+
+
 def test_model_tables_bitexact(pkg, g4lib, torch_gpu, image, ok):
     """geglu with the image's GELU table; embeddings and RoPE from the image."""
     torch = torch_gpu
