@@ -103,8 +103,8 @@ def test_matmul_row_counts_bitexact(pkg, g4lib, torch_gpu, ok, rows):
     assert np.array_equal(y, ok.matmul(xq, xs, hw.record, n))
 
 
-# Prefill products of a layer: grids of 16 to 256 blocks take the 8-stage
-# pipeline, larger ones the 4-stage one (launch_matmul).
+# Prefill products of a layer: grids of up to 256 blocks take 8-wave blocks,
+# larger ones 4-wave blocks (launch_matmul).
 @pytest.mark.parametrize("rows,n,k", [(512, 256, 1536), (512, 2048, 1536), (200, 1536, 6144),
                                       (64, 1536, 12288), (1000, 512, 1536)])
 def test_matmul_prefill_shapes_bitexact(pkg, g4lib, torch_gpu, ok, rows, n, k):
