@@ -1519,14 +1519,15 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
             else G4_PV_DECODE(512, false);
         }
 #undef G4_PV_DECODE
-    } else {  // prefill: 4 tokens x 8 heads per block share each V tile
+    } else {  // prefill: 4 tokens x 8 heads per block share each V tile; one
+              // tile of prefetch (deeper rings cost registers, hence waves)
         dim3 grid(slices, (nn + 3) / 4);
         // with q8 the kernel writes the quantized rows (and no fp32 ones)
         if (head_dim == 256)
-            hipLaunchKernelGGL((k_attn_values<256, 4, 8, 2>), grid, dim3(256), 0, s, out, scores,
+            hipLaunchKernelGGL((k_attn_values<256, 4, 8, 1>), grid, dim3(256), 0, s, out, scores,
                                value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride, q8, qs);
         else
-            hipLaunchKernelGGL((k_attn_values<512, 4, 8, 2>), grid, dim3(256), 0, s, out, scores,
+            hipLaunchKernelGGL((k_attn_values<512, 4, 8, 1>), grid, dim3(256), 0, s, out, scores,
                                value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride, q8, qs);
         return G4_OK;
     }
