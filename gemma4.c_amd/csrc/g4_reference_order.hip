@@ -1481,19 +1481,18 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
         return n > 4 && blocks > cap ? cap : blocks;
     };
     const unsigned nn = (unsigned)n;
-    // decode: 4 keys per 16-lane group; many tokens at head_dim 256: 8 (twice
-    // the fmas per query value read from LDS; at 512 the 8 keys' channel
-    // slices would not fit in registers).  Few tokens per block (2 at 256, 1
-    // at 512): a block's waves run one chain of work each, so more blocks
-    // (more waves a SIMD) hide more of its latencies than staging the keys
-    // for more tokens saves.
+    // 4 keys per 16-lane group (8 would halve the query reads from LDS, but
+    // its 250 registers leave 2 waves a SIMD against 3).  Few tokens per
+    // block in prefill (2 at head_dim 256, 1 at 512): a block's waves run one
+    // chain of work each, so more blocks (more waves a SIMD) hide more of its
+    // latencies than staging the keys for more tokens saves.
 #define G4_SCORES(HD, TQ, KG)                                                                     \
     hipLaunchKernelGGL((k_attn_scores<HD, TQ, KG>), dim3(key_blocks(TQ, 16 * KG), (nn + TQ - 1) / TQ), \
                        dim3(256), 0, s, q, key_cache, cache_len, full, start_pos, (int)n, pos_dev,  \
                        stride, scores)
     if (head_dim == 256) {
         if (n <= 4) G4_SCORES(256, 6, 4);
-        else G4_SCORES(256, 2, 8);
+        else G4_SCORES(256, 2, 4);
     } else {
         G4_SCORES(512, 1, 4);
     }
