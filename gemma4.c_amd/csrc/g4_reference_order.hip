@@ -1482,17 +1482,17 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
     };
     const unsigned nn = (unsigned)n;
     // 4 keys per 16-lane group (8 would halve the query reads from LDS, but
-    // its 250 registers leave 2 waves a SIMD against 3).  Few tokens per
-    // block in prefill (2 at head_dim 256, 1 at 512): a block's waves run one
-    // chain of work each, so more blocks (more waves a SIMD) hide more of its
-    // latencies than staging the keys for more tokens saves.
+    // its 250 registers leave 2 waves a SIMD against 3).  One token per block
+    // in prefill: a block's waves run one chain of work each, so more blocks
+    // (more waves a SIMD) hide more of its latencies than staging the keys
+    // for more tokens saves.
 #define G4_SCORES(HD, TQ, KG)                                                                     \
     hipLaunchKernelGGL((k_attn_scores<HD, TQ, KG>), dim3(key_blocks(TQ, 16 * KG), (nn + TQ - 1) / TQ), \
                        dim3(256), 0, s, q, key_cache, cache_len, full, start_pos, (int)n, pos_dev,  \
                        stride, scores)
     if (head_dim == 256) {
         if (n <= 4) G4_SCORES(256, 6, 4);
-        else G4_SCORES(256, 2, 4);
+        else G4_SCORES(256, 1, 4);
     } else {
         G4_SCORES(512, 1, 4);
     }
