@@ -367,7 +367,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(this path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(this build runs the forward path on a single GPU)", file=sys.stderr)
         return 2
 
     import numpy as np
