@@ -645,7 +645,9 @@ constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 // every 8 groups.  Four LDS stages: group g is read while groups g + 1 ..
 // g + 3 are in flight.  64 x 64 outputs per block of 4 waves (2 x 2 waves of
 // 32 x 32), or of 8 waves (2 x 4 waves of 32 x 16; waves 0-3 then fetch A,
-// waves 4-7 the B tiles, one load each per group), one 64-deep K step per
+// waves 4-7 the B tiles, one load each per group), or 64 x 48 outputs per
+// block of 6 waves (2 x 3 of 32 x 16; waves 0-3 fetch A, waves 4, 5 and 0 the
+// three B tiles), one 64-deep K step per
 // quantization group, the group-ordered fp32 fold of the reference
 // (bit-identical).  Requires groups % 8 == 0.
 //   A  64 rows x 64 B per group: wave w fetches rows 16w .. 16w + 15, lane L
@@ -671,7 +673,7 @@ constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 // scales and 16 column scales from lanes 16 b .. 16 b + 15, and its result
 // lands in the int8 MFMA's output layout (outputs 4 b .. 4 b + 3); a wave of
 // 32 x 16 uses blocks 0 and 2.
-template <int EPI, int WAVES>
+template <int EPI, int WAVES, int NT = 4>
 __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out, size_t out_stride,
                                                          const int8_t *__restrict__ xq,
                                                          const float *__restrict__ xs,
@@ -680,9 +682,13 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
                                                          int n_out, int k, GemmEpilogue ep) {
     // WAVES = 4: 2 x 2 waves of 32 x 32 outputs; WAVES = 8: 2 x 4 waves of
     // 32 x 16 (two waves a SIMD from one block, for grids of one block a CU)
-    constexpr int NWN = WAVES / 2, BM = 64, BN = 64, NT = BN / 16, WN = BN / NWN, NI = WN / 16;
+    // NT = 3 (6 waves, 2 x 3 of 32 x 16): 64 x 48 tiles, so that a 1536-wide
+    // product is 32 column blocks -- 256 blocks at 512 rows, one per CU
+    constexpr int NWN = WAVES / 2, BM = 64, BN = 16 * NT, WN = BN / NWN, NI = WN / 16;
     constexpr int NB = EPI == EPI_GELU_PAIR ? 2 : 1;  // B operands: (gate, up) or one
-    static_assert(WAVES == 4 || (WAVES == 8 && NB == 1), "8 waves: one B operand");
+    static_assert((WAVES == 4 && NT == 4) || (WAVES == 8 && NT == 4 && NB == 1) ||
+                      (WAVES == 6 && NT == 3 && EPI == EPI_PLAIN),
+                  "4 or 8 waves of a 64-wide tile, or 6 waves of a 48-wide plain one");
     // vector-memory loads a wave issues per group: A and B (and B2) parts
     // with 4 waves, one of A or B with 8
     constexpr int LOADS = WAVES == 4 ? 1 + NB : 1;
@@ -692,7 +698,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
     };
     struct alignas(16) Scales {  // 8 groups
         float x[2][BM][4];          // [group / 4][row][group % 4]
-        uint16_t s[2][NT][8][16];   // [0]: [tile][group][row]; [1]: padding
+        uint16_t s[2][4][8][16];    // [0]: [tile][group][row]; [1]: padding (1 KB each)
     };
     // One __shared__ object per stage: the compiler then tells a read of one
     // stage from the DMA writes still landing in the others (with one array
@@ -731,6 +737,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
     const int unit = lane ^ ((lane >> 4) << 2);
     const size_t b_at = (size_t)min(nb0 + part, n_blocks - 1) * groups * 1024 + unit * 16;
     const int8_t *b_src = w + b_at, *b2_src = NB == 2 ? ep.w2 + b_at : nullptr;
+    // 6 waves: the third B tile is wave 0's second load
+    const int8_t *b_third = WAVES == 6 ? w + (size_t)min(nb0 + 2, n_blocks - 1) * groups * 1024 + unit * 16 : nullptr;
     const char *c_src;  // scales: 16 bytes a lane, advancing 8 groups per chunk
     size_t c_step;
     if (wave < 2) {
@@ -742,21 +750,26 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
         c_src = (const char *)(scales + (size_t)min(nb0 + (lane >> 4), n_blocks - 1) * groups * 16 + 8 * l16);
         c_step = 8 * 16 * sizeof(uint16_t);
     }
-    const int c_dst = wave < 2 ? wave * (BM * 16) : 2 * BM * 16 + min(wave - 2, 1) * (NT * 8 * 16 * 2);
-    // 8 waves: one source, step and stage offset per wave, chosen once
+    const int c_dst = wave < 2 ? wave * (BM * 16) : 2 * BM * 16 + min(wave - 2, 1) * 1024;
+    // 6 or 8 waves: one source, step and stage offset per wave, chosen once
     const int8_t *dma_src = wave < 4 ? a_src : b_src;
     const int dma_step = wave < 4 ? 64 : 1024;
     const int dma_dst = (wave < 4 ? 0 : (int)offsetof(Stage, b)) + part * 1024;
-    auto issue = [&](int g, Stage &d) __attribute__((always_inline)) {
+    // third: std::true_type in wave 0 of 6 (it also loads the third B
+    // tile), else std::false_type -- chosen once, around the whole loop
+    auto issue = [&](int g, Stage &d, auto third) __attribute__((always_inline)) {
         g = min(g, groups - 1);  // past the end: reload the last group (never read)
-        if (WAVES == 8) {
+        if (WAVES >= 6) {
             __builtin_amdgcn_global_load_lds((const void *)(dma_src + (size_t)g * dma_step),
                                              (void *)((char *)&d + dma_dst), 16, 0, 0);
+            if constexpr (decltype(third)::value)
+                __builtin_amdgcn_global_load_lds((const void *)(b_third + (size_t)g * 1024),
+                                                 (void *)(d.b[0] + 2 * 1024), 16, 0, 0);
             return;
         }
         __builtin_amdgcn_global_load_lds((const void *)(a_src + g * 64), (void *)(d.a + wave * 1024), 16, 0, 0);
         __builtin_amdgcn_global_load_lds((const void *)(b_src + (size_t)g * 1024), (void *)(d.b[0] + wave * 1024), 16, 0, 0);
-        if (NB == 2)
+        if constexpr (NB == 2)
             __builtin_amdgcn_global_load_lds((const void *)(b2_src + (size_t)g * 1024), (void *)(d.b[1] + wave * 1024), 16, 0, 0);
     };
     auto issue_scales = [&](int chunk, Scales &d) __attribute__((always_inline)) {
@@ -851,9 +864,10 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
     // group g - 1 (every wave finished reading it before the barrier), plus
     // the next chunk's scales when g + S - 1 starts one; read group g's
     // operands, fold group g - 1 and issue group g's MFMAs.
-    constexpr int in_flight = (S - 2) * LOADS;  // loads of groups g + 1 .. g + S - 2
     auto step = [&](int g, int j, Stage &fill, const Stage &use, const Scales &sc_use,
-                    Scales &sc_fill, Dots &cur, const Dots &prev) __attribute__((always_inline)) {
+                    Scales &sc_fill, Dots &cur, const Dots &prev, auto third) __attribute__((always_inline)) {
+        // loads of groups g + 1 .. g + S - 2
+        constexpr int in_flight = (S - 2) * (LOADS + (decltype(third)::value ? 1 : 0));
         // the next chunk's scales (issued right after its first group) are
         // also in flight once that group is among g + 1 .. g + S - 2
         if (j + S - 2 >= 8)
@@ -861,7 +875,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
         else
             __builtin_amdgcn_s_waitcnt(waitcnt_vm(in_flight));
         __builtin_amdgcn_s_barrier();
-        issue(g + S - 1, fill);
+        issue(g + S - 1, fill, third);
         if (j == (9 - S) % 8) issue_scales(g / 8 + 1, sc_fill);
         Frags f;
         fetch(use, sc_use, j, f);       // LDS reads in flight ...
@@ -873,6 +887,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
         // before the fold that reads them)
         __builtin_amdgcn_sched_barrier(0);
     };
+    auto run = [&](auto third) __attribute__((always_inline)) {
     Dots d0, d1;  // d1 starts as dots 0, products 0: fmaf(0, 0, acc) = acc
 #pragma unroll
     for (int ob = 0; ob < NB; ob++) {
@@ -882,22 +897,22 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
 #pragma unroll
             for (int mi = 0; mi < 2; mi++) d1.d[ob][mi][ni] = magic;
     }
-    issue(0, st0);
+    issue(0, st0, third);
     issue_scales(0, sc0);
 #pragma unroll
-    for (int i = 1; i < S - 1; i++) issue(i, stage(i));
+    for (int i = 1; i < S - 1; i++) issue(i, stage(i), third);
     // 16 groups per pass so that every stage and scale buffer is a fixed
     // object (group g in stage g % S; chunk c = g / 8 in sc0 for even c, sc1
     // for odd c)
     auto eight = [&](int g, Scales &sc_use, Scales &sc_next) __attribute__((always_inline)) {
-        step(g + 0, 0, stage((S - 1) % S), stage(0 % S), sc_use, sc_next, d0, d1);
-        step(g + 1, 1, stage((S + 0) % S), stage(1 % S), sc_use, sc_next, d1, d0);
-        step(g + 2, 2, stage((S + 1) % S), stage(2 % S), sc_use, sc_next, d0, d1);
-        step(g + 3, 3, stage((S + 2) % S), stage(3 % S), sc_use, sc_next, d1, d0);
-        step(g + 4, 4, stage((S + 3) % S), stage(4 % S), sc_use, sc_next, d0, d1);
-        step(g + 5, 5, stage((S + 4) % S), stage(5 % S), sc_use, sc_next, d1, d0);
-        step(g + 6, 6, stage((S + 5) % S), stage(6 % S), sc_use, sc_next, d0, d1);
-        step(g + 7, 7, stage((S + 6) % S), stage(7 % S), sc_use, sc_next, d1, d0);
+        step(g + 0, 0, stage((S - 1) % S), stage(0 % S), sc_use, sc_next, d0, d1, third);
+        step(g + 1, 1, stage((S + 0) % S), stage(1 % S), sc_use, sc_next, d1, d0, third);
+        step(g + 2, 2, stage((S + 1) % S), stage(2 % S), sc_use, sc_next, d0, d1, third);
+        step(g + 3, 3, stage((S + 2) % S), stage(3 % S), sc_use, sc_next, d1, d0, third);
+        step(g + 4, 4, stage((S + 3) % S), stage(4 % S), sc_use, sc_next, d0, d1, third);
+        step(g + 5, 5, stage((S + 4) % S), stage(5 % S), sc_use, sc_next, d1, d0, third);
+        step(g + 6, 6, stage((S + 5) % S), stage(6 % S), sc_use, sc_next, d0, d1, third);
+        step(g + 7, 7, stage((S + 6) % S), stage(7 % S), sc_use, sc_next, d1, d0, third);
     };
     int g = 0;
     for (; g + 16 <= groups; g += 16) {
@@ -906,6 +921,11 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
     }
     if (g < groups) eight(g, sc0, sc1);  // uniform: groups % 16 == 8
     fold(d1);  // the last group (groups % 8 == 0: it went to d1)
+    };
+    if (WAVES == 6 && wave == 0)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
     __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): no DMA outlives the block
     if (EPI == EPI_PLAIN) {
 #pragma unroll
@@ -1165,10 +1185,15 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
     const int blocks = n_out / 16, groups = k / 64;
     if (rows > 8) {
         const unsigned mb = (unsigned)((rows + 63) / 64);
-        const dim3 grid((unsigned)((blocks + 3) / 4), mb);
+        const dim3 grid((unsigned)((blocks + 3) / 4), mb), grid48((unsigned)(blocks / 3), mb);
         GemmEpilogue ep{};
         ep.cols[0] = (int)grid.x;
-        if (groups % 8 == 0 && small_grid(grid.x * grid.y))
+        if (groups % 8 == 0 && blocks % 3 == 0 && grid.x * grid.y < 256 && grid48.x * grid48.y <= 256) {
+            // 48-wide tiles fill more of the 256 CUs (N = 1536 at 512 rows: 256 blocks, not 192)
+            ep.cols[0] = (int)grid48.x;
+            hipLaunchKernelGGL((k_gemm_dma<EPI_PLAIN, 6, 3>), grid48, dim3(384), 0, s, out, out_stride, xq,
+                               xs, w, ws, rows, n_out, k, ep);
+        } else if (groups % 8 == 0 && small_grid(grid.x * grid.y))
             hipLaunchKernelGGL((k_gemm_dma<EPI_PLAIN, 8>), grid, dim3(512), 0, s, out,
                                out_stride, xq, xs, w, ws, rows, n_out, k, ep);
         else if (groups % 8 == 0)
