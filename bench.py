@@ -247,6 +247,25 @@ def gemv_sweep(pkg, lib, torch) -> dict:
     }
 
 
+def decode_probe(pkg, lib, np, context: int = 16384, steps: int = 32) -> None:
+    """Fill `context` positions in 512-token chunks, then `steps` decode steps
+    (forward + logits each), as the decode figure of model_benchmarks."""
+    rng = np.random.default_rng(3)
+    out = np.empty(pkg.VOCAB, np.float32)
+    tokens = rng.integers(0, pkg.VOCAB, context).astype(np.int32)
+    for pos in range(0, context, 512):
+        chunk = tokens[pos:pos + 512]
+        pkg.check(lib.g4_forward(chunk.ctypes.data, chunk.size, pos))
+    pkg.check(lib.g4_logits(0, out.ctypes.data))  # (waits for the fill)
+    time.sleep(0.5)  # an idle gap that separates the decode steps in a trace
+    token = np.array([2], np.int32)
+    s = time.perf_counter()
+    for i in range(steps):
+        pkg.check(lib.g4_forward(token.ctypes.data, 1, context + i))
+        pkg.check(lib.g4_logits(0, out.ctypes.data))
+    log(f"decode @{context}: {steps / (time.perf_counter() - s):.1f} tok/s")
+
+
 def model_benchmarks(pkg, lib, np, steps: int, warmup: int, prefill_only: bool = False) -> dict:
     rng = np.random.default_rng(3)
     out = np.empty(pkg.VOCAB, np.float32)
@@ -361,9 +380,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--order", choices=["reference", "parallel"], default="reference")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--probe", choices=["gemm", "gemv", "copy", "prefill"],
+    ap.add_argument("--probe", choices=["gemm", "gemv", "copy", "prefill", "decode"],
                     help="only launch one kernel 20 times (for rocprofv3 --pmc runs), or run "
-                         "3 + 10 prefill-512 steps of the model (prefill); no JSON")
+                         "3 + 10 prefill-512 steps of the model (prefill), or fill 16384 "
+                         "positions and run 32 decode steps (decode); no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -380,12 +400,16 @@ def main() -> int:
     pkg = __graft_entry__.load_package()
     lib = pkg.lib()
     lib.g4_set_order(pkg.ORDER_REFERENCE if args.order == "reference" else pkg.ORDER_PARALLEL)
-    if args.probe == "prefill":
-        # the headline step alone, for a kernel trace of one 512-token prefill
+    if args.probe in ("prefill", "decode"):
+        # one step kind alone, for kernel traces: the headline 512-token
+        # prefill, or decode steps at 16384 positions of context
         image = pkg.Image.synthetic(seed=MODEL_SEED)
         pkg.check(lib.g4_init(image.records, 0))
         try:
-            model_benchmarks(pkg, lib, np, 10, 3, prefill_only=True)
+            if args.probe == "prefill":
+                model_benchmarks(pkg, lib, np, 10, 3, prefill_only=True)
+            else:
+                decode_probe(pkg, lib, np)
         finally:
             lib.g4_shutdown()
         return 0
