@@ -72,12 +72,13 @@ def random_weight(torch, n: int, k: int, gen):
     return w, s.to(torch.float16)
 
 
-def graph_timed(torch, fn, count: int, replays: int) -> float:
+def graph_timed(torch, fn, count: int, replays: int, warmup: int = 20) -> float:
     """Average milliseconds per launch: `count` launches (fn(0) .. fn(count-1),
-    each on torch's current stream) captured once as a HIP graph, then the
-    graph replayed `replays` times between HIP events on the replay stream.
-    The host's launch rate drops out; what remains is each kernel's duration
-    plus the device's gap between dependent kernels."""
+    each on torch's current stream) captured once as a HIP graph, replayed
+    `warmup` times untimed (clocks and caches reach their steady state), then
+    `replays` times between HIP events on the replay stream.  The host's launch
+    rate drops out; what remains is each kernel's duration plus the device's
+    gap between dependent kernels."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -88,7 +89,8 @@ def graph_timed(torch, fn, count: int, replays: int) -> float:
     with torch.cuda.graph(graph):
         for i in range(count):
             fn(i)
-    graph.replay()
+    for _ in range(warmup):
+        graph.replay()
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
