@@ -1199,8 +1199,9 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
         else if (groups % 8 == 0)
             hipLaunchKernelGGL((k_gemm_dma<EPI_PLAIN, 4>), grid, dim3(256), 0, s, out, out_stride, xq,
                                xs, w, ws, rows, n_out, k, ep);
-        else
-            hipLaunchKernelGGL((k_gemm<64, 1>), dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
+        else  // K not a multiple of 512 (the per-layer-embedding projection, K = 256):
+              // the register-staged kernel, two groups per barrier
+            hipLaunchKernelGGL((k_gemm<64, 2>), dim3((unsigned)((blocks + 3) / 4), mb), dim3(256), 0, s,
                                out, out_stride, xq, xs, w, ws, rows, n_out, k);
         return G4_OK;
     }
