@@ -344,6 +344,10 @@ ATTN_CASES = [
     (512, 4096, 1, 0, 16),
     (512, 4096, 1, 3000, 1),
     (512, 4096, 1, 1000, 64),
+    # token counts that leave a partial last block of 4 (taken first)
+    (256, 1024, 0, 0, 5),
+    (256, 1024, 0, 700, 301),
+    (512, 4096, 1, 37, 13),
     # decode (one to four tokens)
     (512, 4096, 1, 63, 1),        # the row ends on a tile edge
     (512, 4096, 1, 4, 3),         # under one tile, three tokens
