@@ -122,6 +122,36 @@ def test_long_prefill_ring_wrap(pkg, model, image, oracle_lib):
     cpu.close()
 
 
+def test_ragged_prefill_chunks(pkg, model, image, oracle_lib):
+    """Chunks whose row counts are not multiples of the kernels' blocks (77 and
+    then 203 tokens: partial 64-row GEMM tiles, a partial last block of 4
+    tokens in attention, the fused quantization of its output), then greedy
+    steps -- logits and tokens follow the oracle."""
+    cpu = oracle_lib.Model(image)
+    tokens = rng(73).integers(0, pkg.VOCAB, 280).astype(np.int32)
+    pos = 0
+    for size in (77, 203):
+        chunk = tokens[pos:pos + size]
+        gpu_forward(pkg, model, chunk, pos)
+        cpu.forward(chunk, pos)
+        for r in (0, size // 2, size - 1):
+            err = float(np.abs(gpu_logits(pkg, model, r) - cpu.logits(r)).max())
+            assert err <= TOL, (pos, r, err)
+        pos += size
+    row = 202
+    for step in range(3):
+        c_lg = cpu.logits(row)
+        g_lg = gpu_logits(pkg, model, row)
+        assert float(np.abs(g_lg - c_lg).max()) <= TOL, step
+        tok = int(np.argmax(c_lg))
+        assert int(np.argmax(g_lg)) == tok, step
+        gpu_forward(pkg, model, [tok], pos)
+        cpu.forward(np.array([tok], np.int32), pos)
+        pos += 1
+        row = 0
+    cpu.close()
+
+
 def test_global_ring_grows(pkg, model, image, oracle_lib):
     """A 4096-token prefill, then decode steps past position 4096: the global
     layers' rings start at 4096 positions and grow (keys and values copied,
