@@ -184,6 +184,42 @@ def test_global_ring_grows(pkg, model, image, oracle_lib):
     cpu.close()
 
 
+@pytest.mark.timeout(900)
+def test_decode_at_16k_context(pkg, model, image, oracle_lib):
+    """The decode benchmark's depth (gemma4.c:636-643 after a 16384-token
+    prefill): 16384 random ids in 512-token chunks on both sides, then 8
+    greedy decode steps at positions 16384.. (the global rings grow to 32768
+    on the first one; the captured decode graph runs the long-row score,
+    softmax and P.V kernels over 16K+ keys).  Logits within 1e-3 on every
+    compared row, tokens identical."""
+    cpu = oracle_lib.Model(image)
+    tokens = rng(79).integers(0, pkg.VOCAB, 16384).astype(np.int32)
+    row = prefill(pkg, model, cpu, tokens)
+    worst = 0.0
+    for r in (0, row):
+        err = float(np.abs(gpu_logits(pkg, model, r) - cpu.logits(r)).max())
+        assert err <= TOL, (r, err)
+        worst = max(worst, err)
+    pos = len(tokens)
+    for step in range(8):
+        c_lg = cpu.logits(row)
+        g_lg = gpu_logits(pkg, model, row)
+        err = float(np.abs(g_lg - c_lg).max())
+        assert err <= TOL, (step, err)
+        worst = max(worst, err)
+        tok = int(np.argmax(c_lg))
+        assert int(np.argmax(g_lg)) == tok, step
+        assert gpu_argmax(pkg, model, row) == tok, step
+        gpu_forward(pkg, model, [tok], pos)
+        cpu.forward(np.array([tok], np.int32), pos)
+        pos += 1
+        row = 0
+    err = float(np.abs(gpu_logits(pkg, model, 0) - cpu.logits(0)).max())
+    assert err <= TOL, err
+    print(f"16384-token fill + 8 greedy steps: tokens identical, max |dlogit| {max(worst, err):.3g}")
+    cpu.close()
+
+
 def test_teacher_forced_dump_2388(pkg, model, image, oracle_lib):
     """The teacher-forced logit dump (gemma4.c:563-573 with dump on): 2388
     random ids in 512-token chunks, every position's 262144 logits

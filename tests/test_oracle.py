@@ -257,6 +257,65 @@ def test_oracle_model_matches_golden(image, oracle_lib):
     m.close()
 
 
+def test_oracle_matches_reference_beyond_the_window(image, oracle_lib):
+    """forward()/logits() of the oracle and of the compiled reference over
+    1100 tokens (the sliding rings wrap at 1024, the window clamp of
+    gemma4.c:448 is active from position 512, global layers attend past 512)
+    and 3 greedy decode steps: every compared logits row identical bit for bit
+    (SHA-256 of all 262144 floats)."""
+    import hashlib
+    if not oracle_lib.ref_available():
+        pytest.skip("reference library not built here")
+    tokens = rng(59).integers(0, 262144, 1100).astype(np.int32)
+    models = [oracle_lib.Model(image), oracle_lib.Model(image, use_ref=True)]
+    digests = [[], []]
+    for i, m in enumerate(models):
+        for pos in range(0, tokens.size, 512):
+            m.forward(tokens[pos:pos + 512], pos)
+        row = (tokens.size - 1) % 512
+        for r in (0, 37, row):
+            digests[i].append(hashlib.sha256(m.logits(r).tobytes()).hexdigest())
+        pos = tokens.size
+        for _ in range(3):
+            lg = m.logits(row)
+            m.forward(np.array([int(np.argmax(lg))], np.int32), pos)
+            pos += 1
+            row = 0
+            digests[i].append(hashlib.sha256(m.logits(0).tobytes()).hexdigest())
+        m.close()
+    assert digests[0] == digests[1]
+
+
+@pytest.mark.parametrize("full,ring,pos", [
+    (0, 1024, 510), (0, 1024, 511), (0, 1024, 512), (0, 1024, 1023), (0, 1024, 1024),
+    (0, 1024, 1535), (0, 1024, 16380), (1, 8192, 700), (1, 8192, 5000)])
+def test_window_and_ring_brute_force(oracle_lib, full, ring, pos):
+    """Attention of one query at `pos` against a brute-force float64
+    restatement of gemma4.c:443-456: sliding layers see exactly the 512
+    positions max(0, pos - 511) .. pos (gemma4.c:448), global layers 0 .. pos,
+    and position p lives in ring row p & (ring - 1).  One key too many or too
+    few moves the output by ~2% of its scale, far above the tolerance."""
+    lib = oracle_lib.oracle()
+    g = rng(pos + ring)
+    hd, heads = 256, 2
+    kc = g.standard_normal((ring, hd)).astype(np.float32)
+    vc = g.standard_normal((ring, hd)).astype(np.float32)
+    # small queries: near-uniform weights, so every key counts (~2% of the
+    # output's scale for one key more or less, or a ring row off by one)
+    q = (g.standard_normal((1, heads, hd)) * 0.02).astype(np.float32)
+    out = np.empty_like(q)
+    lib.orc_attend(out.ctypes.data, q.ctypes.data, kc.ctypes.data, vc.ctypes.data, ring, hd, heads,
+                   full, pos, 1)
+    first = 0 if full else max(0, pos - 511)
+    rows = np.arange(first, pos + 1) & (ring - 1)
+    k64, v64 = kc[rows].astype(np.float64), vc[rows].astype(np.float64)
+    for h in range(heads):
+        s = k64 @ q[0, h].astype(np.float64)
+        p = np.exp(s - s.max())
+        want = (p / p.sum()) @ v64
+        assert np.abs(out[0, h] - want).max() <= 2e-5 * np.abs(want).max(), (h, pos)
+
+
 def test_oracle_thread_count_independent(image, oracle_lib):
     lib = oracle_lib.oracle()
     toks = np.array([5, 6, 7], np.int32)
