@@ -94,6 +94,7 @@ _G4_SIGNATURES = {
     "g4_geglu": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_p, _c_i, _c_f, _c_f]),
     "g4_embedding": (_c_i, [_c_p, _c_p, ctypes.POINTER(Tensor), _c_p, _c_sz, _c_f]),
     "g4_attend": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_sz]),
+    "g4_attend_noalloc": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_sz]),
 }
 
 _IMG_SIGNATURES = {

@@ -171,20 +171,32 @@ void launch_geglu(hipStream_t s, float *gate, const float *up, int rows, int wid
 // Tokens outside [0, table_rows) produce NaN rows instead of reading outside.
 void launch_embedding(hipStream_t s, float *out, const int8_t *table, const uint16_t *scales,
                       int width, int table_rows, const int *tokens, size_t n, float multiplier);
+// A device buffer the caller owns, used by attention in place of the
+// library's growing scratch (the allocation-free entry point): a call that
+// needs more than `bytes` fails with G4_ERR_ARG before it launches anything.
+struct FixedScratch {
+    void *ptr;
+    size_t bytes;
+};
 // gemma4.c:443-456: attention over a ring cache; dispatches on order().
 // pos_dev requires reference order and n == 1.
 // With q8 set, the output is also written quantized (k_quantize's groups).
 int launch_attend(hipStream_t s, float *out, const float *q, const float *key_cache,
                   const float *value_cache, int cache_len, int head_dim, int heads, int full,
                   int start_pos, const int *pos_dev, size_t n, int8_t *q8 = nullptr,
-                  float *qs = nullptr);
+                  float *qs = nullptr, const FixedScratch *fixed = nullptr);
 int launch_attend_parallel(hipStream_t s, float *out, const float *q, const float *key_cache,
                            const float *value_cache, int cache_len, int head_dim, int heads,
-                           int full, int start_pos, size_t n);
+                           int full, int start_pos, size_t n, const FixedScratch *fixed = nullptr);
 int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
                             const float *value_cache, int cache_len, int head_dim, int heads,
                             int full, int start_pos, const int *pos_dev, size_t n,
-                            int8_t *q8 = nullptr, float *qs = nullptr);
+                            int8_t *q8 = nullptr, float *qs = nullptr,
+                            const FixedScratch *fixed = nullptr);
+// Argument checks of g4_attend (shared by its allocation-free variant).
+int check_attend_args(const char *who, float *out, const float *q, const float *key_cache,
+                      const float *value_cache, int cache_len, int head_dim, int heads,
+                      int full_attention, int start_pos, size_t n);
 // Fused tail of the K/V projections (gemma4.c:437-440): rmsnorm+rope of the n
 // new keys and rmsnorm of the new values, written into the rings at
 // (start_pos + t) & (cache_len - 1).

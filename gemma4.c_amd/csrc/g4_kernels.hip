@@ -1640,16 +1640,26 @@ __global__ __launch_bounds__(256) void k_attn_combine(float *__restrict__ out,
 
 int launch_attend_parallel(hipStream_t s, float *out, const float *q, const float *key_cache,
                            const float *value_cache, int cache_len, int head_dim, int heads,
-                           int full, int start_pos, size_t n) {
+                           int full, int start_pos, size_t n, const FixedScratch *fixed) {
     if (!n) return G4_OK;
     const int last_pos = start_pos + (int)n - 1;
     const int max_keys = full ? last_pos + 1 : (last_pos + 1 < G4_WINDOW ? last_pos + 1 : G4_WINDOW);
     const int max_chunks = (max_keys + kAttnChunk - 1) / kAttnChunk;
     const size_t o_floats = n * (size_t)max_chunks * heads * head_dim;
     const size_t ml_floats = n * (size_t)max_chunks * heads * 2;
-    int rc = scratch_reserve(0, (o_floats + ml_floats) * sizeof(float));
-    if (rc) return rc;
-    float *part_o = scratch().attn, *part_ml = part_o + o_floats;
+    const size_t need = (o_floats + ml_floats) * sizeof(float);
+    float *part_o = nullptr;
+    if (fixed) {
+        if (need > fixed->bytes)
+            return set_error(G4_ERR_ARG, "attention needs %zu bytes of scratch, more than the fixed %zu",
+                             need, fixed->bytes);
+        part_o = (float *)fixed->ptr;
+    } else {
+        int rc = scratch_reserve(0, need);
+        if (rc) return rc;
+        part_o = scratch().attn;
+    }
+    float *part_ml = part_o + o_floats;
     dim3 grid1((unsigned)max_chunks, (unsigned)n);
     if (head_dim == 256)
         hipLaunchKernelGGL(k_attn_partial<256>, grid1, dim3(256), 0, s, q, key_cache, value_cache,
@@ -1746,22 +1756,35 @@ extern "C" int g4_embedding(void *stream, float *out, const g4_tensor *table, co
     return G4_OK;
 }
 
-extern "C" int g4_attend(void *stream, float *out, const float *q, const float *key_cache,
-                         const float *value_cache, int cache_len, int head_dim, int heads,
-                         int full_attention, int start_pos, size_t n) {
-    G4_CHECK(out && q && key_cache && value_cache, "g4_attend: null pointer");
-    G4_CHECK(head_dim == 256 || head_dim == 512, "g4_attend: head_dim must be 256 or 512");
-    G4_CHECK(heads >= 1 && heads <= 8, "g4_attend: heads must be 1..8");
-    G4_CHECK(cache_len > 0 && (cache_len & (cache_len - 1)) == 0, "g4_attend: cache_len must be a power of two");
-    G4_CHECK(start_pos >= 0, "g4_attend: negative position");
+int g4::check_attend_args(const char *who, float *out, const float *q, const float *key_cache,
+                          const float *value_cache, int cache_len, int head_dim, int heads,
+                          int full_attention, int start_pos, size_t n) {
+    G4_CHECK(out && q && key_cache && value_cache, "%s: null pointer", who);
+    G4_CHECK(head_dim == 256 || head_dim == 512, "%s: head_dim must be 256 or 512", who);
+    // the reference-order kernels take the model's 8 query heads; the parallel
+    // order any count up to 8
+    G4_CHECK(order() == G4_ORDER_REFERENCE ? heads == 8 : heads >= 1 && heads <= 8,
+             "%s: heads must be 8 (1..8 in the parallel order)", who);
+    G4_CHECK(cache_len > 0 && (cache_len & (cache_len - 1)) == 0, "%s: cache_len must be a power of two", who);
+    G4_CHECK(start_pos >= 0, "%s: negative position", who);
+    G4_CHECK(n <= (size_t)G4_MAX_CONTEXT, "%s: %zu tokens exceed the context", who, n);
     // Keys visible to the batch span positions max(0, start_pos - 511) ..
     // start_pos + n - 1 (sliding) or 0 .. start_pos + n - 1 (full); the ring
     // must hold them all.
     const long span = full_attention ? (long)start_pos + (long)n
                                      : (long)(start_pos < G4_WINDOW - 1 ? start_pos : G4_WINDOW - 1) + (long)n;
-    G4_CHECK(span <= cache_len, "g4_attend: %ld visible keys exceed the %d-row ring", span, cache_len);
-    int rc = launch_attend((hipStream_t)stream, out, q, key_cache, value_cache, cache_len, head_dim,
-                           heads, full_attention, start_pos, nullptr, n);
+    G4_CHECK(span <= cache_len, "%s: %ld visible keys exceed the %d-row ring", who, span, cache_len);
+    return G4_OK;
+}
+
+extern "C" int g4_attend(void *stream, float *out, const float *q, const float *key_cache,
+                         const float *value_cache, int cache_len, int head_dim, int heads,
+                         int full_attention, int start_pos, size_t n) {
+    int rc = check_attend_args("g4_attend", out, q, key_cache, value_cache, cache_len, head_dim, heads,
+                               full_attention, start_pos, n);
+    if (rc) return rc;
+    rc = launch_attend((hipStream_t)stream, out, q, key_cache, value_cache, cache_len, head_dim,
+                       heads, full_attention, start_pos, nullptr, n);
     if (rc) return rc;
     G4_HIP(hipGetLastError());
     return G4_OK;

@@ -1451,7 +1451,7 @@ __global__ __launch_bounds__(64) void k_attn_values_decode(float *__restrict__ o
 int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
                             const float *value_cache, int cache_len, int head_dim, int heads,
                             int full, int start_pos, const int *pos_dev, size_t n, int8_t *q8,
-                            float *qs) {
+                            float *qs, const FixedScratch *fixed) {
     if (!n) return G4_OK;
     if (heads != 8) return set_error(G4_ERR_ARG, "reference-order attention needs 8 query heads");
     if (pos_dev && n != 1) return set_error(G4_ERR_ARG, "device-side positions are for one token");
@@ -1462,9 +1462,17 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
                                  : full ? last_pos + 1 : (last_pos + 1 < G4_WINDOW ? last_pos + 1 : G4_WINDOW);
     const size_t stride = ((size_t)max_keys + 63) & ~(size_t)63;
     const size_t score_floats = n * heads * stride;
-    int rc = scratch_reserve(0, score_floats * sizeof(float));
-    if (rc) return rc;
-    float *scores = scratch().attn;
+    float *scores = nullptr;
+    if (fixed) {
+        if (score_floats * sizeof(float) > fixed->bytes)
+            return set_error(G4_ERR_ARG, "attention needs %zu bytes of scratch, more than the fixed %zu",
+                             score_floats * sizeof(float), fixed->bytes);
+        scores = (float *)fixed->ptr;
+    } else {
+        int rc = scratch_reserve(0, score_floats * sizeof(float));
+        if (rc) return rc;
+        scores = scratch().attn;
+    }
     // key blocks spanned by one block of tokens: its first token's window
     // start to its last token (a fixed count with a device-side position:
     // the kernel then strides over the blocks it needs)
@@ -1536,13 +1544,14 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
 
 int launch_attend(hipStream_t s, float *out, const float *q, const float *key_cache,
                   const float *value_cache, int cache_len, int head_dim, int heads, int full,
-                  int start_pos, const int *pos_dev, size_t n, int8_t *q8, float *qs) {
+                  int start_pos, const int *pos_dev, size_t n, int8_t *q8, float *qs,
+                  const FixedScratch *fixed) {
     if (g_order == G4_ORDER_REFERENCE)
         return launch_attend_reference(s, out, q, key_cache, value_cache, cache_len, head_dim,
-                                       heads, full, start_pos, pos_dev, n, q8, qs);
+                                       heads, full, start_pos, pos_dev, n, q8, qs, fixed);
     if (pos_dev) return set_error(G4_ERR_ARG, "device-side positions need reference order");
     const int rc = launch_attend_parallel(s, out, q, key_cache, value_cache, cache_len, head_dim,
-                                          heads, full, start_pos, n);
+                                          heads, full, start_pos, n, fixed);
     if (!rc && q8) launch_quantize(s, q8, qs, out, n * heads * head_dim / 64);
     return rc;
 }

@@ -158,10 +158,30 @@ int g4_sample_logits(void *stream, const float *logits, int vocab, float tempera
 
 /* gemma4.c:443-456: causal attention of n query tokens (heads x head_dim each,
  * row-major) at positions start_pos.. over a ring KV cache of cache_len rows;
- * sliding layers (full_attention = 0) see the last G4_WINDOW positions. */
+ * sliding layers (full_attention = 0) see the last G4_WINDOW positions.
+ * head_dim 256 or 512; heads must be 8 (the model's) in G4_ORDER_REFERENCE,
+ * 1..8 in G4_ORDER_PARALLEL.  Grows a library-owned device scratch buffer
+ * (hipMalloc) when a call needs more than it holds. */
 int g4_attend(void *stream, float *out, const float *q, const float *key_cache,
               const float *value_cache, int cache_len, int head_dim, int heads,
               int full_attention, int start_pos, size_t n);
+
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  g4_attend with the same arguments and results, its
+ * scratch (the score rows, or the split-KV partials in G4_ORDER_PARALLEL)
+ * taken from a fixed array of G4_ATTEND_NOALLOC_SCRATCH_BYTES that the
+ * library holds on every device it runs on until the process ends.  Allocates
+ * nothing.  Returns G4_ERR_ARG, launching nothing, when a call needs more:
+ * reference order needs n * 8 * align64(visible keys) floats (e.g. one token
+ * at the full 131072-token context, or a 512-token chunk whose keys reach
+ * position 2047); parallel order n * ceil(keys / 64) * heads * (head_dim + 2)
+ * floats.  Every call on a device shares that device's array: calls that
+ * overlap in time on one device race. */
+#define G4_ATTEND_NOALLOC_SCRATCH_BYTES (32u << 20)
+int g4_attend_noalloc(void *stream, float *out, const float *q, const float *key_cache,
+                      const float *value_cache, int cache_len, int head_dim, int heads,
+                      int full_attention, int start_pos, size_t n);
 
 #ifdef __cplusplus
 }
