@@ -305,9 +305,14 @@ def model_benchmarks(pkg, lib, np, steps: int, warmup: int, prefill_only: bool =
     log(f"prefill 8192: {res['prefill8192_tok_s']:.0f} tok/s")
 
     # decode at 16384 tokens of context: fill, then 128 steps of forward + logits
+    # at positions 16384.., after one untimed step at 16384 that captures the
+    # decode graph (the first timed step rewrites that position's K/V rows
+    # with the same values)
     t16k = rng.integers(0, pkg.VOCAB, 16384).astype(np.int32)
     prefill(t16k)
     token = np.array([2], np.int32)  # gemma4.c:637 decodes token 2
+    forward(token, 16384)
+    pkg.check(lib.g4_logits(0, out.ctypes.data))
     s = time.perf_counter()
     for i in range(128):
         forward(token, 16384 + i)
@@ -331,47 +336,93 @@ def model_benchmarks(pkg, lib, np, steps: int, warmup: int, prefill_only: bool =
 
 
 def cpu_baseline(pkg, image, np) -> dict:
-    """The oracle (CPU restatement of the same path, bit-identical to the
-    reference) on this host: 512-token prefill + logits, 1 discarded warmup +
-    the mean of 3 (the reference README's protocol), at the host's thread
-    count (OMP_NUM_THREADS when set, else the oracle's default, at most 16)
-    and at 8 threads for comparability with the reference's published setup;
-    then decode at 512 tokens of context (4 steps of forward + logits)."""
+    """gemma4.c's own forward()/logits() on this host's cores, on the same
+    synthetic model: oracle/_ref/libgemma4ref.so, the reference's source built
+    by oracle/Makefile for AVX-512 VNNI hosts (its VNNI matmul path).  Where
+    that library is absent, the oracle (the CPU restatement, equal speed on
+    the same cores) stands in, with kind "port".  Bounded samples of the
+    reference's own measurements (gemma4.c:627-645), about a minute of CPU:
+      - prefill 512 + logits of the last row: 1 discarded warmup + the mean of
+        3 (the reference README's protocol), at the host's thread count (one
+        per physical core, gemma4.c:182-188, or OMP_NUM_THREADS; at most 16)
+        and at 8 threads (the README's published setup);
+      - prefill 8192 in 512-token chunks + logits: one run after the warmups
+        (about 16 s on 16 Zen 5 cores);
+      - decode at 16384 positions of context: forward + logits per step, 1
+        untimed and 4 timed steps, with KV rows 0..16383 filled with N(0,1)
+        values in place of a 16384-token prefill (the step's work does not
+        depend on them; the rows the model writes are RMS-normalized, so of
+        that scale)."""
+    import ctypes
+
     import psutil
 
     from oracle import binding
-    lib = binding.oracle()
-    threads = min(lib.orc_threads(), 16)
-    model = binding.Model(image)
-    tokens = np.random.default_rng(3).integers(0, pkg.VOCAB, 512).astype(np.int32)
+    use_ref = binding.ref_available()
+    lib = binding.ref() if use_ref else binding.oracle()
+    threads = min(lib.ref_thread_count() if use_ref else lib.orc_threads(), 16)
+    gomp = ctypes.CDLL(lib._name)  # omp_set_num_threads from the library's libgomp
 
-    def prefill_rate(n_threads: int) -> float:
-        lib.orc_set_threads(n_threads)
-        model.forward(tokens, 0)
+    def set_threads(n: int) -> None:
+        # the reference reads OMP_NUM_THREADS per call (gemma4.c:187): with it
+        # set, the team size is omp_get_max_threads()
+        os.environ["OMP_NUM_THREADS"] = str(n)
+        gomp.omp_set_num_threads(n)
+        if not use_ref:
+            lib.orc_set_threads(n)
+
+    model = binding.Model(image, use_ref=use_ref)
+    rng = np.random.default_rng(3)
+    t512 = rng.integers(0, pkg.VOCAB, 512).astype(np.int32)
+    t8k = rng.integers(0, pkg.VOCAB, 8192).astype(np.int32)
+    token = np.array([2], np.int32)  # gemma4.c:637
+
+    def timed(fn) -> float:
+        s = time.perf_counter()
+        fn()
+        return time.perf_counter() - s
+
+    def prefill512_rate(n_threads: int) -> float:
+        set_threads(n_threads)
+        model.forward(t512, 0)
         model.logits(511)
-        times = []
-        for _ in range(3):
-            s = time.perf_counter()
-            model.forward(tokens, 0)
-            model.logits(511)
-            times.append(time.perf_counter() - s)
+        times = [timed(lambda: (model.forward(t512, 0), model.logits(511))) for _ in range(3)]
         return 512 / (sum(times) / len(times))
 
-    prefill8 = prefill_rate(8)
-    prefill = prefill_rate(threads)
-    s = time.perf_counter()
-    for i in range(4):
-        model.forward(np.array([2], np.int32), 512 + i)
-        model.logits(0)
-    decode = 4 / (time.perf_counter() - s)
-    model.close()
+    def prefill(tokens) -> None:
+        for pos in range(0, tokens.size, 512):
+            model.forward(tokens[pos:pos + 512], pos)
+        model.logits((tokens.size - 1) % 512)
+
+    old_env = os.environ.get("OMP_NUM_THREADS")
+    decode = None
+    try:
+        prefill8 = prefill512_rate(8)
+        rate = prefill512_rate(threads)
+        prefill8k = 8192 / timed(lambda: prefill(t8k))
+        if use_ref:
+            model.fill_kv_random(16384, seed=5)
+            model.forward(token, 16384)
+            model.logits(0)
+            decode = 4 / timed(lambda: [(model.forward(token, 16384 + i), model.logits(0)) for i in range(4)])
+    finally:
+        model.close()
+        if old_env is None:
+            os.environ.pop("OMP_NUM_THREADS", None)
+        else:
+            os.environ["OMP_NUM_THREADS"] = old_env
     nproc, physical = os.cpu_count(), psutil.cpu_count(logical=False)
-    log(f"cpu oracle ({threads} threads; nproc {nproc}, {physical} physical cores): prefill 512 "
-        f"{prefill:.1f} tok/s ({prefill8:.1f} at 8 threads), decode@512 {decode:.2f} tok/s")
-    return {"value": prefill, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": "512-token prefill + logits of the same synthetic model, 1 discarded warmup + "
-                      f"mean of 3; decode@512 ctx {decode:.2f} tok/s over 4 steps",
-            "prefill512_tok_s_8_threads": prefill8, "decode512_tok_s": decode,
+    kind = "reference" if use_ref else "port"
+    log(f"cpu {kind} ({threads} threads; nproc {nproc}, {physical} physical cores): prefill 512 "
+        f"{rate:.1f} tok/s ({prefill8:.1f} at 8 threads); prefill 8192 {prefill8k:.1f} tok/s; "
+        f"decode@16K {decode} tok/s")
+    return {"value": rate, "unit": "tok/s", "cores": threads, "kind": kind,
+            "sample": "gemma4.c forward()+logits() on the same synthetic model: 512-token prefill + "
+                      "logits, 1 discarded warmup + mean of 3; prefill 8192 in 512-token chunks + logits, "
+                      "1 run; decode at 16384 positions (KV rows filled with N(0,1) in place of the "
+                      "prefill), 1 untimed + 4 timed steps of forward + logits",
+            "prefill512_tok_s_8_threads": prefill8, "prefill8192_tok_s": prefill8k,
+            "decode16k_tok_s": decode,
             "host": {"nproc": nproc, "physical_cores": physical, "threads": threads}}
 
 

@@ -6,7 +6,6 @@
 Products (all in-tree, git-ignored):
   gemma4.c_amd/libg4.so      HIP kernels + C ABI (hipcc, gfx950)
   gemma4.c_amd/libg4img.so   model-image loader / synthetic writer (gcc)
-  gemma4.c_amd/g4run         command-line host (gcc, links both)
 Test infrastructure built alongside:
   oracle/liboracle.so        CPU restatement (make -C oracle)
   oracle/_ref/libgemma4ref.so  the reference's own gemma4.c, when its
@@ -65,16 +64,6 @@ def build_img() -> str:
     return out
 
 
-def build_host() -> str:
-    out = os.path.join(PKG, "g4run")
-    src = os.path.join(PKG, "host", "g4run.c")
-    if not os.path.exists(src):
-        return ""
-    run(["gcc", *C_FLAGS, src, "-o", out, f"-L{PKG}", "-lg4", "-lg4img",
-         "-Wl,-rpath,$ORIGIN", "-lm"])
-    return out
-
-
 def build_oracle(with_ref: bool = True) -> None:
     run(["make", "-s", "-C", ORACLE, "all"])
     if with_ref and os.path.exists(os.path.join(REFERENCE, "gemma4.c")):
@@ -84,7 +73,6 @@ def build_oracle(with_ref: bool = True) -> None:
 def build_all(with_ref: bool = True) -> None:
     build_img()
     build_hip()
-    build_host()
     build_oracle(with_ref)
 
 

@@ -68,6 +68,9 @@ struct Scratch {
 };
 Scratch &scratch();
 int scratch_reserve(size_t dots_bytes, size_t attn_bytes);
+// Frees both buffers (after the device has finished with them); the next
+// reservation allocates afresh and bumps the generation.
+void scratch_release();
 
 // ---- launchers (asynchronous on `stream`; shapes validated by callers) -------
 

@@ -3,10 +3,13 @@
 //
 // Arithmetic contract (parity with gemma4.c):
 //   quantize, the matmul (exact int32 group dots + the group-ordered fp32
-//   fold), rope, geglu, embedding, add_and_scale and the attention scores are
-//   bit-identical to the reference on identical inputs; rmsnorm sums, softmax
-//   and the value sums use a parallel order (rounding differs in the last
-//   bits); expf/tanhf come from the device math library.
+//   fold), rope, geglu, embedding and add_and_scale are bit-identical to the
+//   reference on identical inputs.  The rmsnorm, softmax and attention kernels
+//   here are the parallel summation order (G4_ORDER_PARALLEL: tree sums,
+//   split-KV flash decoding, the device expf), equal to within fp32 rounding;
+//   the default order's kernels, bit-identical to the reference, are in
+//   g4_reference_order.hip.  The final soft cap's tanhf is the device
+//   library's (within an ulp of the host's).
 //   Built with -ffp-contract=off: a*b+c rounds twice unless fmaf() is written.
 #include <float.h>
 #include <math.h>
@@ -45,6 +48,17 @@ int scratch_reserve(size_t dots_bytes, size_t attn_bytes) {
         s.generation++;
     }
     return G4_OK;
+}
+
+void scratch_release() {
+    Scratch &s = g_scratch;
+    if (s.dots || s.attn) (void)hipDeviceSynchronize();
+    if (s.dots) (void)hipFree(s.dots);
+    if (s.attn) (void)hipFree(s.attn);
+    s.dots = nullptr;
+    s.attn = nullptr;
+    s.dots_bytes = s.attn_bytes = 0;
+    s.generation++;
 }
 
 // ---------------------------------------------------------------------------
@@ -473,150 +487,6 @@ __global__ __launch_bounds__(256) void k_gemm(float *__restrict__ out, size_t ou
             gload(st + 2, r);
         }
         __syncthreads();
-    }
-#pragma unroll
-    for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-        for (int ni = 0; ni < NI; ni++) {
-            const int col = wn * WN + ni * 16;
-            if (nb0 + (col >> 4) >= n_blocks) continue;
-            const size_t n = (size_t)nb0 * 16 + col + l16;
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int m = m0 + wm * 32 + mi * 16 + 4 * q + v;
-                if (m < rows) out[(size_t)m * out_stride + n] = acc[mi][ni][v];
-            }
-        }
-}
-
-// Variant with B read straight from global memory: LDS then carries only the
-// activation tiles (and their scales), halving its traffic.  With the k-slots
-// of lane (l%16, l/16) taken as k = 16 (l/16) .. + 15, a lane's B operand is
-// four 4-byte words of the packed tile -- chunks 4 (l/16) .. + 3 of weight row
-// l%16 -- so B needs no reordering; A keeps its contiguous 16-byte reads.
-// B operands and weight scales are prefetched DEPTH groups ahead.
-template <int DEPTH>
-__global__ __launch_bounds__(256) void k_gemm_bg(float *__restrict__ out, size_t out_stride,
-                                                 const int8_t *__restrict__ xq,
-                                                 const float *__restrict__ xs,
-                                                 const int8_t *__restrict__ w,
-                                                 const uint16_t *__restrict__ ws, int rows,
-                                                 int n_out, int k) {
-    constexpr int BM = 64, BN = 64, NT = BN / 16, WN = BN / 2, NI = WN / 16, RS = 80;
-    __shared__ __attribute__((aligned(16))) int8_t s_a[2][BM * RS];
-    __shared__ __attribute__((aligned(16))) float s_xs[2][BM];
-    const int groups = k >> 6;
-    const int m0 = blockIdx.y * BM, nb0 = blockIdx.x * NT, n_blocks = n_out >> 4;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1, q = lane >> 4, l16 = lane & 15;
-    const v4i zero = {0, 0, 0, 0};
-
-    const int a_row = tid >> 2, a_part = tid & 3;
-    const int8_t *a_src = xq + (size_t)min(m0 + a_row, rows - 1) * k + a_part * 16;
-    const float *x_src = xs + (size_t)min(m0 + (tid & (BM - 1)), rows - 1) * groups;
-    // this lane's words of its two B tiles: chunk 4q + i of row l16 at
-    // tile + (4q + i) * 64 + 4 l16; scales at [tile][g][l16]
-    const int *b_src[NI];
-    const uint16_t *w_src[NI];
-#pragma unroll
-    for (int ni = 0; ni < NI; ni++) {
-        const int t = min(nb0 + wn * (WN / 16) + ni, n_blocks - 1);
-        b_src[ni] = reinterpret_cast<const int *>(w + (size_t)t * groups * 1024) + q * 64 + l16;
-        w_src[ni] = ws + (size_t)t * groups * 16 + l16;
-    }
-    struct BStage {
-        v4i b[NI];
-        uint16_t w[NI];
-    };
-    auto bload = [&](int g, BStage &r) {
-        g = min(g, groups - 1);
-#pragma unroll
-        for (int ni = 0; ni < NI; ni++) {
-            const int *src = b_src[ni] + (size_t)g * 256;
-#pragma unroll
-            for (int i = 0; i < 4; i++) r.b[ni][i] = src[i * 16];
-            r.w[ni] = w_src[ni][g * 16];
-        }
-    };
-    struct AStage {
-        v4i a;
-        float x;
-    };
-    auto aload = [&](int g, AStage &r) {
-        g = min(g, groups - 1);
-        r.a = *reinterpret_cast<const v4i *>(a_src + g * 64);
-        r.x = x_src[g];
-    };
-    auto astore = [&](int buf, const AStage &r) {
-        *reinterpret_cast<v4i *>(s_a[buf] + a_row * RS + a_part * 16) = r.a;
-        if (tid < BM) s_xs[buf][tid] = r.x;
-    };
-
-    float acc[2][NI][4];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < NI; j++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) acc[i][j][v] = 0.0f;
-
-    auto compute = [&](int buf, const BStage &bs) {
-        v4i a[2];
-        float4 xv[2];
-#pragma unroll
-        for (int mi = 0; mi < 2; mi++) {
-            const int r = wm * 32 + mi * 16;
-            a[mi] = *reinterpret_cast<const v4i *>(s_a[buf] + (r + l16) * RS + q * 16);
-            xv[mi] = *reinterpret_cast<const float4 *>(&s_xs[buf][r + 4 * q]);
-        }
-#pragma unroll
-        for (int ni = 0; ni < NI; ni++) {
-            const float wsf = half_bits_to_float(bs.w[ni]);
-#pragma unroll
-            for (int mi = 0; mi < 2; mi++) {
-                const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], bs.b[ni], zero, 0, 0, 0);
-                acc[mi][ni][0] = fmaf((float)d[0], wsf * xv[mi].x, acc[mi][ni][0]);
-                acc[mi][ni][1] = fmaf((float)d[1], wsf * xv[mi].y, acc[mi][ni][1]);
-                acc[mi][ni][2] = fmaf((float)d[2], wsf * xv[mi].z, acc[mi][ni][2]);
-                acc[mi][ni][3] = fmaf((float)d[3], wsf * xv[mi].w, acc[mi][ni][3]);
-            }
-        }
-    };
-
-    // A: double-buffered LDS, next group in registers; B: DEPTH groups in
-    // registers.  One barrier per group.
-    AStage an;
-    BStage bring[DEPTH];
-    {
-        AStage a0;
-        aload(0, a0);
-        aload(1, an);
-#pragma unroll
-        for (int s2 = 0; s2 < DEPTH; s2++) bload(s2, bring[s2]);
-        astore(0, a0);
-    }
-    __syncthreads();
-    int g = 0;
-    for (; g + DEPTH <= groups; g += DEPTH) {
-#pragma unroll
-        for (int s2 = 0; s2 < DEPTH; s2++) {
-            const int gg = g + s2, buf = gg & 1;
-            compute(buf, bring[s2]);
-            bload(gg + DEPTH, bring[s2]);
-            astore(buf ^ 1, an);
-            aload(gg + 2, an);
-            __syncthreads();
-        }
-    }
-#pragma unroll
-    for (int s2 = 0; s2 < DEPTH; s2++) {
-        if (g + s2 < groups) {  // uniform
-            const int gg = g + s2, buf = gg & 1;
-            compute(buf, bring[s2]);
-            astore(buf ^ 1, an);
-            aload(gg + 2, an);
-            __syncthreads();
-        }
     }
 #pragma unroll
     for (int mi = 0; mi < 2; mi++)

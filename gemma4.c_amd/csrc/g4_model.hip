@@ -120,6 +120,7 @@ static void free_all(Context &c) {
     if (c.pos_pinned) (void)hipHostFree(c.pos_pinned);
     if (c.decode_graph) (void)hipGraphExecDestroy(c.decode_graph);
     if (c.stream) (void)hipStreamDestroy(c.stream);
+    scratch_release();  // the model's reservation (and anything per-op calls grew)
     c = Context();
 }
 
@@ -537,12 +538,16 @@ static int capture_decode(Context &c) {
 // double (to G4_MAX_CONTEXT at most), keys and values copied to the new
 // buffer, the new rows zeroed: a short context does not pay for 131072
 // positions of fp32 keys and values per ring (gemma4.c:164-165 allocates
-// them all).  Runs between forward passes, outside any graph capture.
+// them all).  A ring grows once it would hold less than one more batch past
+// the pass, so a prefill leaves room for the decode steps that follow (they
+// do not stop to grow it).  Runs between forward passes, outside any graph
+// capture.
 static int ensure_kv(Context &c, int last_pos) {
+    const int need = last_pos + G4_BATCH < G4_MAX_CONTEXT ? last_pos + G4_BATCH : G4_MAX_CONTEXT - 1;
     for (int l = 0; l < 15; l++) {
-        if (!c.cache[l] || c.cache_dim[l] != 512 || last_pos < c.cache_len[l]) continue;
+        if (!c.cache[l] || c.cache_dim[l] != 512 || need < c.cache_len[l]) continue;
         int len = c.cache_len[l];
-        while (len <= last_pos && len < G4_MAX_CONTEXT) len *= 2;
+        while (len <= need && len < G4_MAX_CONTEXT) len *= 2;
         const size_t hd = (size_t)c.cache_dim[l], old_len = (size_t)c.cache_len[l];
         float *grown = nullptr;
         G4_HIP(hipMalloc(&grown, 2 * (size_t)len * hd * sizeof(float)));

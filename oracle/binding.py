@@ -209,6 +209,25 @@ class Model:
         p = self._lg(self.model, self.state, row)
         return np.ctypeslib.as_array(p, shape=(VOCAB,)).copy()
 
+    def fill_kv_random(self, positions: int, seed: int) -> None:
+        """Fill rows 0 .. positions - 1 of the three global KV caches and every
+        row of the twelve sliding rings with N(0,1) values: a stand-in for a
+        long prefill where only the timing of later steps matters (the cache
+        rows the model writes are RMS-normalized, so of that scale).  The
+        compiled reference's own state layout (gemma4.c:157-167)."""
+        assert self.is_ref and 0 < positions <= 131072
+        rng = np.random.default_rng(seed)
+        full = self.lib.ref_off_full()
+        ring = 131072 * 512
+        for owner in range(3):
+            for part in range(2):  # keys, then values
+                at = full + (owner * 2 * ring + part * ring) * 4
+                view = np.frombuffer(self._state_buf, np.float32, positions * 512, at)
+                view[:] = rng.standard_normal(positions * 512, dtype=np.float32)
+        sliding = self.lib.ref_off_sliding()
+        count = 12 * 2 * 1024 * 256
+        np.frombuffer(self._state_buf, np.float32, count, sliding)[:] = rng.standard_normal(count, dtype=np.float32)
+
     def residual(self, rows: int) -> np.ndarray:
         if self.is_ref:
             off = self.lib.ref_off_residual()

@@ -283,8 +283,20 @@ static void matmul_body(float *out, const int8_t *xq, const float *xs, const orc
  * ((l0..7 + l8..15) -> 4 -> (s0 + s2) + (s1 + s3)). */
 static float score_one(const float *q, const float *key, int head_dim) {
     float lane[16] = {0};
+#if defined(__AVX2__) && defined(__FMA__)
+    /* the 16 lanes in two registers (lanes 0-7, 8-15), so the chains stay in
+     * registers; each lane's fma chain is the scalar one */
+    __m256 lo = _mm256_setzero_ps(), hi = _mm256_setzero_ps();
+    for (int j = 0; j < head_dim; j += 16) {
+        lo = _mm256_fmadd_ps(_mm256_loadu_ps(q + j), _mm256_loadu_ps(key + j), lo);
+        hi = _mm256_fmadd_ps(_mm256_loadu_ps(q + j + 8), _mm256_loadu_ps(key + j + 8), hi);
+    }
+    _mm256_storeu_ps(lane, lo);
+    _mm256_storeu_ps(lane + 8, hi);
+#else
     for (int j = 0; j < head_dim; j += 16)
         for (int l = 0; l < 16; l++) lane[l] = fmaf(q[j + l], key[j + l], lane[l]);
+#endif
     float s8[8], s4[4];
     for (int l = 0; l < 8; l++) s8[l] = lane[l] + lane[l + 8];
     for (int l = 0; l < 4; l++) s4[l] = s8[l] + s8[l + 4];
@@ -314,6 +326,20 @@ static void softmax_serial(float *v, int n) {
 /* gemma4.c:296-307: per output channel, an fma chain over keys in order. */
 static void value_sum_serial(float *out, const float *p, const float *vc, int first, int n,
                              int mask, int head_dim) {
+#if defined(__AVX2__) && defined(__FMA__)
+    /* 64 channels at a time, their chains held in eight registers (kept in
+     * memory, the chains are store-forwarding bound: ~5x slower) */
+    for (int j = 0; j < head_dim; j += 64) {
+        __m256 acc[8];
+        for (int r = 0; r < 8; r++) acc[r] = _mm256_setzero_ps();
+        for (int i = 0; i < n; i++) {
+            const float *v = vc + (size_t)((first + i) & mask) * head_dim + j;
+            const __m256 pi = _mm256_broadcast_ss(p + i);
+            for (int r = 0; r < 8; r++) acc[r] = _mm256_fmadd_ps(pi, _mm256_loadu_ps(v + 8 * r), acc[r]);
+        }
+        for (int r = 0; r < 8; r++) _mm256_storeu_ps(out + j + 8 * r, acc[r]);
+    }
+#else
     for (int j = 0; j < head_dim; j += 64) {
         float acc[64] = {0};
         for (int i = 0; i < n; i++) {
@@ -322,6 +348,7 @@ static void value_sum_serial(float *out, const float *p, const float *vc, int fi
         }
         memcpy(out + j, acc, sizeof(acc));
     }
+#endif
 }
 
 /* gemma4.c:310-331: table GELU with linear interpolation, times up. */

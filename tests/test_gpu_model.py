@@ -153,12 +153,13 @@ def test_ragged_prefill_chunks(pkg, model, image, oracle_lib):
 
 
 def test_global_ring_grows(pkg, model, image, oracle_lib):
-    """A 4096-token prefill, then decode steps past position 4096: the global
-    layers' rings start at 4096 positions and grow (keys and values copied,
+    """A 3584-token prefill, then decode steps from position 3584: the global
+    layers' rings start at 4096 positions and grow once a pass would leave
+    less than one batch of room (here inside decode: keys and values copied,
     the captured decode graph taken again) -- logits and greedy tokens still
     follow the oracle."""
     cpu = oracle_lib.Model(image)
-    tokens = rng(71).integers(0, pkg.VOCAB, 4096).astype(np.int32)
+    tokens = rng(71).integers(0, pkg.VOCAB, 3584).astype(np.int32)
     row = prefill(pkg, model, cpu, tokens)
     pos = len(tokens)
     for step in range(4):
@@ -188,9 +189,9 @@ def test_global_ring_grows(pkg, model, image, oracle_lib):
 def test_decode_at_16k_context(pkg, model, image, oracle_lib):
     """The decode benchmark's depth (gemma4.c:636-643 after a 16384-token
     prefill): 16384 random ids in 512-token chunks on both sides, then 8
-    greedy decode steps at positions 16384.. (the global rings grow to 32768
-    on the first one; the captured decode graph runs the long-row score,
-    softmax and P.V kernels over 16K+ keys).  Logits within 1e-3 on every
+    greedy decode steps at positions 16384.. (the global rings grew to 32768
+    in the last prefill chunk; the captured decode graph runs the long-row
+    score, softmax and P.V kernels over 16K+ keys).  Logits within 1e-3 on every
     compared row, tokens identical."""
     cpu = oracle_lib.Model(image)
     tokens = rng(79).integers(0, pkg.VOCAB, 16384).astype(np.int32)
