@@ -493,11 +493,42 @@ __device__ __forceinline__ float exact_sum_events(const float (&t)[J], uint32_t 
     return s;
 }
 
-// The sum of squares of a row of 1536 held one float4 per thread of a
-// 384-thread block (thread T: elements 4 T .. 4 T + 3), in index order.
-__device__ __forceinline__ float row_sum_squares_block(float4 x, EsumShared &sh) {
-    const float t[4] = {x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w};
-    return exact_sum_events<6, 4, false>(t, 0u, 0.0f, sh);
+// A hidden row of 1536 held by a block of 4 waves, lane-major: thread T
+// holds elements 6 T .. 6 T + 5 (three 8-byte loads), the layout the
+// exact-sum engine takes (thread T's J terms are terms J T .. J T + J - 1).
+// Of the block shapes that split 1536 (waves x terms a thread: 1 x 24, 2 x
+// 12, 3 x 8, 4 x 6, 6 x 4, 8 x 3, 12 x 2), 4 x 6 took the least time for a
+// fused row tail, alone (decode) and 512 rows at once (prefill): fewer terms
+// a thread shorten each wave's serial loops, more waves lengthen the block's
+// barriers.
+constexpr int kRowWaves = 4, kRowJ = 1536 / (64 * kRowWaves);
+__device__ __forceinline__ void load_row6(const float *row, float (&v)[kRowJ]) {
+    const float2 *p = reinterpret_cast<const float2 *>(row) + 3 * threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const float2 f = p[i];
+        v[2 * i] = f.x, v[2 * i + 1] = f.y;
+    }
+}
+__device__ __forceinline__ void store_row6(float *row, const float (&v)[kRowJ]) {
+    float2 *p = reinterpret_cast<float2 *>(row) + 3 * threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 3; i++) p[i] = make_float2(v[2 * i], v[2 * i + 1]);
+}
+// The reference's sequential sum of squares (gemma4.c:366-368) of such a row:
+// each square rounded on its own, then the in-order fp32 chain through the
+// engine.  Every thread of the block calls it and gets the sum.
+__device__ __forceinline__ float row6_sum_squares(const float (&x)[kRowJ], EsumShared &sh) {
+    float t[kRowJ];
+#pragma unroll
+    for (int j = 0; j < kRowJ; j++) t[j] = x[j] * x[j];
+    return exact_sum_events<kRowWaves, kRowJ, false>(t, 0u, 0.0f, sh);
+}
+// y = w * (inverse * x) (gemma4.c:371-372).
+__device__ __forceinline__ void row6_scale(float (&y)[kRowJ], const float (&w)[kRowJ], float inverse,
+                                           const float (&x)[kRowJ]) {
+#pragma unroll
+    for (int j = 0; j < kRowJ; j++) y[j] = w[j] * (inverse * x[j]);
 }
 
 // The reference's sequential sum of squares (gemma4.c:366-368) of a row held
@@ -560,26 +591,27 @@ __global__ __launch_bounds__(256) void k_rmsnorm_reference_v(float *out, const f
                                         wv[v].z * (inverse * xv[v].z), wv[v].w * (inverse * xv[v].w));
 }
 
-__device__ __forceinline__ float4 scale_by(float4 w, float inverse, float4 x) {
-    return make_float4(w.x * (inverse * x.x), w.y * (inverse * x.y), w.z * (inverse * x.z),
-                       w.w * (inverse * x.w));
-}
-
-// Rows of 1536 (the hidden width): one row per 384-thread block, one float4
-// per thread, the sum through row_sum_squares_block.
-__global__ __launch_bounds__(384) void k_rmsnorm_1536(float *out, const float *in,
+// Rows of 1536 (the hidden width): one row per block (row6 layout).
+__global__ __launch_bounds__(256) void k_rmsnorm_1536(float *out, const float *in,
                                                       const float *__restrict__ weight, float eps) {
     __shared__ EsumShared sh;
-    const int T = threadIdx.x;
     const size_t row = blockIdx.x;
-    const float4 x = reinterpret_cast<const float4 *>(in + row * 1536)[T];
-    const float4 w = weight ? reinterpret_cast<const float4 *>(weight)[T] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-    const float inverse = 1.0f / sqrtf(row_sum_squares_block(x, sh) / 1536.0f + eps);
-    reinterpret_cast<float4 *>(out + row * 1536)[T] = scale_by(w, inverse, x);
+    float x[kRowJ], w[kRowJ];
+    load_row6(in + row * 1536, x);
+    if (weight) {
+        load_row6(weight, w);
+    } else {
+#pragma unroll
+        for (int j = 0; j < kRowJ; j++) w[j] = 1.0f;
+    }
+    const float inverse = 1.0f / sqrtf(row6_sum_squares(x, sh) / 1536.0f + eps);
+    float y[kRowJ];
+    row6_scale(y, w, inverse, x);
+    store_row6(out + row * 1536, y);
 }
 
-// The row-local tail of a sublayer, fused for hidden rows of 1536 (one row
-// per 384-thread block, one float4 per thread), reference order throughout:
+// The row-local tail of a sublayer, fused for hidden rows of 1536, reference
+// order throughout, one row per block (row6 layout):
 //   a = NORM_IN ? rmsnorm(h, w_in) : h                 (gemma4.c:360-373)
 //   if ADD:  residual = (residual + a) * scale         (gemma4.c:375-378)
 //   b = NORM_OUT ? rmsnorm(residual, w_out) : residual
@@ -587,44 +619,60 @@ __global__ __launch_bounds__(384) void k_rmsnorm_1536(float *out, const float *i
 //   if y:     y = b
 // It replaces, e.g., rmsnorm + add_and_scale + rmsnorm + quantize between two
 // matmuls by one launch.  In-place use (y == h or y == residual) is allowed:
-// each thread reads only the elements it writes.
+// each thread reads only the elements it writes.  The quantization groups (64
+// values) do not align with the threads' 6, so b goes through an LDS row and
+// comes back in k_quantize's layout: 16 lanes per group, four values a lane.
 template <bool NORM_IN, bool ADD, bool NORM_OUT, bool QUANT>
-__global__ __launch_bounds__(384) void k_row_tail(const float *h, const float *__restrict__ w_in,
+__global__ __launch_bounds__(256) void k_row_tail(const float *h, const float *__restrict__ w_in,
                                                   float *residual, float scale,
                                                   const float *__restrict__ w_out, float *y,
                                                   int8_t *__restrict__ q8, float *__restrict__ qs,
                                                   float eps) {
     constexpr int W = 1536;
     __shared__ EsumShared sh;
-    const int T = threadIdx.x, lane = T & 63;
+    __shared__ __attribute__((aligned(16))) float s_b[QUANT ? W : 4];
+    const int T = threadIdx.x;
     const size_t row = blockIdx.x;
-    float4 r = reinterpret_cast<const float4 *>(residual + row * W)[T];
-    float4 wi, wo;
-    // weights first: their loads overlap the sums instead of following them
-    if (NORM_IN) wi = reinterpret_cast<const float4 *>(w_in)[T];
-    if (NORM_OUT) wo = reinterpret_cast<const float4 *>(w_out)[T];
+    float r[kRowJ], wi[kRowJ], wo[kRowJ], a[kRowJ];
+    // every load first: the weights' and the residual's arrive during the sums
+    load_row6(residual + row * W, r);
+    if (ADD) load_row6(h + row * W, a);
+    if (NORM_IN) load_row6(w_in, wi);
+    if (NORM_OUT) load_row6(w_out, wo);
     if (ADD) {
-        float4 a = reinterpret_cast<const float4 *>(h + row * W)[T];
-        if (NORM_IN) a = scale_by(wi, 1.0f / sqrtf(row_sum_squares_block(a, sh) / (float)W + eps), a);
-        r = make_float4((r.x + a.x) * scale, (r.y + a.y) * scale, (r.z + a.z) * scale, (r.w + a.w) * scale);
-        reinterpret_cast<float4 *>(residual + row * W)[T] = r;
-    }
-    if (NORM_OUT) r = scale_by(wo, 1.0f / sqrtf(row_sum_squares_block(r, sh) / (float)W + eps), r);
-    if (y) reinterpret_cast<float4 *>(y + row * W)[T] = r;
-    if (QUANT) {
-        // group T / 16 is the 16 lanes of one DPP row: absmax across them
-        float m = fmaxf(fmaxf(fabsf(r.x), fabsf(r.y)), fmaxf(fabsf(r.z), fabsf(r.w)));
+        if (NORM_IN) {
+            const float inverse = 1.0f / sqrtf(row6_sum_squares(a, sh) / (float)W + eps);
+            row6_scale(a, wi, inverse, a);
+        }
 #pragma unroll
-        for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
-        const float gscale = m / 127.0f;
-        const float inverse = gscale > 0.0f ? 1.0f / gscale : 0.0f;
-        char4 out;
-        out.x = (signed char)(int)rintf(r.x * inverse);
-        out.y = (signed char)(int)rintf(r.y * inverse);
-        out.z = (signed char)(int)rintf(r.z * inverse);
-        out.w = (signed char)(int)rintf(r.w * inverse);
-        reinterpret_cast<char4 *>(q8 + row * W)[T] = out;
-        if ((lane & 15) == 0) qs[row * (W / 64) + T / 16] = gscale;
+        for (int j = 0; j < kRowJ; j++) r[j] = (r[j] + a[j]) * scale;
+        store_row6(residual + row * W, r);
+    }
+    if (NORM_OUT) {
+        const float inverse = 1.0f / sqrtf(row6_sum_squares(r, sh) / (float)W + eps);
+        row6_scale(r, wo, inverse, r);
+    }
+    if (y) store_row6(y + row * W, r);
+    if (QUANT) {
+#pragma unroll
+        for (int i = 0; i < 3; i++) reinterpret_cast<float2 *>(s_b)[3 * T + i] = make_float2(r[2 * i], r[2 * i + 1]);
+        __syncthreads();
+        const int lane = T & 63;
+        for (int i = T; i < W / 4; i += 256) {  // group i / 16: the 16 lanes of one DPP row
+            const float4 x = reinterpret_cast<const float4 *>(s_b)[i];
+            float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+            const float gscale = m / 127.0f;
+            const float inverse = gscale > 0.0f ? 1.0f / gscale : 0.0f;
+            char4 out;
+            out.x = (signed char)(int)rintf(x.x * inverse);
+            out.y = (signed char)(int)rintf(x.y * inverse);
+            out.z = (signed char)(int)rintf(x.z * inverse);
+            out.w = (signed char)(int)rintf(x.w * inverse);
+            reinterpret_cast<char4 *>(q8 + row * W)[i] = out;
+            if ((lane & 15) == 0) qs[row * (W / 64) + i / 16] = gscale;
+        }
     }
 }
 
@@ -632,7 +680,7 @@ void launch_row_tail(hipStream_t s, const float *h, const float *w_in, float *re
                      const float *w_out, float *y, int8_t *q8, float *qs, float eps, size_t rows,
                      int norm_in, int add, int norm_out, int quant) {
     if (!rows) return;
-    const dim3 grid((unsigned)rows), block(384);
+    const dim3 grid((unsigned)rows), block(64 * kRowWaves);
 #define G4_TAIL(A, B, C, D)                                                                    \
     if (norm_in == A && add == B && norm_out == C && quant == D) {                             \
         hipLaunchKernelGGL((k_row_tail<A, B, C, D>), grid, block, 0, s, h, w_in, residual, scale, \
@@ -684,7 +732,7 @@ void launch_rmsnorm_reference(hipStream_t s, float *out, const float *in, const 
     const bool aligned = ((uintptr_t)in % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
                          ((uintptr_t)weight % 16 == 0);
     if (aligned && width == 1536)
-        hipLaunchKernelGGL(k_rmsnorm_1536, dim3((unsigned)rows), dim3(384), 0, s, out, in, weight, eps);
+        hipLaunchKernelGGL(k_rmsnorm_1536, dim3((unsigned)rows), dim3(64 * kRowWaves), 0, s, out, in, weight, eps);
     else if (aligned && width == 512)
         hipLaunchKernelGGL(k_rmsnorm_reference_v<2>, grid, block, 0, s, out, in, weight, eps, rows);
     else if (aligned && width == 256)
