@@ -54,6 +54,35 @@ __device__ __forceinline__ float gelu_table_lookup(float x, const float *table, 
     return x <= lower ? t0 : (x >= upper || x != x) ? x : inside;
 }
 
+// The exact int32 group dots of one packed 1 KB weight tile (16 rows x 64
+// columns, byte (chunk c, row r, j) at c*64 + r*4 + j) against M activation
+// rows.  Lane l holds the 16-byte unit l (chunk l/4, rows 4(l%4)..+3) and
+// x4[m], row m's activation dword for chunk l/4.  Four v_dot4_i32_i8 give the
+// lane's partial dots; a transposing butterfly over the 16 lanes that share
+// l%4 leaves the dot of row 4(l%4) + 2 b2 + b3 (b2, b3 = bits 2, 3 of l) in
+// lanes 0..15.
+template <int M>
+__device__ __forceinline__ void gemv_group_dots(const uint4 t, const int (&x4)[M], int b2, int b3,
+                                                int (&d)[M]) {
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        const int p0 = __builtin_amdgcn_sdot4((int)t.x, x4[m], 0, false);
+        const int p1 = __builtin_amdgcn_sdot4((int)t.y, x4[m], 0, false);
+        const int p2 = __builtin_amdgcn_sdot4((int)t.z, x4[m], 0, false);
+        const int p3 = __builtin_amdgcn_sdot4((int)t.w, x4[m], 0, false);
+        int k0 = b2 ? p2 : p0, k1 = b2 ? p3 : p1;
+        const int s0 = b2 ? p0 : p2, s1 = b2 ? p1 : p3;
+        k0 += __shfl_xor(s0, 4);
+        k1 += __shfl_xor(s1, 4);
+        int kk = b3 ? k1 : k0;
+        const int ss = b3 ? k0 : k1;
+        kk += __shfl_xor(ss, 8);
+        kk += __shfl_xor(kk, 16);
+        kk += __shfl_xor(kk, 32);
+        d[m] = kk;
+    }
+}
+
 // ---- scratch owned by the library ------------------------------------------
 
 // Device scratch for split-K matmul dot products and attention partials or
@@ -110,8 +139,8 @@ void launch_row_tail(hipStream_t s, const float *h, const float *w_in, float *re
 void launch_rope(hipStream_t s, const float *cosines, const float *sines, int pairs, float *v,
                  int heads, int head_dim, int start_pos, const int *pos_dev, size_t n);
 // gemma4.c:310-331
-// One token's fused products (k_gemv_fused): up to three matrices on one
-// input, GELU epilogues that can also write the next product's quantized input.
+// One token's products (k_gemv_tail): up to three matrices on one input,
+// GELU epilogues that also write the next product's quantized input.
 struct GemvMat {
     const int8_t *w;
     const uint16_t *ws;
@@ -121,18 +150,30 @@ struct GemvMat {
 struct GemvJob {
     GemvMat m[3];
     int count;
-    const int8_t *xq;  // quantized input and its group scales
-    const float *xs;
     const float *mul;  // EPI_GELU_MUL
     const float *gelu_table;
     int gelu_size;
     float gelu_lower, gelu_upper;
-    int8_t *q_out;  // GELU epilogues: the output quantized (or null)
+    int8_t *q_out;  // GELU epilogues: the output, quantized
     float *qs_out;
     int k;
 };
 enum { EPI_PLAIN = 0, EPI_GELU_PAIR = 1, EPI_GELU_MUL = 2 };
-int launch_gemv_fused(hipStream_t s, const GemvJob &job, int epi);
+// The row tail that feeds a decode product (k_row_tail's arithmetic for one
+// 1536-wide row), run inside the product's launch (k_gemv_tail).
+struct RowTailJob {
+    const float *h;        // the sublayer's output (tails that add)
+    const float *w_in;     // its norm weight
+    const float *res_in;   // the residual before the add (read by every block)
+    float *res_out;        // after it (written by block 0; must differ from res_in)
+    float scale;           // residual = (residual + norm(h)) * scale
+    const float *w_out;    // the norm of the updated residual (tails 1, 3)
+    float eps;
+};
+// tail 1: norm h, add, norm, quantize; 2: norm h, add, quantize the residual;
+// 3: norm the residual, quantize.  K must be 1536.  epi/W pairs with a kernel:
+// EPI_PLAIN with tails 1, 3; EPI_GELU_PAIR with 1; EPI_GELU_MUL with 2.
+int launch_gemv_tail(hipStream_t s, const GemvJob &job, int epi, const RowTailJob &tj, int tail);
 
 // Prefill products with a GELU epilogue (k_gemm_dma<EPI_GELU_*>): the output
 // is written quantized only (q_out [rows][n_out], qs_out [rows][n_out / 64]).

@@ -135,28 +135,6 @@ void launch_quantize(hipStream_t s, int8_t *q, float *scales, const float *x, si
 // dots and k_gemv_fold (the next launch on the stream) folds all groups in
 // order -- the kernel boundary orders the two, no device-scope fences needed.
 
-template <int M>
-__device__ __forceinline__ void gemv_group_dots(const uint4 t, const int (&x4)[M], int b2, int b3,
-                                                int (&d)[M]) {
-#pragma unroll
-    for (int m = 0; m < M; m++) {
-        const int p0 = __builtin_amdgcn_sdot4((int)t.x, x4[m], 0, false);
-        const int p1 = __builtin_amdgcn_sdot4((int)t.y, x4[m], 0, false);
-        const int p2 = __builtin_amdgcn_sdot4((int)t.z, x4[m], 0, false);
-        const int p3 = __builtin_amdgcn_sdot4((int)t.w, x4[m], 0, false);
-        int k0 = b2 ? p2 : p0, k1 = b2 ? p3 : p1;
-        const int s0 = b2 ? p0 : p2, s1 = b2 ? p1 : p3;
-        k0 += __shfl_xor(s0, 4);
-        k1 += __shfl_xor(s1, 4);
-        int kk = b3 ? k1 : k0;
-        const int ss = b3 ? k0 : k1;
-        kk += __shfl_xor(ss, 8);
-        kk += __shfl_xor(kk, 16);
-        kk += __shfl_xor(kk, 32);
-        d[m] = kk;
-    }
-}
-
 template <int M, int U>
 __global__ __launch_bounds__(64) void k_gemv(float *__restrict__ out, size_t out_stride,
                                              const int8_t *__restrict__ xq,
@@ -868,133 +846,6 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
         }
 }
 
-
-// ---------------------------------------------------------------------------
-// One token's products, fused with what surrounds them in the decode step.
-// The block layout is k_gemv_split's: S 16-row strips per block (of each of
-// NM matrices), W waves splitting the groups of each, exact group dots and
-// scale products folded in group order from LDS (the reference's order).
-//   EPI_PLAIN (S = 1): up to three weight matrices that read the same input
-//     in one launch (q, k and v), blocks taken in matrix order.
-//   EPI_GELU_PAIR (S = 4): strips of matrices 0 and 1 (gate, up); writes
-//     gelu(gate) * up (gemma4.c geglu).
-//   EPI_GELU_MUL (S = 4): writes gelu(acc) * mul[n] (the per-layer-embedding
-//     gate).
-// The GELU epilogues cover 64 outputs per block, one quantization group:
-// with job.q_out set they also write it quantized exactly as k_quantize does
-// (absmax / 127, rint(x / scale)), so the next product reads it directly.
-template <int U, int EPI>
-__global__ __launch_bounds__(1024) void k_gemv_fused(GemvJob job) {
-    extern __shared__ __attribute__((aligned(16))) float s_fold[];
-    constexpr int NM = EPI == EPI_GELU_PAIR ? 2 : 1, S = EPI == EPI_PLAIN ? 1 : 4, SM = NM * S;
-    const int k = job.k, groups = k >> 6;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int W = (blockDim.x >> 6) / SM;  // waves per strip of a matrix
-    const int sm = wave / W, wv = wave % W;
-    int mi = EPI == EPI_GELU_PAIR ? sm / S : 0, strip = blockIdx.x * S + sm % S;
-    if (EPI == EPI_PLAIN)
-        while (mi + 1 < job.count && strip >= job.m[mi].strips) strip -= job.m[mi++].strips;
-    const int g_begin = (int)((long)wv * groups / W), g_end = (int)((long)(wv + 1) * groups / W);
-    const GemvMat mat = job.m[mi];
-    float *s_d = s_fold + (size_t)sm * groups * 16;  // [sm][g][r]
-    float *s_c = s_fold + (size_t)(SM + sm) * groups * 16;
-    const int chunk = lane >> 2, b2 = (lane >> 2) & 1, b3 = (lane >> 3) & 1;
-    const int row = 4 * (lane & 3) + 2 * b2 + b3;
-    const uint4 *tiles = reinterpret_cast<const uint4 *>(mat.w + (size_t)strip * 16 * k) + lane;
-    const uint16_t *wscale = mat.ws + (size_t)strip * groups * 16 + row;
-    const int *xrow = reinterpret_cast<const int *>(job.xq) + chunk;
-
-    auto batch = [&](int g0, auto bsize) __attribute__((always_inline)) {
-        constexpr int B = decltype(bsize)::value;
-        uint4 t[B];
-        uint16_t wsr[B];
-        int x4[B];
-        float xsc[B];
-#pragma unroll
-        for (int u = 0; u < B; u++) {
-            t[u] = tiles[(size_t)(g0 + u) * 64];
-            x4[u] = xrow[(g0 + u) * 16];
-            xsc[u] = job.xs[g0 + u];
-            wsr[u] = wscale[(g0 + u) * 16];
-        }
-#pragma unroll
-        for (int u = 0; u < B; u++) {
-            int d[1];
-            const int xx[1] = {x4[u]};
-            gemv_group_dots<1>(t[u], xx, b2, b3, d);
-            if (lane < 16) {
-                s_d[(g0 + u) * 16 + row] = (float)d[0];
-                s_c[(g0 + u) * 16 + row] = half_bits_to_float(wsr[u]) * xsc[u];
-            }
-        }
-    };
-    int g = g_begin;
-    for (; g + U <= g_end; g += U) batch(g, std::integral_constant<int, U>());
-    if constexpr (U >= 16) if (g + 8 <= g_end) { batch(g, std::integral_constant<int, 8>()); g += 8; }
-    if constexpr (U >= 8) if (g + 4 <= g_end) { batch(g, std::integral_constant<int, 4>()); g += 4; }
-    if constexpr (U >= 4) if (g + 2 <= g_end) { batch(g, std::integral_constant<int, 2>()); g += 2; }
-    if (g < g_end) batch(g, std::integral_constant<int, 1>());
-    __syncthreads();
-    const int tid = threadIdx.x;
-    float acc = 0.0f;
-    if (tid < 16 * SM) {  // strip-matrix tid / 16, row tid % 16
-        const float *pd = s_fold + (size_t)(tid >> 4) * groups * 16 + (tid & 15);
-        const float *pc = s_fold + (size_t)(SM + (tid >> 4)) * groups * 16 + (tid & 15);
-        for (int gg = 0; gg < groups; gg++) acc = fmaf(pd[gg * 16], pc[gg * 16], acc);
-    }
-    if (EPI == EPI_PLAIN) {
-        if (tid < 16) mat.out[strip * 16 + tid] = acc;
-        return;
-    }
-    float *s_e = s_fold + (size_t)2 * SM * groups * 16;  // [NM][64] folded outputs
-    if (tid < 16 * SM) s_e[tid] = acc;
-    __syncthreads();
-    if (tid >= 64) return;
-    const int n = blockIdx.x * 64 + tid;
-    const float gl = gelu_table_lookup(s_e[tid], job.gelu_table, job.gelu_size, job.gelu_lower,
-                                       job.gelu_upper);
-    const float v = EPI == EPI_GELU_PAIR ? gl * s_e[64 + tid] : gl * job.mul[n];
-    if (job.m[0].out) job.m[0].out[n] = v;
-    if (job.q_out) {  // k_quantize's arithmetic over the block's 64 outputs
-        float m = fabsf(v);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        const float scale = m / 127.0f;
-        const float inverse = scale > 0.0f ? 1.0f / scale : 0.0f;
-        job.q_out[n] = (int8_t)(int)rintf(v * inverse);
-        if (tid == 0) job.qs_out[blockIdx.x] = scale;
-    }
-}
-
-// The decode products of one token with their fused neighbours; `epi` one of
-// EPI_*.  Waves per strip: enough for ~2048 waves in all, at most 16 per
-// block, and groups spread evenly.
-int launch_gemv_fused(hipStream_t s, const GemvJob &job, int epi) {
-    const int groups = job.k / 64;
-    const int S = epi == EPI_PLAIN ? 1 : 4, nm = epi == EPI_GELU_PAIR ? 2 : 1, sm = S * nm;
-    int strips = 0;
-    for (int i = 0; i < job.count; i++) strips += job.m[i].strips;
-    if (job.k % 64 || job.count < 1 || job.count > 3 || (epi != EPI_PLAIN && job.count != nm) ||
-        (epi != EPI_PLAIN && job.m[0].strips % 4) ||
-        (epi == EPI_GELU_PAIR && job.m[1].strips != job.m[0].strips))
-        return set_error(G4_ERR_ARG, "fused product: bad shape");
-    const int blocks = epi == EPI_PLAIN ? strips : job.m[0].strips / 4;
-    int waves = (2048 + blocks * sm - 1) / (blocks * sm);
-    const int max_waves = groups / 4 > 0 ? groups / 4 : 1;
-    if (waves > max_waves) waves = max_waves;
-    if (waves * sm > 16) waves = 16 / sm;
-    if (waves < 1) waves = 1;
-    const size_t lds = ((size_t)2 * sm * groups * 16 + 128) * sizeof(float);
-    if (lds > 64 * 1024) return set_error(G4_ERR_ARG, "fused product: K too large");
-    const dim3 grid((unsigned)blocks), block((unsigned)(64 * waves * sm));
-    if (epi == EPI_PLAIN)
-        hipLaunchKernelGGL((k_gemv_fused<16, EPI_PLAIN>), grid, block, lds, s, job);
-    else if (epi == EPI_GELU_MUL)
-        hipLaunchKernelGGL((k_gemv_fused<16, EPI_GELU_MUL>), grid, block, lds, s, job);
-    else
-        hipLaunchKernelGGL((k_gemv_fused<16, EPI_GELU_PAIR>), grid, block, lds, s, job);
-    return G4_OK;
-}
 
 // Grids of at most one block a CU (256 CUs) take 8-wave blocks: a lone
 // block's step is bound by latency, which two waves a SIMD partly hide.

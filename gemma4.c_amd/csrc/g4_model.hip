@@ -53,6 +53,7 @@ struct Context {
     int gelu_size = 0;
     float gelu_lower = 0, gelu_upper = 0;
     float *residual = nullptr, *hidden = nullptr, *aux = nullptr, *ple = nullptr;
+    float *residual_alt = nullptr;  // one token: the row tails alternate residual rows
     float *k_new = nullptr, *v_new = nullptr, *logits = nullptr, *logits_all = nullptr;
     int8_t *q8 = nullptr, *q8b = nullptr;  // quantized activations; q8b: written by a
     float *qs = nullptr, *qsb = nullptr;   // product that reads q8 (the GELU epilogues)
@@ -101,6 +102,7 @@ static void free_all(Context &c) {
     if (c.stream) (void)hipStreamSynchronize(c.stream);
     release(c.arena);
     release(c.residual);
+    release(c.residual_alt);
     release(c.hidden);
     release(c.aux);
     release(c.ple);
@@ -283,6 +285,7 @@ static int init(const g4_tensor *records, int device) {
 
     const size_t wide = (size_t)G4_BATCH * 8 * G4_HIDDEN;
     G4_HIP(hipMalloc(&c.residual, (size_t)G4_BATCH * G4_HIDDEN * sizeof(float)));
+    G4_HIP(hipMalloc(&c.residual_alt, (size_t)G4_HIDDEN * sizeof(float)));
     G4_HIP(hipMalloc(&c.hidden, wide * sizeof(float)));
     G4_HIP(hipMalloc(&c.aux, wide * sizeof(float)));
     G4_HIP(hipMalloc(&c.ple, (size_t)G4_BATCH * G4_LAYERS * G4_PLE * sizeof(float)));
@@ -344,18 +347,33 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
     // In reference order the row-local ops between matmuls run fused
     // (launch_row_tail): the same arithmetic in one launch instead of up to four.
     const bool fused = order() == G4_ORDER_REFERENCE;
-    if (fused)  // layer 0's input norm + quantize
+    // One token in reference order: the products fused with their neighbours
+    // (k_gemv_tail): each row tail runs inside the product it feeds (q, k and
+    // v in one launch; gate/up with geglu and the quantize that follows it;
+    // the per-layer-embedding gate likewise, into q8b).  The tails alternate
+    // two residual rows, since every block of a product reads the residual
+    // that block 0 updates: 104 updates a step, so the step ends in
+    // c.residual again.
+    const bool one = fused && n == 1;
+    float *res[2] = {c.residual, c.residual_alt};
+    int p = 0;  // res[p] holds the residual
+    auto tail_job = [&](const float *h, const float *w_in, float scale, const float *w_out) {
+        RowTailJob tj{};
+        tj.h = h;
+        tj.w_in = w_in;
+        tj.res_in = res[p];
+        tj.res_out = h ? res[p ^ 1] : nullptr;
+        tj.scale = scale;
+        tj.w_out = w_out;
+        tj.eps = 1e-6f;
+        if (h) p ^= 1;
+        return tj;
+    };
+    if (fused && !one)  // layer 0's input norm + quantize
         launch_row_tail(s, nullptr, nullptr, c.residual, 1.0f, c.layers[0].input_ln, nullptr, c.q8,
                         c.qs, 1e-6f, n, 0, 0, 1, 1);
-    // One token in reference order: the products fused with their neighbours
-    // (k_gemv_fused): q, k and v in one launch; geglu and the quantize that
-    // follows it in the gate/up and ple_gate epilogues (into q8b: those
-    // products read q8).
-    const bool one = fused && n == 1;
     auto job_on = [&]() {
         GemvJob job{};
-        job.xq = c.q8;
-        job.xs = c.qs;
         job.gelu_table = c.gelu;
         job.gelu_size = c.gelu_size;
         job.gelu_lower = c.gelu_lower;
@@ -384,7 +402,12 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
                 job.m[2] = GemvMat{L.v.data, L.v.scales, c.v_new, hd / 16};
                 job.count = 3;
             }
-            G4_TRY(launch_gemv_fused(s, job, EPI_PLAIN));
+            // the previous layer's last tail + this layer's input norm (layer
+            // 0: the input norm alone)
+            const RowTailJob tj = l == 0 ? tail_job(nullptr, nullptr, 1.0f, L.input_ln)
+                                         : tail_job(c.hidden, c.layers[l - 1].post_ple_ln,
+                                                    c.layers[l - 1].layer_scalar, L.input_ln);
+            G4_TRY(launch_gemv_tail(s, job, EPI_PLAIN, tj, l == 0 ? 3 : 1));
         } else if (L.k.data && n > 8 && G4_HIDDEN % 512 == 0) {
             // q, k and v read the same rows: one launch fills the chip
             const int8_t *w[3] = {L.q.data, L.k.data, L.v.data};
@@ -416,7 +439,9 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
         G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.o, n));
 
         // feed-forward
-        if (fused) {
+        if (one) {
+            // the tail runs inside the gate/up product below
+        } else if (fused) {
             launch_row_tail(s, c.hidden, L.post_attn_ln, c.residual, 1.0f, L.pre_ffn_ln, nullptr,
                             c.q8, c.qs, 1e-6f, n, 1, 1, 1, 1);
         } else {
@@ -452,7 +477,8 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
             job.count = 2;
             job.q_out = c.q8b;
             job.qs_out = c.qsb;
-            G4_TRY(launch_gemv_fused(s, job, EPI_GELU_PAIR));
+            const RowTailJob tj = tail_job(c.hidden, L.post_attn_ln, 1.0f, L.pre_ffn_ln);
+            G4_TRY(launch_gemv_tail(s, job, EPI_GELU_PAIR, tj, 1));
         } else {
             G4_TRY(matmul(c, c.hidden, L.ffn, L.gate, n));
             G4_TRY(matmul(c, c.aux, L.ffn, L.up, n));
@@ -463,7 +489,9 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
         G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.down, n, one || gemm_fused));
 
         // per-layer embedding
-        if (fused) {
+        if (one) {
+            // the tail runs inside the per-layer-embedding gate below
+        } else if (fused) {
             launch_row_tail(s, c.hidden, L.post_ffn_ln, c.residual, 1.0f, nullptr, nullptr, c.q8,
                             c.qs, 1e-6f, n, 1, 1, 0, 1);
         } else {
@@ -485,7 +513,8 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
             job.mul = c.ple + (size_t)l * G4_PLE;
             job.q_out = c.q8b;
             job.qs_out = c.qsb;
-            G4_TRY(launch_gemv_fused(s, job, EPI_GELU_MUL));
+            const RowTailJob tj = tail_job(c.hidden, L.post_ffn_ln, 1.0f, nullptr);
+            G4_TRY(launch_gemv_tail(s, job, EPI_GELU_MUL, tj, 2));
         } else {
             G4_TRY(matmul(c, c.hidden, G4_PLE, L.ple_gate, n));
             launch_geglu(s, c.hidden, c.ple + (size_t)l * G4_PLE, n, G4_PLE, ple_width, c.gelu,
@@ -493,7 +522,11 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
             launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_PLE / 64);
         }
         G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.ple_proj, n, one || gemm_fused));
-        if (fused) {
+        if (one) {
+            if (l + 1 == G4_LAYERS)  // the last tail, in place (the others run in the next q/k/v)
+                launch_row_tail(s, c.hidden, L.post_ple_ln, res[p], L.layer_scalar, nullptr, nullptr,
+                                nullptr, nullptr, 1e-6f, n, 1, 1, 0, 0);
+        } else if (fused) {
             if (l + 1 < G4_LAYERS)  // + the next layer's input norm and quantize
                 launch_row_tail(s, c.hidden, L.post_ple_ln, c.residual, L.layer_scalar,
                                 c.layers[l + 1].input_ln, nullptr, c.q8, c.qs, 1e-6f, n, 1, 1, 1, 1);
@@ -505,6 +538,7 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
             launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, L.layer_scalar);
         }
     }
+    if (p != 0) return set_error(G4_ERR_STATE, "one-token step ended in the alternate residual row");
     G4_HIP(hipGetLastError());
     return G4_OK;
 }

@@ -694,6 +694,234 @@ void launch_row_tail(hipStream_t s, const float *h, const float *w_in, float *re
 #undef G4_TAIL
 }
 
+// ---------------------------------------------------------------------------
+// One token's products fused with the row tail that feeds them (decode,
+// reference order).  The tail of the previous sublayer -- k_row_tail's
+// arithmetic on a 1536-wide hidden row -- runs at the start of every block,
+// all of the block's waves taking part in the exact sums, and leaves the
+// quantized row in LDS; the blocks compute it from the same inputs with the
+// same code, so every block holds the same bits.  Before the tail, each wave
+// has already issued the loads of all of its weight tiles, so the tail runs
+// while they are in flight and one launch (and its gap) per tail is saved.
+// Block 0 writes the updated residual to res_out; every block reads res_in,
+// so the two must differ (the caller alternates two buffers).
+// The products (one token, K = 1536, 24 groups): a block covers S 16-row
+// strips of each of its NM matrices (S = 1 for EPI_PLAIN: up to three
+// matrices that read the same input, blocks taken in matrix order; S = 4 for
+// the GELU epilogues: 64 outputs per block, one quantization group), W waves
+// per strip-matrix, each taking 24 / W groups; the exact group dots and scale
+// products go through LDS and 16 lanes per strip-matrix fold them in group
+// order (gemma4.c:216-218).  Epilogues:
+//   EPI_PLAIN      out = x W^T
+//   EPI_GELU_PAIR  gelu(gate) * up (gemma4.c:309-331), quantized
+//   EPI_GELU_MUL   gelu(x W^T) * mul (the per-layer-embedding gate), quantized
+// (k_quantize's arithmetic over each block's 64 outputs).
+constexpr int kTailGroups = 1536 / 64;
+
+// J = 24 / NW consecutive elements per thread, thread T holding J T ..
+// J T + J - 1: the lane-major layout of exact_sum_events.
+template <int J>
+__device__ __forceinline__ void load_row_j(const float *row, float (&v)[J]) {
+    if constexpr (J == 4) {
+        const float4 f = reinterpret_cast<const float4 *>(row)[threadIdx.x];
+        v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+    } else if constexpr (J == 2) {
+        const float2 f = reinterpret_cast<const float2 *>(row)[threadIdx.x];
+        v[0] = f.x, v[1] = f.y;
+    } else {
+#pragma unroll
+        for (int j = 0; j < J; j++) v[j] = row[J * threadIdx.x + j];
+    }
+}
+template <int J>
+__device__ __forceinline__ void store_row_j(float *row, const float (&v)[J]) {
+    if constexpr (J == 4) {
+        reinterpret_cast<float4 *>(row)[threadIdx.x] = make_float4(v[0], v[1], v[2], v[3]);
+    } else if constexpr (J == 2) {
+        reinterpret_cast<float2 *>(row)[threadIdx.x] = make_float2(v[0], v[1]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < J; j++) row[J * threadIdx.x + j] = v[j];
+    }
+}
+
+// y = w * (inverse * x), inverse = 1 / sqrt(sum x^2 / 1536 + eps) with the
+// sum in index order (gemma4.c:366-372); all NW waves of the block call it.
+template <int NW, int J>
+__device__ __forceinline__ void tail_rmsnorm(float (&x)[J], const float (&w)[J], float eps,
+                                             EsumShared &sh) {
+    float t[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) t[j] = x[j] * x[j];
+    const float sum = exact_sum_events<NW, J, false>(t, 0u, 0.0f, sh);
+    const float inverse = 1.0f / sqrtf(sum / 1536.0f + eps);
+#pragma unroll
+    for (int j = 0; j < J; j++) x[j] = w[j] * (inverse * x[j]);
+}
+
+// k_row_tail<NORM_IN, ADD, NORM_OUT, QUANT = true> for one row, by the NW
+// waves of the block, into LDS: s_q8 (1536 int8 as 384 dwords) and s_qs (24
+// group scales).  The loads are split from the arithmetic so that a caller
+// can issue them before its own (vector-memory loads complete in order: a
+// tail whose inputs queue behind a wave's weight tiles would wait for all of
+// them).  compute() ends with a block barrier.
+template <int NW, bool NORM_IN, bool ADD, bool NORM_OUT>
+struct RowTail {
+    static constexpr int J = kTailGroups / NW;
+    static_assert(J * NW == kTailGroups, "NW divides 24");
+    float r[J], a[J], wi[J], wo[J];
+    __device__ __forceinline__ void load(const RowTailJob &tj) {
+        load_row_j<J>(tj.res_in, r);
+        if (ADD) load_row_j<J>(tj.h, a);
+        if (NORM_IN) load_row_j<J>(tj.w_in, wi);
+        if (NORM_OUT) load_row_j<J>(tj.w_out, wo);
+    }
+    __device__ __forceinline__ void compute(const RowTailJob &tj, float *s_row, int *s_q8, float *s_qs,
+                                            EsumShared &sh) {
+        if (ADD) {
+            if (NORM_IN) tail_rmsnorm<NW, J>(a, wi, tj.eps, sh);
+#pragma unroll
+            for (int j = 0; j < J; j++) r[j] = (r[j] + a[j]) * tj.scale;
+            if (blockIdx.x == 0) store_row_j<J>(tj.res_out, r);
+        }
+        if (NORM_OUT) tail_rmsnorm<NW, J>(r, wo, tj.eps, sh);
+        store_row_j<J>(s_row, r);
+        __syncthreads();
+        // quantize (gemma4.c:265-279) in k_quantize's layout: 16 lanes per
+        // group of 64, four values a lane; waves past the 384 float4s sit out
+        const int T = threadIdx.x;
+        if (T < 384) {
+            const float4 x = reinterpret_cast<const float4 *>(s_row)[T];
+            float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+            const float gscale = m / 127.0f;
+            const float inverse = gscale > 0.0f ? 1.0f / gscale : 0.0f;
+            char4 q;
+            q.x = (signed char)(int)rintf(x.x * inverse);
+            q.y = (signed char)(int)rintf(x.y * inverse);
+            q.z = (signed char)(int)rintf(x.z * inverse);
+            q.w = (signed char)(int)rintf(x.w * inverse);
+            reinterpret_cast<char4 *>(s_q8)[T] = q;
+            if ((T & 15) == 0) s_qs[T >> 4] = gscale;
+        }
+        __syncthreads();
+    }
+};
+
+template <int EPI, int W, int TAIL>
+__global__ __launch_bounds__(64 * W * (EPI == EPI_PLAIN ? 1 : EPI == EPI_GELU_PAIR ? 8 : 4))
+void k_gemv_tail(GemvJob job, RowTailJob tj) {
+    constexpr int NM = EPI == EPI_GELU_PAIR ? 2 : 1, S = EPI == EPI_PLAIN ? 1 : 4, SM = NM * S;
+    constexpr int NW = W * SM, NG = kTailGroups / W;
+    static_assert(NG * W == kTailGroups, "W divides 24");
+    __shared__ EsumShared sh;
+    __shared__ __attribute__((aligned(16))) float s_row[1536];
+    __shared__ int s_q8[384];
+    __shared__ float s_qs[kTailGroups];
+    __shared__ float s_d[SM][kTailGroups][16], s_c[SM][kTailGroups][16], s_e[NM][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sm = wave / W, wv = wave % W;
+    int mi = EPI == EPI_GELU_PAIR ? sm / S : 0, strip = blockIdx.x * S + sm % S;
+    if (EPI == EPI_PLAIN)
+        while (mi + 1 < job.count && strip >= job.m[mi].strips) strip -= job.m[mi++].strips;
+    const GemvMat mat = job.m[mi];
+    const int g0 = wv * NG;
+    const int chunk = lane >> 2, b2 = (lane >> 2) & 1, b3 = (lane >> 3) & 1;
+    const int row = 4 * (lane & 3) + 2 * b2 + b3;
+    const uint4 *tiles = reinterpret_cast<const uint4 *>(mat.w + (size_t)strip * 16 * 1536) + lane;
+    const uint16_t *wscale = mat.ws + (size_t)strip * kTailGroups * 16 + row;
+    // the tail's inputs first, then the first PRE of this wave's weight tiles,
+    // in flight while the tail runs (more would stall the wave at issue: the
+    // memory pipeline takes only so many requests, and the tail would then
+    // start after the tiles' data instead of beside it); the rest after it
+    constexpr int PRE = NG < 8 ? NG : 8;
+    RowTail<NW, TAIL != 3, TAIL != 3, TAIL != 2> tail;
+    tail.load(tj);
+    __builtin_amdgcn_sched_barrier(0);  // keep the tail's loads ahead of the tiles'
+    uint4 t[NG];
+    uint16_t wsr[NG];
+#pragma unroll
+    for (int u = 0; u < PRE; u++) {
+        t[u] = tiles[(size_t)(g0 + u) * 64];
+        wsr[u] = wscale[(g0 + u) * 16];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    tail.compute(tj, s_row, s_q8, s_qs, sh);
+#pragma unroll
+    for (int u = PRE; u < NG; u++) {
+        t[u] = tiles[(size_t)(g0 + u) * 64];
+        wsr[u] = wscale[(g0 + u) * 16];
+    }
+    // every group's dot first (their butterflies interleave), then the stores
+    int d[NG];
+#pragma unroll
+    for (int u = 0; u < NG; u++) {
+        int dd[1];
+        const int xx[1] = {s_q8[(g0 + u) * 16 + chunk]};
+        gemv_group_dots<1>(t[u], xx, b2, b3, dd);
+        d[u] = dd[0];
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int u = 0; u < NG; u++) {
+            s_d[sm][g0 + u][row] = (float)d[u];
+            s_c[sm][g0 + u][row] = half_bits_to_float(wsr[u]) * s_qs[g0 + u];
+        }
+    }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    float acc = 0.0f;
+    if (tid < 16 * SM) {  // strip-matrix tid / 16, row tid % 16
+        const int m = tid >> 4, r = tid & 15;
+        for (int g = 0; g < kTailGroups; g++) acc = fmaf(s_d[m][g][r], s_c[m][g][r], acc);
+    }
+    if (EPI == EPI_PLAIN) {
+        if (tid < 16) mat.out[strip * 16 + tid] = acc;
+        return;
+    }
+    if (tid < 16 * SM) s_e[tid >> 6][tid & 63] = acc;
+    __syncthreads();
+    if (tid >= 64) return;
+    const int n = blockIdx.x * 64 + tid;
+    const float gl = gelu_table_lookup(s_e[0][tid], job.gelu_table, job.gelu_size, job.gelu_lower,
+                                       job.gelu_upper);
+    const float v = EPI == EPI_GELU_PAIR ? gl * s_e[NM - 1][tid] : gl * job.mul[n];
+    float m = fabsf(v);  // k_quantize's arithmetic over the block's 64 outputs
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float scale = m / 127.0f;
+    const float inverse = scale > 0.0f ? 1.0f / scale : 0.0f;
+    job.q_out[n] = (int8_t)(int)rintf(v * inverse);
+    if (tid == 0) job.qs_out[blockIdx.x] = scale;
+}
+
+int launch_gemv_tail(hipStream_t s, const GemvJob &job, int epi, const RowTailJob &tj, int tail) {
+    int strips = 0;
+    for (int i = 0; i < job.count; i++) strips += job.m[i].strips;
+    if (job.k != 1536 || job.count < 1 || job.count > 3 || (epi != EPI_PLAIN && job.count != (epi == EPI_GELU_PAIR ? 2 : 1)) ||
+        (epi != EPI_PLAIN && (job.m[0].strips % 4 || !job.q_out)) ||
+        (epi == EPI_GELU_PAIR && job.m[1].strips != job.m[0].strips) || tail < 1 || tail > 3 ||
+        (tail != 3 && tj.res_out == tj.res_in))
+        return set_error(G4_ERR_ARG, "fused tail product: bad shape");
+    const unsigned blocks = (unsigned)(epi == EPI_PLAIN ? strips : job.m[0].strips / 4);
+#define G4_GT(E, WW, T)                                                                     \
+    if (epi == E && tail == T) {                                                            \
+        constexpr int SM_ = (E == EPI_PLAIN ? 1 : E == EPI_GELU_PAIR ? 8 : 4);              \
+        hipLaunchKernelGGL((k_gemv_tail<E, WW, T>), dim3(blocks), dim3(64 * WW * SM_), 0, s, job, tj); \
+        return G4_OK;                                                                       \
+    }
+    // q, k and v: 6 waves a strip (4 groups each); the GELU pair: 8 strip-
+    // matrices of one wave (24 groups); the per-layer-embedding gate: 4 strips
+    // of 2 waves (12 groups)
+    G4_GT(EPI_PLAIN, 6, 1)
+    G4_GT(EPI_PLAIN, 6, 3)
+    G4_GT(EPI_GELU_PAIR, 1, 1)
+    G4_GT(EPI_GELU_MUL, 2, 2)
+#undef G4_GT
+    return set_error(G4_ERR_ARG, "fused tail product: no kernel for epilogue %d with tail %d", epi, tail);
+}
+
 // Any other width (per-op entry point): the same order, plainer loads.
 __global__ __launch_bounds__(256) void k_rmsnorm_reference(float *out, const float *in,
                                                            const float *__restrict__ weight,
