@@ -10,6 +10,9 @@ Test infrastructure built alongside:
   oracle/liboracle.so        CPU restatement (make -C oracle)
   oracle/_ref/libgemma4ref.so  the reference's own gemma4.c, when its
                              checkout is present (make -C oracle ref)
+  oracle/_ref/run_g4         the reference's program with
+                             gemma4.c_amd/host/gemma4c.patch, linked to
+                             libg4.so (make -C oracle run_g4)
 """
 
 from __future__ import annotations
@@ -68,6 +71,8 @@ def build_oracle(with_ref: bool = True) -> None:
     run(["make", "-s", "-C", ORACLE, "all"])
     if with_ref and os.path.exists(os.path.join(REFERENCE, "gemma4.c")):
         run(["make", "-s", "-C", ORACLE, "ref", f"REF={REFERENCE}"])
+        # the reference's program patched onto libg4.so (the drop-in check)
+        run(["make", "-s", "-C", ORACLE, "run_g4", f"REF={REFERENCE}"])
 
 
 def build_all(with_ref: bool = True) -> None:
