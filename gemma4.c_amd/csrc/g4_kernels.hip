@@ -8,8 +8,8 @@
 //   here are the parallel summation order (G4_ORDER_PARALLEL: tree sums,
 //   split-KV flash decoding, the device expf), equal to within fp32 rounding;
 //   the default order's kernels, bit-identical to the reference, are in
-//   g4_reference_order.hip.  The final soft cap's tanhf is the device
-//   library's (within an ulp of the host's).
+//   g4_reference_order.hip.  The final soft cap's tanhf restates the host
+//   libm's method (tanhf_libm), bit-identical.
 //   Built with -ffp-contract=off: a*b+c rounds twice unless fmaf() is written.
 #include <float.h>
 #include <math.h>
@@ -1164,9 +1164,98 @@ void launch_kv_finish(hipStream_t s, float *key_cache, float *value_cache, const
                        pos_dev, order() == G4_ORDER_REFERENCE ? 1 : 0);
 }
 
+// The host libm's tanhf, restated: glibc's single-precision tanh
+// (sysdeps/ieee754/flt-32/s_tanhf.c, from Sun's fdlibm) on its expm1f
+// (s_expm1f.c).  Every step is one rounded fp32 operation (this file is built
+// with -ffp-contract=off; division is correctly rounded), so the results are
+// the host's bit for bit: tests/csrc/tanhf_method_check.c runs the same steps
+// against the host libm on every float below 22 in magnitude.
+//   expm1(x) = 2^k (1 + r + r^2/2 ...) - 1, x = k ln2 + r (ln2 in a high part
+//   exact in 24 bits times k, and a low part), with the rational form
+//   r1 = 1 + h (Q1 + h (Q2 + h (Q3 + h (Q4 + h Q5)))), h = r^2 / 2, and the
+//   reconstruction arranged by the size of k.  Arguments here: |x| < 44.
+__device__ __forceinline__ float expm1f_libm(float x) {
+    constexpr uint32_t kQ1 = 0xbd088889u, kQ2 = 0x3ad00d01u, kQ3 = 0xb8a670cdu, kQ4 = 0x36867e54u,
+                       kQ5 = 0xb457edbbu, kLn2Hi = 0x3f317180u, kLn2Lo = 0x3717f7d1u,
+                       kInvLn2 = 0x3fb8aa3bu;
+    const float Q1 = __uint_as_float(kQ1), Q2 = __uint_as_float(kQ2), Q3 = __uint_as_float(kQ3),
+                Q4 = __uint_as_float(kQ4), Q5 = __uint_as_float(kQ5);
+    const float ln2_hi = __uint_as_float(kLn2Hi), ln2_lo = __uint_as_float(kLn2Lo),
+                invln2 = __uint_as_float(kInvLn2);
+    const uint32_t ux = __float_as_uint(x), ax = ux & 0x7fffffffu;
+    const bool negative = ux >> 31;
+    if (negative && ax >= 0x4195b844u) return -1.0f;  // x <= -27 ln2
+    int k;
+    float c = 0.0f;
+    if (ax > 0x3eb17218u) {       // |x| > ln2 / 2
+        float hi, lo;
+        if (ax < 0x3f851592u) {  // |x| < 3 ln2 / 2
+            hi = negative ? x + ln2_hi : x - ln2_hi;
+            lo = negative ? -ln2_lo : ln2_lo;
+            k = negative ? -1 : 1;
+        } else {
+            k = (int)(invln2 * x + (negative ? -0.5f : 0.5f));
+            const float t = (float)k;
+            hi = x - t * ln2_hi;  // exact
+            lo = t * ln2_lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (ax < 0x33000000u) {  // |x| < 2^-25
+        return x;
+    } else {
+        k = 0;
+    }
+    const float hfx = 0.5f * x, hxs = x * hfx;
+    const float r1 = 1.0f + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+    float t = 3.0f - r1 * hfx;
+    float e = hxs * ((r1 - t) / (6.0f - x * t));
+    if (k == 0) return x - (x * e - hxs);
+    e = x * (e - c) - c;
+    e -= hxs;
+    if (k == -1) return 0.5f * (x - e) - 0.5f;
+    if (k == 1) return x < -0.25f ? -2.0f * (e - (x + 0.5f)) : 1.0f + 2.0f * (x - e);
+    float y;
+    if (k <= -2 || k > 56) {
+        y = 1.0f - (e - x);
+        y = __uint_as_float(__float_as_uint(y) + ((uint32_t)k << 23));
+        return y - 1.0f;
+    }
+    if (k < 23) {
+        t = __uint_as_float(0x3f800000u - (0x1000000u >> k));  // 1 - 2^-k
+        y = t - (e - x);
+    } else {
+        t = __uint_as_float((uint32_t)(0x7f - k) << 23);  // 2^-k
+        y = x - (e + t);
+        y += 1.0f;
+    }
+    return __uint_as_float(__float_as_uint(y) + ((uint32_t)k << 23));
+}
+__device__ __forceinline__ float tanhf_libm(float x) {
+    const uint32_t ux = __float_as_uint(x), ax = ux & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (ux >> 31) ? 1.0f / x - 1.0f : 1.0f / x + 1.0f;  // +-1, NaN
+    float z;
+    if (ax < 0x41b00000u) {  // |x| < 22
+        if (ax == 0) return x;
+        if (ax < 0x24000000u) return x * (1.0f + x);  // |x| < 2^-55
+        const float a = __uint_as_float(ax);
+        if (ax >= 0x3f800000u) {  // |x| >= 1
+            const float t = expm1f_libm(2.0f * a);
+            z = 1.0f - 2.0f / (t + 2.0f);
+        } else {
+            const float t = expm1f_libm(-2.0f * a);
+            z = -t / (t + 2.0f);
+        }
+    } else {
+        z = 1.0f;
+    }
+    return (ux >> 31) ? -z : z;
+}
+
+// gemma4.c:518-519: 30 tanh(x / 30), bit-identical to the host's.
 __global__ __launch_bounds__(256) void k_softcap(float *x, size_t n) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) x[i] = 30.0f * tanhf(x[i] / 30.0f);
+    if (i < n) x[i] = 30.0f * tanhf_libm(x[i] / 30.0f);
 }
 
 void launch_softcap(hipStream_t s, float *x, size_t n) {
