@@ -268,6 +268,72 @@ def decode_probe(pkg, lib, np, context: int = 16384, steps: int = 32) -> None:
     log(f"decode @{context}: {steps / (time.perf_counter() - s):.1f} tok/s")
 
 
+def prefill_8192_rate(prefill, rng, pkg, np) -> float:
+    """8192 tokens in 512-token chunks + the last row's logits (gemma4.c:563-573
+    with --bench 8192): 1 warmup + the mean of 3."""
+    t8k = rng.integers(0, pkg.VOCAB, 8192).astype(np.int32)
+    prefill(t8k)
+    times = []
+    for _ in range(3):
+        s = time.perf_counter()
+        prefill(t8k)
+        times.append(time.perf_counter() - s)
+    return 8192 / (sum(times) / len(times))
+
+
+def decode_16k_rate(prefill, forward, logits, rng, pkg, np) -> float:
+    """Decode at 16384 tokens of context (gemma4.c:636-643): fill, then 128 steps
+    of forward + logits at positions 16384.., after one untimed step at 16384
+    that captures the decode graph (the first timed step rewrites that
+    position's K/V rows with the same values)."""
+    t16k = rng.integers(0, pkg.VOCAB, 16384).astype(np.int32)
+    prefill(t16k)
+    token = np.array([2], np.int32)  # gemma4.c:637 decodes token 2
+    forward(token, 16384)
+    logits()
+    s = time.perf_counter()
+    for i in range(128):
+        forward(token, 16384 + i)
+        logits()
+    return 128 / (time.perf_counter() - s)
+
+
+def parallel_order_figures(pkg, lib, np) -> dict:
+    """The other summation order (G4_ORDER_PARALLEL: tree sums, split-KV flash
+    decoding) measured the same way in the same session, and how far it moves
+    the logits: one 512-token prefill's last row in both orders."""
+    rng = np.random.default_rng(5)
+    out = np.empty(pkg.VOCAB, np.float32)
+    rows = {}
+
+    def forward(tokens, pos):
+        pkg.check(lib.g4_forward(tokens.ctypes.data, tokens.size, pos))
+
+    def prefill(tokens):
+        for pos in range(0, tokens.size, 512):
+            forward(tokens[pos:pos + 512], pos)
+        pkg.check(lib.g4_logits((tokens.size - 1) % 512, out.ctypes.data))
+
+    t512 = rng.integers(0, pkg.VOCAB, 512).astype(np.int32)
+    for name, order in (("reference", pkg.ORDER_REFERENCE), ("parallel", pkg.ORDER_PARALLEL)):
+        lib.g4_set_order(order)
+        prefill(t512)
+        rows[name] = out.copy()
+    res = {
+        "max_abs_logit_delta_vs_reference_order": float(np.abs(rows["reference"] - rows["parallel"]).max()),
+        "argmax_agrees": bool(np.argmax(rows["reference"]) == np.argmax(rows["parallel"])),
+    }
+    try:
+        res["prefill8192_tok_s"] = round(prefill_8192_rate(prefill, rng, pkg, np), 1)
+        res["decode16k_tok_s"] = round(decode_16k_rate(prefill, forward,
+                                                       lambda: pkg.check(lib.g4_logits(0, out.ctypes.data)),
+                                                       rng, pkg, np), 2)
+    finally:
+        lib.g4_set_order(pkg.ORDER_REFERENCE)
+    log(f"parallel order: {res}")
+    return res
+
+
 def model_benchmarks(pkg, lib, np, steps: int, warmup: int, prefill_only: bool = False) -> dict:
     rng = np.random.default_rng(3)
     out = np.empty(pkg.VOCAB, np.float32)
@@ -293,31 +359,10 @@ def model_benchmarks(pkg, lib, np, steps: int, warmup: int, prefill_only: bool =
     if prefill_only:
         return res
 
-    # prefill 8192 in 512-token chunks: 1 warmup + mean of 3
-    t8k = rng.integers(0, pkg.VOCAB, 8192).astype(np.int32)
-    prefill(t8k)
-    times = []
-    for _ in range(3):
-        s = time.perf_counter()
-        prefill(t8k)
-        times.append(time.perf_counter() - s)
-    res["prefill8192_tok_s"] = 8192 / (sum(times) / len(times))
+    res["prefill8192_tok_s"] = prefill_8192_rate(prefill, rng, pkg, np)
     log(f"prefill 8192: {res['prefill8192_tok_s']:.0f} tok/s")
-
-    # decode at 16384 tokens of context: fill, then 128 steps of forward + logits
-    # at positions 16384.., after one untimed step at 16384 that captures the
-    # decode graph (the first timed step rewrites that position's K/V rows
-    # with the same values)
-    t16k = rng.integers(0, pkg.VOCAB, 16384).astype(np.int32)
-    prefill(t16k)
-    token = np.array([2], np.int32)  # gemma4.c:637 decodes token 2
-    forward(token, 16384)
-    pkg.check(lib.g4_logits(0, out.ctypes.data))
-    s = time.perf_counter()
-    for i in range(128):
-        forward(token, 16384 + i)
-        pkg.check(lib.g4_logits(0, out.ctypes.data))
-    res["decode16k_tok_s"] = 128 / (time.perf_counter() - s)
+    res["decode16k_tok_s"] = decode_16k_rate(prefill, forward, lambda: pkg.check(lib.g4_logits(0, out.ctypes.data)),
+                                             rng, pkg, np)
     log(f"decode @16K: {res['decode16k_tok_s']:.1f} tok/s")
 
     # teacher-forced logit dump (gemma4.c:563-573 with dump on): 2388 ids in
@@ -487,6 +532,7 @@ def main() -> int:
     log(f"g4_init (upload + KV allocation) {time.perf_counter() - t:.1f} s")
     try:
         res = model_benchmarks(pkg, lib, np, args.steps, args.warmup)
+        parallel = parallel_order_figures(pkg, lib, np) if args.order == "reference" else None
     finally:
         lib.g4_shutdown()
 
@@ -514,6 +560,11 @@ def main() -> int:
         "prefill8192_tok_s": round(res["prefill8192_tok_s"], 1),
         "decode16k_tok_s": round(res["decode16k_tok_s"], 2),
         "dump2388_rows_s": round(res["dump2388_rows_s"], 1),
+        # the same figures in the parallel summation order, which is not
+        # bit-identical: the logits of one 512-token prefill move by the delta
+        "prefill8192_tok_s_parallel": parallel and parallel["prefill8192_tok_s"],
+        "decode16k_tok_s_parallel": parallel and parallel["decode16k_tok_s"],
+        "parallel_order_logit_delta": parallel and round(parallel["max_abs_logit_delta_vs_reference_order"], 4),
         "roofline": {
             "bound": "mfma",
             "kernel": "k_gemm (prefill W8A8 GEMM, X[512x1536] x W[6144x1536])",
