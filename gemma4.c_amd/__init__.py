@@ -36,6 +36,7 @@ RECORDS = 671
 
 FFN_6144 = 1
 UNIT_NORMS = 2
+BF16_VALUES = 4
 
 ORDER_REFERENCE = 0
 ORDER_PARALLEL = 1
@@ -97,8 +98,25 @@ _G4_SIGNATURES = {
     "g4_attend_noalloc": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_sz]),
 }
 
+class ImageItem(ctypes.Structure):
+    """g4img_item (include/g4img.h): one distinct tensor of the image."""
+    _fields_ = [("record", ctypes.c_int), ("kind", ctypes.c_int), ("rows", ctypes.c_int),
+                ("cols", ctypes.c_int), ("global_rope", ctypes.c_int),
+                ("data", ctypes.c_uint64), ("scales", ctypes.c_uint64)]
+
+
+ITEM_QUANT, ITEM_VECTOR, ITEM_SCALAR, ITEM_ROPE_COS, ITEM_ROPE_SIN, ITEM_GELU = range(6)
+DTYPE_F32, DTYPE_BF16, DTYPE_F16 = range(3)
+TOKENIZER_SPAN = 33_429_932
+DATA_START = 33_484_992
+
 _IMG_SIGNATURES = {
     "g4img_size": (_c_sz, [ctypes.c_uint]),
+    "g4img_layout": (_c_i, [ctypes.c_uint, ctypes.POINTER(ImageItem), _c_i]),
+    "g4img_write_header": (_c_i, [_c_p, _c_sz, ctypes.c_uint]),
+    "g4img_pack_matrix": (_c_i, [_c_p, _c_i, _c_i, _c_i, _c_p, _c_p, _c_i]),
+    "g4img_fill_table": (_c_i, [_c_p, _c_sz, ctypes.POINTER(ImageItem), _c_i]),
+    "g4img_draw": (_c_i, [ctypes.c_uint64, ctypes.c_uint, ctypes.POINTER(ImageItem), _c_p, _c_i, _c_i]),
     "g4img_generate": (_c_i, [_c_p, _c_sz, ctypes.c_uint64, ctypes.c_uint, _c_i]),
     "g4img_write_file": (_c_i, [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_uint, _c_i]),
     "g4img_records": (_c_i, [_c_p, _c_sz, ctypes.POINTER(Tensor)]),

@@ -71,10 +71,27 @@ static float f16_to_f32(uint16_t h) {
     return f;
 }
 
+/* Round to bfloat16 (nearest, ties to even), kept as fp32: what a BF16
+ * checkpoint holds for a value (finite inputs). */
+static float round_bf16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    x = (x + 0x7fffu + ((x >> 16) & 1u)) & 0xffff0000u;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
 /* ------------------------------------------------------------------------- */
 /* Layout plan: the exporter's tensor() call order (exporter.py:95-150).       */
 
-enum { K_QUANT, K_VECTOR, K_SCALAR, K_ROPE_COS, K_ROPE_SIN, K_GELU };
+enum {
+    K_QUANT = G4IMG_KIND_QUANT,
+    K_VECTOR = G4IMG_KIND_VECTOR,
+    K_SCALAR = G4IMG_KIND_SCALAR,
+    K_ROPE_COS = G4IMG_KIND_ROPE_COS,
+    K_ROPE_SIN = G4IMG_KIND_ROPE_SIN,
+    K_GELU = G4IMG_KIND_GELU
+};
 
 typedef struct {
     int record;  /* first record that references the item (also the RNG key) */
@@ -269,7 +286,7 @@ static uint16_t quantize_group(const float *v, int8_t *q) {
     return h;
 }
 
-static void fill_quant(uint8_t *base, const item *it, uint64_t seed, int threads) {
+static void fill_quant(uint8_t *base, const item *it, uint64_t seed, unsigned flags, int threads) {
     const size_t cols = (size_t)it->cols, groups = cols / 64, blocks = (size_t)it->rows / 16;
     int8_t *data = (int8_t *)(base + it->data);
     uint16_t *scales = (uint16_t *)(base + it->scales);
@@ -284,6 +301,8 @@ static void fill_quant(uint8_t *base, const item *it, uint64_t seed, int threads
             float v[64];
             int8_t q[64];
             normals64(key_of(seed, it->record, (block * 16 + (size_t)r) * groups + g), 0.02f, v);
+            if (flags & G4IMG_BF16_VALUES)
+                for (int j = 0; j < 64; j++) v[j] = round_bf16(v[j]);
             tile_scales[r] = quantize_group(v, q);
             for (int c = 0; c < 16; c++) memcpy(tile + c * 64 + r * 4, q + c * 4, 4);
         }
@@ -348,7 +367,7 @@ int g4img_generate(void *buf, size_t size, uint64_t seed, unsigned flags, int th
             memset(base + it->data + count * 4, 0, end - (it->data + count * 4));
         }
         switch (it->kind) {
-        case K_QUANT: fill_quant(base, it, seed, threads); break;
+        case K_QUANT: fill_quant(base, it, seed, flags, threads); break;
         case K_ROPE_COS:
         case K_ROPE_SIN: fill_rope(base, it, threads); break;
         case K_GELU: fill_gelu(base, it); break;
@@ -356,11 +375,13 @@ int g4img_generate(void *buf, size_t size, uint64_t seed, unsigned flags, int th
         case K_VECTOR: {
             float *out = (float *)(base + it->data);
             const int scalar = it->kind == K_SCALAR;
-            for (int j = 0; j < it->rows; j++)
+            for (int j = 0; j < it->rows; j++) {
                 out[j] = (flags & G4IMG_UNIT_NORMS)
                              ? 1.0f
                              : uniform(key_of(seed, it->record, (uint64_t)j),
                                        scalar ? 0.9f : 0.75f, scalar ? 1.1f : 1.25f);
+                if (flags & G4IMG_BF16_VALUES) out[j] = round_bf16(out[j]);
+            }
             break;
         }
         }
@@ -384,6 +405,163 @@ int g4img_write_file(const char *path, uint64_t seed, unsigned flags, int thread
     if (msync(map, size, MS_SYNC) != 0 && rc == 0) rc = fail("msync failed", -1);
     munmap(map, size);
     return rc;
+}
+
+/* ------------------------------------------------------------------------- */
+/* Pieces of the image for a checkpoint writer (gemma4.c_amd/export.py): the
+ * layout, the header, the quantize-and-pack step and the tables, so that the
+ * writer fills the same bytes from a checkpoint's weights that the synthetic
+ * generator fills from its seeded ones.                                      */
+
+int g4img_layout(unsigned flags, g4img_item *out, int max_items) {
+    plan *p = malloc(sizeof(plan));
+    if (!p) return fail("out of memory", -1);
+    make_plan(p, flags);
+    const int n = p->count;
+    if (!out || max_items < n) {
+        free(p);
+        return fail("item buffer too small", -1);
+    }
+    for (int i = 0; i < n; i++) {
+        const item *it = &p->items[i];
+        out[i].record = it->record;
+        out[i].kind = it->kind;
+        out[i].rows = it->rows;
+        out[i].cols = it->cols;
+        out[i].global_rope = it->global_rope;
+        out[i].data = it->data;
+        out[i].scales = it->scales;
+    }
+    free(p);
+    return n;
+}
+
+int g4img_write_header(void *buf, size_t size, unsigned flags) {
+    plan *p = malloc(sizeof(plan));
+    if (!p) return fail("out of memory", -1);
+    make_plan(p, flags);
+    if (!buf || size < G4IMG_DATA_START) {
+        free(p);
+        return fail("buffer smaller than the header", -1);
+    }
+    uint8_t *base = buf;
+    memset(base, 0, G4IMG_DATA_START);
+    memcpy(base, "MOG", 4);
+    for (int r = 0; r < G4_RECORDS; r++) {
+        uint8_t *rec = base + G4IMG_RECORDS_OFFSET + (size_t)r * 32;
+        memcpy(rec, &p->rec_data[r], 8);
+        memcpy(rec + 8, &p->rec_scales[r], 8);
+        memcpy(rec + 16, p->rec_shape[r], 16);
+    }
+    free(p);
+    return 0;
+}
+
+static float bf16_to_f32(uint16_t h) {
+    const uint32_t bits = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static float load_value(const uint8_t *src, int dtype, size_t index) {
+    if (dtype == G4IMG_F32) {
+        float f;
+        memcpy(&f, src + index * 4, 4);
+        return f;
+    }
+    uint16_t h;
+    memcpy(&h, src + index * 2, 2);
+    return dtype == G4IMG_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+int g4img_pack_matrix(const void *src, int dtype, int rows, int cols, void *data, void *scales,
+                      int threads) {
+    if (!src || !data || !scales || rows <= 0 || cols <= 0 || rows % 16 || cols % 64 ||
+        (dtype != G4IMG_F32 && dtype != G4IMG_BF16 && dtype != G4IMG_F16))
+        return fail("pack: bad matrix", -1);
+    if (threads <= 0) threads = omp_get_num_procs();
+    const size_t ncols = (size_t)cols, groups = ncols / 64, blocks = (size_t)rows / 16;
+    const uint8_t *in = src;
+    int8_t *out = data;
+    uint16_t *out_scales = scales;
+    int bad = 0;
+#pragma omp parallel for schedule(static) num_threads(threads) reduction(| : bad)
+    for (size_t ti = 0; ti < blocks * groups; ti++) {
+        const size_t block = ti / groups, g = ti % groups;
+        int8_t tile[1024];
+        uint16_t tile_scales[16];
+        for (int r = 0; r < 16; r++) {
+            float v[64];
+            int8_t q[64];
+            const size_t row = block * 16 + (size_t)r;
+            for (int j = 0; j < 64; j++) {
+                v[j] = load_value(in, dtype, row * ncols + g * 64 + (size_t)j);
+                bad |= !(fabsf(v[j]) <= 3.40282347e38f); /* NaN or inf: no scale can hold it */
+            }
+            tile_scales[r] = quantize_group(v, q);
+            for (int c = 0; c < 16; c++) memcpy(tile + c * 64 + r * 4, q + c * 4, 4);
+        }
+        memcpy(out + block * 16 * ncols + g * 1024, tile, sizeof(tile));
+        memcpy(out_scales + (block * groups + g) * 16, tile_scales, sizeof(tile_scales));
+    }
+    return bad ? fail("pack: the matrix holds a NaN or an infinity", -1) : 0;
+}
+
+int g4img_fill_table(void *base, size_t size, const g4img_item *it, int threads) {
+    if (!base || !it || it->data + (size_t)it->rows * (size_t)it->cols * 4 > size)
+        return fail("table: item outside the buffer", -1);
+    if (threads <= 0) threads = omp_get_num_procs();
+    item local = {it->record, it->kind, it->rows, it->cols, it->global_rope, it->data, it->scales};
+    if (it->kind == K_ROPE_COS || it->kind == K_ROPE_SIN)
+        fill_rope(base, &local, threads);
+    else if (it->kind == K_GELU)
+        fill_gelu(base, &local);
+    else
+        return fail("table: not a table item", it->record);
+    return 0;
+}
+
+static void store_value(void *out, int dtype, size_t index, float v) {
+    if (dtype == G4IMG_F32) {
+        memcpy((uint8_t *)out + index * 4, &v, 4);
+    } else {  /* G4IMG_BF16: v is already a bfloat16 value */
+        uint32_t x;
+        memcpy(&x, &v, 4);
+        const uint16_t h = (uint16_t)(x >> 16);
+        memcpy((uint8_t *)out + index * 2, &h, 2);
+    }
+}
+
+int g4img_draw(uint64_t seed, unsigned flags, const g4img_item *it, void *out, int dtype, int threads) {
+    if (!it || !out || (dtype != G4IMG_F32 && dtype != G4IMG_BF16) ||
+        (dtype == G4IMG_BF16 && !(flags & G4IMG_BF16_VALUES)))
+        return fail("draw: bad arguments (BF16 output needs G4IMG_BF16_VALUES)", -1);
+    if (threads <= 0) threads = omp_get_num_procs();
+    if (it->kind == K_QUANT) {
+        const size_t cols = (size_t)it->cols, groups = cols / 64, rows = (size_t)it->rows;
+#pragma omp parallel for schedule(static) num_threads(threads)
+        for (size_t rg = 0; rg < rows * groups; rg++) {
+            float v[64];
+            normals64(key_of(seed, it->record, rg), 0.02f, v);
+            const size_t at = (rg / groups) * cols + (rg % groups) * 64;
+            for (int j = 0; j < 64; j++)
+                store_value(out, dtype, at + (size_t)j, (flags & G4IMG_BF16_VALUES) ? round_bf16(v[j]) : v[j]);
+        }
+        return 0;
+    }
+    if (it->kind == K_VECTOR || it->kind == K_SCALAR) {
+        const int scalar = it->kind == K_SCALAR;
+        for (int j = 0; j < it->rows; j++) {
+            float v = (flags & G4IMG_UNIT_NORMS) ? 1.0f
+                                                 : uniform(key_of(seed, it->record, (uint64_t)j),
+                                                           scalar ? 0.9f : 0.75f, scalar ? 1.1f : 1.25f);
+            if (flags & G4IMG_BF16_VALUES) v = round_bf16(v);
+            store_value(out, dtype, (size_t)j, v);
+        }
+        return 0;
+    }
+    return fail("draw: a table item has no draws", it->record);
 }
 
 /* ------------------------------------------------------------------------- */

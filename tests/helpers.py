@@ -152,3 +152,57 @@ def sample_cases(vocab: int = 4096):
     temps = [0.0, 0.3, 1.0, 2.5]
     states = [42, 0x9E3779B97F4A7C15]
     return rows, temps, states
+
+
+# ---------------------------------------------------------------------------
+# A fabricated Gemma 4 E2B checkpoint (for the checkpoint writer's tests and
+# the golden tokenizer block)
+
+def fabricated_config() -> dict:
+    """config.json with the E2B text configuration the exporter accepts
+    (exporter.py:153-175)."""
+    return {
+        "model_type": "gemma4",
+        "text_config": {
+            "hidden_size": 1536, "vocab_size": 262144, "num_hidden_layers": 35, "num_kv_shared_layers": 20,
+            "num_key_value_heads": 1, "head_dim": 256, "global_head_dim": 512, "intermediate_size": 6144,
+            "use_double_wide_mlp": True, "max_position_embeddings": 131072, "sliding_window": 512,
+            "hidden_size_per_layer_input": 256, "rms_norm_eps": 1e-6, "final_logit_softcapping": 30.0,
+            "layer_types": (["sliding_attention"] * 4 + ["full_attention"]) * 7,
+            "rope_parameters": {"sliding_attention": {"rope_theta": 10000.0},
+                                "full_attention": {"rope_theta": 1000000.0, "partial_rotary_factor": 0.25}},
+        },
+    }
+
+
+def fabricated_tokenizer() -> dict:
+    """tokenizer.json of 262144 ids that the exporter's rules accept: ids 0-5
+    and 105/106 special (turn markers included), the byte tokens <0x00>..<0xFF>
+    at 238-493, the 26 letters (direct lookups), their 676 two-letter
+    concatenations built by merges, a few multi-byte and word-marker tokens,
+    and filler words elsewhere."""
+    specials = {0: "<pad>", 1: "<eos>", 2: "<bos>", 3: "<unk>", 4: "<mask>", 5: "[multimodal]",
+                105: "<|turn>", 106: "<turn|>"}
+    vocab = {}
+    for b in range(256):
+        vocab[f"<0x{b:02X}>"] = 238 + b
+    letters = [chr(ord("a") + i) for i in range(26)]
+    for i, ch in enumerate(letters):
+        vocab[ch] = 494 + i
+    merges = []
+    n = 520
+    for a in letters:
+        for b in letters:
+            vocab[a + b] = n
+            merges.append(f"{a} {b}")
+            n += 1
+    extra = ["▁", "▁the", "é", "ß", "€", "日本", "▁▁", "\t", "x▁y"]
+    for t in extra:
+        vocab[t] = n
+        n += 1
+    used = set(vocab.values()) | set(specials)
+    for i in range(262144):
+        if i not in used:
+            vocab[f"▁w{i}"] = i
+    added = [{"id": i, "content": t, "special": True} for i, t in sorted(specials.items())]
+    return {"model": {"vocab": vocab, "merges": merges}, "added_tokens": added}
