@@ -135,6 +135,59 @@ void launch_quantize(hipStream_t s, int8_t *q, float *scales, const float *x, si
 // dots and k_gemv_fold (the next launch on the stream) folds all groups in
 // order -- the kernel boundary orders the two, no device-scope fences needed.
 
+// One wave's share of a one-strip GEMV: groups [g_begin, g_end) of the strip
+// at `tiles` / `wscale`, for M activation rows; `emit(g, d[M], wsr, xsv[M])`
+// gets each group's exact dots (in lanes 0..15, row `row`), raw weight scale
+// and -- with XS -- the rows' activation scales (else zeros).  Loads for a
+// batch of up to U groups are issued before any is consumed: full batches of
+// U, then one batch of the n < U left (n is the same in the whole wave; the
+// launchers pick U to suit a wave's share); slots past n reload the batch's
+// last group -- unconditional loads, so no wait at branch joins -- and are
+// not consumed.
+template <int M, int U, bool XS, typename Emit>
+__device__ __forceinline__ void gemv_strip_groups(const uint4 *tiles, const uint16_t *wscale, const int *xrow,
+                                                  const float *xs, int k, int rows, int g_begin, int g_end,
+                                                  int b2, int b3, Emit emit) {
+    const int groups = k >> 6;
+    auto batch = [&](int g0, int n) __attribute__((always_inline)) {
+        uint4 t[U];
+        int x4[U][M];
+        uint16_t wsr[U];
+        float xsv[U][M];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int gu = g0 + min(u, n - 1);
+            t[u] = tiles[(size_t)gu * 64];
+#pragma unroll
+            for (int m = 0; m < M; m++) {  // rows past `rows` reread the last row (unused)
+                const int mm = min(m, rows - 1);
+                x4[u][m] = xrow[((size_t)mm * k + (size_t)gu * 64) >> 2];
+                xsv[u][m] = XS ? xs[(size_t)mm * groups + gu] : 0.0f;
+            }
+            wsr[u] = wscale[gu * 16];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (u < n) {
+                int d[M];
+                gemv_group_dots<M>(t[u], x4[u], b2, b3, d);
+                emit(g0 + u, d, wsr[u], xsv[u]);
+            }
+        }
+    };
+    int g = g_begin;
+    for (; g + U <= g_end; g += U) batch(g, U);
+    if (g < g_end) batch(g, g_end - g);
+}
+
+// Batch size for a wave's share of `count` groups: the fewest batches of at
+// most `cap`, each rounded up to a multiple of 4.
+inline int gemv_batch(int count, int cap) {
+    const int batches = (count + cap - 1) / cap;
+    const int u = (count + batches - 1) / batches;
+    return (u + 3) & ~3;
+}
+
 template <int M, int U>
 __global__ __launch_bounds__(64) void k_gemv(float *__restrict__ out, size_t out_stride,
                                              const int8_t *__restrict__ xq,
@@ -152,65 +205,72 @@ __global__ __launch_bounds__(64) void k_gemv(float *__restrict__ out, size_t out
     const uint4 *tiles = reinterpret_cast<const uint4 *>(w + (size_t)block * 16 * k) + lane;
     const uint16_t *wscale = ws + (size_t)block * groups * 16 + row;
     const int *xrow = reinterpret_cast<const int *>(xq) + chunk;
-    const bool fold = splits == 1;
 
-    float acc[M];
+    if (splits == 1) {  // the wave folds as it goes
+        float acc[M];
 #pragma unroll
-    for (int m = 0; m < M; m++) acc[m] = 0.0f;
-
-    auto consume = [&](int gg, const uint4 &t, const int (&x4)[M], uint16_t wsr) {
-        int d[M];
-        gemv_group_dots<M>(t, x4, b2, b3, d);
-        if (fold) {
-            const float wsf = half_bits_to_float(wsr);
+        for (int m = 0; m < M; m++) acc[m] = 0.0f;
+        gemv_strip_groups<M, U, true>(
+            tiles, wscale, xrow, xs, k, rows, g_begin, g_end, b2, b3,
+            [&](int, const int (&d)[M], uint16_t wsr, const float (&xsv)[M]) __attribute__((always_inline)) {
+                const float wsf = half_bits_to_float(wsr);
+#pragma unroll
+                for (int m = 0; m < M; m++) acc[m] = fmaf((float)d[m], wsf * xsv[m], acc[m]);
+            });
+        if (lane < 16) {
 #pragma unroll
             for (int m = 0; m < M; m++)
-                if (m < rows) acc[m] = fmaf((float)d[m], wsf * xs[(size_t)m * groups + gg], acc[m]);
-        } else if (lane < 16) {
-#pragma unroll
-            for (int m = 0; m < M; m++)
-                dots[(((size_t)block * groups + gg) * M + m) * 16 + row] = d[m];
+                if (m < rows) out[(size_t)m * out_stride + (size_t)block * 16 + row] = acc[m];
         }
-    };
-
-    // Loads for a batch of B groups are issued before any is consumed; the
-    // range is covered by batches of U, then U/2, U/4, ... (all loads of a
-    // batch in flight together), so a wave's few groups never go one by one.
-    auto batch = [&](int g0, auto bsize) __attribute__((always_inline)) {
-        constexpr int B = decltype(bsize)::value;
-        uint4 t[B];
-        int x4[B][M];
-        uint16_t wsr[B];
-#pragma unroll
-        for (int u = 0; u < B; u++) {
-            t[u] = tiles[(size_t)(g0 + u) * 64];
-#pragma unroll
-            for (int m = 0; m < M; m++)  // rows past `rows` reread the last row (unused)
-                x4[u][m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)(g0 + u) * 64) >> 2];
-            wsr[u] = wscale[(g0 + u) * 16];
-        }
-#pragma unroll
-        for (int u = 0; u < B; u++) consume(g0 + u, t[u], x4[u], wsr[u]);
-    };
-    int g = g_begin;
-    for (; g + U <= g_end; g += U) batch(g, std::integral_constant<int, U>());
-    if constexpr (U >= 16) if (g + 8 <= g_end) { batch(g, std::integral_constant<int, 8>()); g += 8; }
-    if constexpr (U >= 8) if (g + 4 <= g_end) { batch(g, std::integral_constant<int, 4>()); g += 4; }
-    if constexpr (U >= 4) if (g + 2 <= g_end) { batch(g, std::integral_constant<int, 2>()); g += 2; }
-    if (g < g_end) batch(g, std::integral_constant<int, 1>());
-    if (fold && lane < 16) {
-#pragma unroll
-        for (int m = 0; m < M; m++)
-            if (m < rows) out[(size_t)m * out_stride + (size_t)block * 16 + row] = acc[m];
+        return;
     }
+    gemv_strip_groups<M, U, false>(
+        tiles, wscale, xrow, xs, k, rows, g_begin, g_end, b2, b3,
+        [&](int gg, const int (&d)[M], uint16_t, const float (&)[M]) __attribute__((always_inline)) {
+            if (lane < 16) {
+#pragma unroll
+                for (int m = 0; m < M; m++) dots[(((size_t)block * groups + gg) * M + m) * 16 + row] = d[m];
+            }
+        });
 }
+
+// The in-order fold of G groups for one output from LDS rows (16-byte
+// aligned, readable up to the next multiple of 4 plus 4): the exact dots `d`,
+// the weight scales `w` (fp16 widened to fp32, exact) and the activation
+// scales `x`; c = w * x is the reference's scale product (one rounding) and
+// acc = fma(d, c, acc) its fold step.  Quads are read one quad ahead of the
+// fma chain, so the chain never waits on LDS.
+__device__ __forceinline__ float fold_lds_row(const float *d, const float *w, const float *x, int groups,
+                                              float acc) {
+    const float4 *d4 = reinterpret_cast<const float4 *>(d), *w4 = reinterpret_cast<const float4 *>(w),
+                 *x4 = reinterpret_cast<const float4 *>(x);
+    const int quads = groups >> 2;
+    float4 dq = d4[0], wq = w4[0], xq = x4[0];
+    for (int i = 0; i < quads; i++) {
+        const float4 dn = d4[i + 1], wn = w4[i + 1], xn = x4[i + 1];
+        acc = fmaf(dq.x, wq.x * xq.x, acc);
+        acc = fmaf(dq.y, wq.y * xq.y, acc);
+        acc = fmaf(dq.z, wq.z * xq.z, acc);
+        acc = fmaf(dq.w, wq.w * xq.w, acc);
+        dq = dn, wq = wn, xq = xn;
+    }
+    const int rest = groups & 3;  // the last partial quad, in dq / wq / xq now
+    if (rest > 0) acc = fmaf(dq.x, wq.x * xq.x, acc);
+    if (rest > 1) acc = fmaf(dq.y, wq.y * xq.y, acc);
+    if (rest > 2) acc = fmaf(dq.z, wq.z * xq.z, acc);
+    return acc;
+}
+// LDS row length (floats) for fold_lds_row over `groups` groups
+__host__ __device__ constexpr int fold_row_floats(int groups) { return ((groups + 3) & ~3) + 4; }
 
 // Few rows, split K inside one block: W = blockDim.x / 64 waves share one
 // 16-row weight strip, wave w taking groups [w G / W, (w + 1) G / W).  Each
-// group's exact dots go to LDS as floats together with the group's scale
-// product f16(ws) * xs; after one barrier, thread (m, r) folds its output's
-// groups in order (the reference's order, one fma each).  No second kernel.
-// Dynamic LDS: 2 x G x M x 16 floats.
+// group's exact dots and weight scale go to LDS (one row per output (m, r),
+// one per weight row r), the activation scales too (loaded first, stored
+// after the weight loads); after one barrier, thread (m, r) folds its
+// output's groups in order (the reference's order, one fma each).  No second
+// kernel.  Dynamic LDS: (16 M + 16 + M) x fold_row_floats(G) floats; M x G
+// <= 4 x blockDim.x.
 template <int M, int U>
 __global__ __launch_bounds__(1024) void k_gemv_split(float *__restrict__ out, size_t out_stride,
                                                      const int8_t *__restrict__ xq,
@@ -219,8 +279,10 @@ __global__ __launch_bounds__(1024) void k_gemv_split(float *__restrict__ out, si
                                                      const uint16_t *__restrict__ ws, int k,
                                                      int rows) {
     extern __shared__ __attribute__((aligned(16))) float s_fold[];
-    const int groups = k >> 6, waves = blockDim.x >> 6;
-    float *s_d = s_fold, *s_c = s_fold + (size_t)groups * M * 16;  // [g][m][r]
+    const int groups = k >> 6, waves = blockDim.x >> 6, gp = fold_row_floats(groups);
+    float *s_d = s_fold;                         // [m][r][g]
+    float *s_w = s_d + (size_t)M * 16 * gp;      // [r][g]
+    float *s_x = s_w + (size_t)16 * gp;          // [m][g]
     const int block = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int g_begin = (int)((long)wave * groups / waves);
     const int g_end = (int)((long)(wave + 1) * groups / waves);
@@ -229,52 +291,30 @@ __global__ __launch_bounds__(1024) void k_gemv_split(float *__restrict__ out, si
     const uint4 *tiles = reinterpret_cast<const uint4 *>(w + (size_t)block * 16 * k) + lane;
     const uint16_t *wscale = ws + (size_t)block * groups * 16 + row;
     const int *xrow = reinterpret_cast<const int *>(xq) + chunk;
-
-    auto consume = [&](int gg, const uint4 &t, const int (&x4)[M], uint16_t wsr) {
-        int d[M];
-        gemv_group_dots<M>(t, x4, b2, b3, d);
-        if (lane < 16) {
-            const float wsf = half_bits_to_float(wsr);
+    float xsv[4];  // this thread's activation scales, stored to LDS after the weight loads
 #pragma unroll
-            for (int m = 0; m < M; m++) {
-                const int mm = min(m, rows - 1);
-                s_d[(gg * M + m) * 16 + row] = (float)d[m];
-                s_c[(gg * M + m) * 16 + row] = wsf * xs[(size_t)mm * groups + gg];
-            }
-        }
-    };
-    // Loads for a batch of B groups are issued before any is consumed; the
-    // range is covered by batches of U, then U/2, U/4, ... (all loads of a
-    // batch in flight together), so a wave's few groups never go one by one.
-    auto batch = [&](int g0, auto bsize) __attribute__((always_inline)) {
-        constexpr int B = decltype(bsize)::value;
-        uint4 t[B];
-        int x4[B][M];
-        uint16_t wsr[B];
+    for (int j = 0; j < 4; j++) {
+        const int i = min((int)threadIdx.x + j * (int)blockDim.x, M * groups - 1);
+        xsv[j] = M == 1 ? xs[i] : xs[(size_t)min(i / groups, rows - 1) * groups + i % groups];
+    }
+    gemv_strip_groups<M, U, false>(tiles, wscale, xrow, xs, k, rows, g_begin, g_end, b2, b3,
+                            [&](int gg, const int (&d)[M], uint16_t wsr, const float (&)[M]) __attribute__((always_inline)) {
+                                if (lane < 16) {
 #pragma unroll
-        for (int u = 0; u < B; u++) {
-            t[u] = tiles[(size_t)(g0 + u) * 64];
+                                    for (int m = 0; m < M; m++) s_d[(m * 16 + row) * gp + gg] = (float)d[m];
+                                    s_w[row * gp + gg] = half_bits_to_float(wsr);
+                                }
+                            });
 #pragma unroll
-            for (int m = 0; m < M; m++)  // rows past `rows` reread the last row (unused)
-                x4[u][m] = xrow[((size_t)min(m, rows - 1) * k + (size_t)(g0 + u) * 64) >> 2];
-            wsr[u] = wscale[(g0 + u) * 16];
-        }
-#pragma unroll
-        for (int u = 0; u < B; u++) consume(g0 + u, t[u], x4[u], wsr[u]);
-    };
-    int g = g_begin;
-    for (; g + U <= g_end; g += U) batch(g, std::integral_constant<int, U>());
-    if constexpr (U >= 16) if (g + 8 <= g_end) { batch(g, std::integral_constant<int, 8>()); g += 8; }
-    if constexpr (U >= 8) if (g + 4 <= g_end) { batch(g, std::integral_constant<int, 4>()); g += 4; }
-    if constexpr (U >= 4) if (g + 2 <= g_end) { batch(g, std::integral_constant<int, 2>()); g += 2; }
-    if (g < g_end) batch(g, std::integral_constant<int, 1>());
+    for (int j = 0; j < 4; j++) {
+        const int i = threadIdx.x + j * blockDim.x;
+        if (i < M * groups) s_x[M == 1 ? i : (i / groups) * gp + i % groups] = xsv[j];
+    }
     __syncthreads();
     const int tid = threadIdx.x;
     if (tid < 16 * M) {
         const int m = tid >> 4, r = tid & 15;
-        const float *pd = s_d + m * 16 + r, *pc = s_c + m * 16 + r;
-        float acc = 0.0f;
-        for (int gg = 0; gg < groups; gg++) acc = fmaf(pd[gg * M * 16], pc[gg * M * 16], acc);
+        const float acc = fold_lds_row(s_d + (size_t)tid * gp, s_w + (size_t)r * gp, s_x + (size_t)m * gp, groups, 0.0f);
         if (m < rows) out[(size_t)m * out_stride + (size_t)block * 16 + r] = acc;
     }
 }
@@ -936,14 +976,22 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
         if (splits > max_splits) splits = max_splits;
     }
     // Split K inside one block when the per-group dots fit in LDS: no fold kernel.
-    const size_t fold_lds = (size_t)2 * groups * m_pad * 16 * sizeof(float);
-    if (splits > 1 && fold_lds <= 64 * 1024) {
-        const int waves = splits < 16 ? splits : 16;
+    const int split_waves = splits < 16 ? splits : 16;
+    const size_t fold_lds = (size_t)(16 * m_pad + 16 + m_pad) * fold_row_floats(groups) * sizeof(float);
+    if (splits > 1 && fold_lds <= 64 * 1024 && m_pad * groups <= 4 * 64 * split_waves) {
+        // one batch of loads per wave where the registers allow it
+        const int per_wave = (groups + split_waves - 1) / split_waves;
 #define G4_GEMV_SPLIT(MM, UU)                                                                   \
-    hipLaunchKernelGGL((k_gemv_split<MM, UU>), dim3((unsigned)blocks), dim3(64 * waves), fold_lds, s, \
+    hipLaunchKernelGGL((k_gemv_split<MM, UU>), dim3((unsigned)blocks), dim3(64 * split_waves), fold_lds, s, \
                        out, out_stride, xq, xs, w, ws, k, rows)
         switch (m_pad) {
-        case 1: G4_GEMV_SPLIT(1, 16); break;
+        case 1:  // batches of at most 12 (16 would spill with 16 waves a block)
+            switch (gemv_batch(per_wave, 12)) {
+            case 4: G4_GEMV_SPLIT(1, 4); break;
+            case 8: G4_GEMV_SPLIT(1, 8); break;
+            default: G4_GEMV_SPLIT(1, 12); break;
+            }
+            break;
         case 2: G4_GEMV_SPLIT(2, 8); break;
         case 4: G4_GEMV_SPLIT(4, 4); break;
         default: G4_GEMV_SPLIT(8, 4); break;
@@ -963,7 +1011,14 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
     hipLaunchKernelGGL((k_gemv<MM, UU>), grid, dim3(64), 0, s, out, out_stride, xq, xs, w, ws, \
                        k, splits, rows, dots)
     switch (m_pad) {
-    case 1: G4_GEMV(1, 16); break;
+    case 1:
+        switch (gemv_batch((groups + splits - 1) / splits, 16)) {
+        case 4: G4_GEMV(1, 4); break;
+        case 8: G4_GEMV(1, 8); break;
+        case 12: G4_GEMV(1, 12); break;
+        default: G4_GEMV(1, 16); break;
+        }
+        break;
     case 2: G4_GEMV(2, 8); break;
     case 4: G4_GEMV(4, 4); break;
     default: G4_GEMV(8, 4); break;
