@@ -1597,17 +1597,21 @@ void launch_qkv_finish(hipStream_t s, float *q, int heads, const float *q_norm, 
 // exactly (o is never -0, v finite or 0), and steps past the last tile skip
 // the chain.
 
-template <int HD, int DEPTH, bool FULL>
-__global__ __launch_bounds__(64) void k_attn_values_decode(float *__restrict__ out,
-                                                           const float *__restrict__ probs,
-                                                           const float *__restrict__ value_cache,
-                                                           int cache_len, int full, int start_pos,
-                                                           const int *__restrict__ pos_dev,
-                                                           size_t stride) {
-    __shared__ __attribute__((aligned(16))) float s_v[2][16][68];  // [slot][channel][position]
+template <int HD, int DEPTH, bool FULL, bool QUANT>
+__global__ __launch_bounds__(QUANT ? 256 : 64) void k_attn_values_decode(float *__restrict__ out,
+                                                                         const float *__restrict__ probs,
+                                                                         const float *__restrict__ value_cache,
+                                                                         int cache_len, int full, int start_pos,
+                                                                         const int *__restrict__ pos_dev,
+                                                                         size_t stride, int8_t *__restrict__ q8,
+                                                                         float *__restrict__ qs) {
+    constexpr int WPB = QUANT ? 4 : 1;  // waves a block; each stages its own tiles
+    __shared__ __attribute__((aligned(16))) float s_vw[WPB][2][16][68];  // [wave][slot][channel][position]
     if (pos_dev) start_pos = *pos_dev;
-    const int lane = threadIdx.x, r = lane >> 4, j = lane & 15;
-    const int c0 = blockIdx.x * 16, t = blockIdx.z;
+    const int wave = WPB > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
+    auto &s_v = s_vw[wave];
+    const int lane = threadIdx.x & 63, r = lane >> 4, j = lane & 15;
+    const int c0 = (blockIdx.x * WPB + wave) * 16, t = blockIdx.z;
     const int pos = start_pos + t, first = FULL ? 0 : first_visible(pos, full);
     const int keys = pos - first + 1, tiles = (keys + 63) / 64, mask = cache_len - 1;
     constexpr uint32_t ROW = HD * 4, TILE = 64 * ROW;  // bytes
@@ -1721,7 +1725,25 @@ __global__ __launch_bounds__(64) void k_attn_values_decode(float *__restrict__ o
         step(tile + 6, v_ring[7], p_ring[6]);
         step(tile + 7, v_ring[0], p_ring[7]);
     }
-    out[((size_t)t * 8 + 4 * blockIdx.y + r) * HD + c0 + j] = o;
+    if constexpr (!QUANT) {
+        out[((size_t)t * 8 + 4 * blockIdx.y + r) * HD + c0 + j] = o;
+    } else {
+        // The block holds channels 64 x .. 64 x + 63 of four heads: one
+        // quantization group each (gemma4.c:264-279, k_quantize's arithmetic),
+        // wave w taking head 4 y + w.  Only the quantized rows are written.
+        __shared__ float s_o[4][64];  // [head][channel]
+        s_o[r][wave * 16 + j] = o;
+        __syncthreads();
+        const float x = s_o[wave][lane];
+        float m = fabsf(x);
+#pragma unroll
+        for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+        const float scale = m / 127.0f;
+        const float inverse = scale > 0.0f ? 1.0f / scale : 0.0f;
+        const size_t at = ((size_t)t * 8 + 4 * blockIdx.y + wave) * HD + (size_t)blockIdx.x * 64;
+        q8[at + lane] = (int8_t)(int)rintf(x * inverse);
+        if (lane == 0) qs[at / 64] = scale;
+    }
 }
 
 int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
@@ -1789,19 +1811,33 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
                            scores, heads, full, start_pos, pos_dev, stride);
     }
     const unsigned slices = (unsigned)(head_dim / 64);
-    if (n <= 4) {  // decode: a wave per (16 channels, 4 heads, token), deep prefetch
-        dim3 grid((unsigned)(head_dim / 16), 2, nn);
-#define G4_PV_DECODE(HD, FULL)                                                                    \
-    hipLaunchKernelGGL((k_attn_values_decode<HD, 8, FULL>), grid, dim3(64), 0, s, out, scores,     \
-                       value_cache, cache_len, full, start_pos, pos_dev, stride)
+    if (n <= 4) {  // decode: a wave per (16 channels, 4 heads, token), deep prefetch; with
+                   // q8 over a window, blocks of 4 such waves (64 channels) quantize their
+                   // rows in place of the fp32 ones.  (Over a long context, four chains
+                   // sharing a CU run at half speed: those waves keep a CU each and the
+                   // rows are quantized after.)
+        const bool fuse = q8 && !full;
+        const unsigned wpb = fuse ? 4u : 1u;
+        dim3 grid((unsigned)(head_dim / 16) / wpb, 2, nn);
+#define G4_PV_DECODE(HD, FULL, QUANT)                                                                 \
+    hipLaunchKernelGGL((k_attn_values_decode<HD, 8, FULL, QUANT>), grid, dim3(64 * wpb), 0, s, out,   \
+                       scores, value_cache, cache_len, full, start_pos, pos_dev, stride, q8, qs)
+#define G4_PV_DECODE_Q(HD, FULL)  \
+    if (fuse)                     \
+        G4_PV_DECODE(HD, FULL, true); \
+    else                          \
+        G4_PV_DECODE(HD, FULL, false)
         if (head_dim == 256) {
-            if (full) G4_PV_DECODE(256, true);
-            else G4_PV_DECODE(256, false);
+            if (full) G4_PV_DECODE(256, true, false);
+            else G4_PV_DECODE_Q(256, false);
         } else {
-            if (full) G4_PV_DECODE(512, true);
-            else G4_PV_DECODE(512, false);
+            if (full) G4_PV_DECODE(512, true, false);
+            else G4_PV_DECODE_Q(512, false);
         }
+#undef G4_PV_DECODE_Q
 #undef G4_PV_DECODE
+        if (q8 && !fuse) launch_quantize(s, q8, qs, out, n * heads * head_dim / 64);
+        return G4_OK;
     } else {  // prefill: 4 tokens x 8 heads per block share each V tile; one
               // tile of prefetch (deeper rings cost registers, hence waves)
         dim3 grid(slices, (nn + 3) / 4);
@@ -1814,8 +1850,6 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
                                value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride, q8, qs);
         return G4_OK;
     }
-    if (q8) launch_quantize(s, q8, qs, out, n * heads * head_dim / 64);
-    return G4_OK;
 }
 
 int launch_attend(hipStream_t s, float *out, const float *q, const float *key_cache,
