@@ -96,6 +96,7 @@ _G4_SIGNATURES = {
     "g4_embedding": (_c_i, [_c_p, _c_p, ctypes.POINTER(Tensor), _c_p, _c_sz, _c_f]),
     "g4_attend": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_sz]),
     "g4_attend_noalloc": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_sz]),
+    "g4_attention_layer": (_c_i, [_c_p, _c_p, _c_sz, _c_i, ctypes.POINTER(Tensor), _c_p, _c_i, _c_i]),
 }
 
 class ImageItem(ctypes.Structure):

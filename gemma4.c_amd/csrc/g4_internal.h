@@ -27,6 +27,13 @@ int set_error(int status, const char *fmt, ...);
         if (!(cond)) return ::g4::set_error(G4_ERR_ARG, __VA_ARGS__);                   \
     } while (0)
 
+// Returns a nonzero status from a call that already recorded its message.
+#define G4_TRY(x)                                                                       \
+    do {                                                                                \
+        int rc_ = (x);                                                                  \
+        if (rc_) return rc_;                                                            \
+    } while (0)
+
 // ---- device helpers ---------------------------------------------------------
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
@@ -100,6 +107,8 @@ int scratch_reserve(size_t dots_bytes, size_t attn_bytes);
 // Frees both buffers (after the device has finished with them); the next
 // reservation allocates afresh and bumps the generation.
 void scratch_release();
+// Frees the per-op attention layer's intermediate buffers (g4_attention_layer).
+void layer_buffers_release();
 
 // ---- launchers (asynchronous on `stream`; shapes validated by callers) -------
 

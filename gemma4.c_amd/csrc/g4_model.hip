@@ -123,6 +123,7 @@ static void free_all(Context &c) {
     if (c.decode_graph) (void)hipGraphExecDestroy(c.decode_graph);
     if (c.stream) (void)hipStreamDestroy(c.stream);
     scratch_release();  // the model's reservation (and anything per-op calls grew)
+    layer_buffers_release();
     c = Context();
 }
 
@@ -138,12 +139,6 @@ static int check_vector(const g4_tensor &t, int n, const char *what, int layer) 
         return set_error(G4_ERR_ARG, "g4_init: %s of layer %d must be fp32 [%d]", what, layer, n);
     return G4_OK;
 }
-
-#define G4_TRY(x)                  \
-    do {                           \
-        int rc_ = (x);             \
-        if (rc_) return rc_;       \
-    } while (0)
 
 // Shape checks for everything the forward pass relies on (the reference trusts
 // the image; gemma4.c:414-421, 464, 131-140 of exporter.py).
@@ -730,7 +725,12 @@ extern "C" int g4_sample(size_t token, float temperature, uint64_t *rng_state, i
 }
 
 extern "C" void g4_shutdown(void) {
-    if (g_ctx.ready || g_ctx.arena) free_all(g_ctx);
+    if (g_ctx.ready || g_ctx.arena) {
+        free_all(g_ctx);
+    } else {  // per-op use only: the buffers those calls grew
+        scratch_release();
+        layer_buffers_release();
+    }
 }
 
 extern "C" void *g4_stream(void) { return g_ctx.stream; }

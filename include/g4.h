@@ -166,6 +166,21 @@ int g4_attend(void *stream, float *out, const float *q, const float *key_cache,
               const float *value_cache, int cache_len, int head_dim, int heads,
               int full_attention, int start_pos, size_t n);
 
+/* gemma4.c:411-461 (attention()): one layer's attention in place over the n
+ * rows (1..G4_BATCH) of `hidden` ([n x G4_HIDDEN] fp32, device, 16-byte
+ * aligned): they come in as attention()'s input (the input norm applied,
+ * gemma4.c:483) and leave as the o projection's output.  `layer` holds the
+ * layer's 19 records in LayerWeights order (gemma4.c:125-155) with device
+ * data; a layer whose k_proj has no data reads the cache without writing it
+ * (the shared layers, gemma4.c:419-421, 432).  `cache` is the cache owner's
+ * keys [cache_len x head_dim] followed by its values (gemma4.c:421-422); new rows
+ * go to (start_pos + t) & (cache_len - 1).  head_dim is q_norm's length (256
+ * or 512), 8 query heads; sliding layers (full_attention = 0) see the last
+ * G4_WINDOW positions.  Grows library-owned device buffers (hipMalloc) when a
+ * call has more rows than they hold; g4_shutdown frees them. */
+int g4_attention_layer(void *stream, float *hidden, size_t n, int start_pos, const g4_tensor *layer,
+                       float *cache, int cache_len, int full_attention);
+
 /* No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  g4_attend with the same arguments and results, its

@@ -48,6 +48,8 @@ _ORACLE_EXTRA = {
     "orc_state_reset": (None, [_p]),
     "orc_state_cache": (ctypes.POINTER(ctypes.c_float), [_p, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "orc_state_residual": (ctypes.POINTER(ctypes.c_float), [_p]),
+    "orc_state_hidden": (ctypes.POINTER(ctypes.c_float), [_p]),
+    "orc_attention_layer": (None, [_p, _p, _i, _i, _sz]),
     "orc_set_threads": (None, [_i]),
     "orc_threads": (_i, []),
     "orc_set_fast": (None, [_i]),
@@ -64,6 +66,7 @@ _REF_EXTRA = {
     "ref_off_sliding": (_sz, []),
     "ref_off_full": (_sz, []),
     "ref_model_weights_offset": (_sz, []),
+    "attention": (None, [_p, _p, _i, _i, _sz, _p]),
     "ref_thread_count": (_i, []),
     "sample": (_i, [_p, _i, _f]),
 }
@@ -235,6 +238,43 @@ class Model:
         else:
             p = self.lib.orc_state_residual(self.state)
         return np.ctypeslib.as_array(p, shape=(rows * HIDDEN,)).reshape(rows, HIDDEN).copy()
+
+    def hidden(self, rows: int) -> np.ndarray:
+        """Writable view of the state's first `rows` hidden rows (the input
+        and output of attention(), gemma4.c:483-484)."""
+        if self.is_ref:
+            p = ctypes.cast(self.state + self.lib.ref_off_hidden(), ctypes.POINTER(ctypes.c_float))
+        else:
+            p = self.lib.orc_state_hidden(self.state)
+        return np.ctypeslib.as_array(p, shape=(rows * HIDDEN,)).reshape(rows, HIDDEN)
+
+    def cache(self, owner: int) -> tuple[np.ndarray, np.ndarray]:
+        """Writable (keys, values) views of cache owner `owner` (0..14):
+        [cache_len x head_dim] each, as the implementation holds them
+        (gemma4.c:164-165, 421-422)."""
+        full = owner % 5 == 4
+        cache_len, hd = (131072, 512) if full else (1024, 256)
+        if self.is_ref:
+            if full:
+                at = self.lib.ref_off_full() + (owner // 5) * 2 * cache_len * hd * 4
+            else:
+                at = self.lib.ref_off_sliding() + ((owner // 5) * 4 + owner % 5) * 2 * cache_len * hd * 4
+            p = ctypes.cast(self.state + at, ctypes.POINTER(ctypes.c_float))
+        else:
+            cl, d = ctypes.c_int(), ctypes.c_int()
+            p = self.lib.orc_state_cache(self.state, owner, ctypes.byref(cl), ctypes.byref(d))
+            assert (cl.value, d.value) == (cache_len, hd)
+        both = np.ctypeslib.as_array(p, shape=(2 * cache_len * hd,)).reshape(2, cache_len, hd)
+        return both[0], both[1]
+
+    def attention_layer(self, layer: int, start_pos: int, n: int) -> None:
+        """attention() of one layer over the first n hidden rows (gemma4.c:411-461)."""
+        if self.is_ref:  # its orphaned `omp for` runs on this one thread
+            layers = self.model + self.lib.ref_model_weights_offset() + 2 * 32
+            scores = np.empty(start_pos + n, np.float32)
+            self.lib.attention(self.state, layers, layer, start_pos, n, ptr(scores))
+        else:
+            self.lib.orc_attention_layer(self.model, self.state, layer, start_pos, n)
 
     def close(self) -> None:
         if not self.is_ref and self.state:

@@ -560,6 +560,18 @@ void orc_attend(float *out, const float *q, const float *key_cache, const float 
     }
 }
 
+/* gemma4.c:411-461: attention() of one layer alone, over the first n rows of
+ * the state's hidden buffer (in: the normalized rows, gemma4.c:483; out: the
+ * o projection's rows), reading and writing the state's caches. */
+void orc_attention_layer(const orc_weights *w, orc_state *s, int layer, int start_pos, size_t n) {
+#pragma omp parallel num_threads(orc_threads())
+    {
+        float *scores = malloc(((size_t)start_pos + n) * sizeof(float));
+        attention_body(s, w->layers, layer, start_pos, n, scores);
+        free(scores);
+    }
+}
+
 /* gemma4.c:463-509: one team for the whole step; every kernel shares its loop. */
 void orc_forward(const orc_weights *w, orc_state *s, const int *tokens, size_t n,
                  int start_pos) {

@@ -69,6 +69,8 @@ void orc_state_reset(orc_state *s);
 float *orc_state_cache(orc_state *s, int layer, int *cache_len, int *head_dim);
 float *orc_state_residual(orc_state *s);
 float *orc_state_hidden(orc_state *s);
+/* gemma4.c:411-461: one layer's attention() over the state's first n hidden rows. */
+void orc_attention_layer(const orc_weights *w, orc_state *s, int layer, int start_pos, size_t n);
 
 /* Threads for the parallel entry points (0 = one per physical core, the rule of
  * gemma4.c:182-188; OMP_NUM_THREADS overrides as there). */

@@ -51,6 +51,14 @@ def test_call_order_errors(pkg):
 
 def test_argument_errors(pkg):
     lib = pkg.lib()
+    # the attention layer checks its arguments before any device call
+    layer = (pkg.Tensor * 19)()
+    assert lib.g4_attention_layer(None, None, 1, 0, layer, 16, 1024, 0) == 1
+    assert b"null pointer" in lib.g4_last_error()
+    assert lib.g4_attention_layer(None, 16, 0, 0, layer, 16, 1024, 0) == 1
+    assert b"rows" in lib.g4_last_error()
+    assert lib.g4_attention_layer(None, 16, 1, 0, layer, 16, 1024, 0) == 1  # empty records
+    assert b"head_dim" in lib.g4_last_error()
     # width not a multiple of 64
     assert lib.g4_quantize(None, 16, 16, 16, 1, 100) == 1
     assert b"multiple of 64" in lib.g4_last_error()

@@ -413,3 +413,52 @@ def test_sample_closed_forms(oracle_lib):
         tok, state = _orc_sample(oracle_lib, flat, 1.0, state)
         assert state == nxt
         assert tok == want, (tok, want)
+
+
+# (layer, start_pos, n): a sliding layer's first chunk and a later chunk over a
+# wrapped ring, a global layer, and two shared layers (layers 15..34 read the
+# caches of owners 13 and 14 without writing, gemma4.c:419-421, 432) in
+# decode and a ragged batch
+ATTENTION_LAYER_CASES = [(0, 0, 512), (3, 1536, 512), (4, 512, 64), (16, 700, 1), (19, 2000, 3)]
+
+
+def attention_layer_inputs(layer: int, start_pos: int, n: int):
+    """The hidden rows and the owner's prior cache rows of one case (N(0,1)):
+    rows start_pos - 1023 .. start_pos - 1 of a sliding ring, 0 .. start_pos - 1
+    of a global one."""
+    owner = layer if layer < 15 else (14 if layer % 5 == 4 else 13)
+    full = owner % 5 == 4
+    g = rng(1000 * layer + start_pos + n)
+    hidden = g.standard_normal((n, 1536)).astype(np.float32)
+    rows = start_pos if full else min(start_pos, 1024)
+    keys = g.standard_normal((rows, 512 if full else 256)).astype(np.float32)
+    values = g.standard_normal(keys.shape).astype(np.float32)
+    slots = np.arange(start_pos - rows, start_pos) & ((131072 if full else 1024) - 1)
+    return owner, hidden, slots, keys, values
+
+
+@pytest.mark.parametrize("layer,start_pos,n", ATTENTION_LAYER_CASES)
+def test_oracle_attention_layer_matches_reference(image, oracle_lib, layer, start_pos, n):
+    """orc_attention_layer against the compiled reference's own attention()
+    (gemma4.c:411-461) on the same hidden rows and prior cache: the output rows
+    and the whole cache owner identical bit for bit."""
+    if not oracle_lib.ref_available():
+        pytest.skip("reference library not built here")
+    owner, hidden, slots, keys, values = attention_layer_inputs(layer, start_pos, n)
+    out = []
+    for use_ref in (False, True):
+        m = oracle_lib.Model(image, use_ref=use_ref)
+        kc, vc = m.cache(owner)
+        kc[slots], vc[slots] = keys, values
+        m.hidden(n)[:] = hidden
+        m.attention_layer(layer, start_pos, n)
+        used = max(start_pos + n, 1024) if owner % 5 == 4 else 1024
+        out.append((m.hidden(n).copy(), kc[:used].copy(), vc[:used].copy()))
+        m.close()
+    for a, b in zip(*out):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # the layer did its work: new output rows, and the new cache rows written
+    assert np.all(np.isfinite(out[0][0])) and not np.array_equal(out[0][0], hidden)
+    if layer < 15:
+        new = np.arange(start_pos, start_pos + n) & (out[0][1].shape[0] - 1)
+        assert np.all(np.abs(out[0][1][new]).sum(axis=1) > 0)
