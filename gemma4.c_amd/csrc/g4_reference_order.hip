@@ -788,9 +788,9 @@ struct RowTail {
         store_row_j<J>(s_row, r);
         __syncthreads();
         // quantize (gemma4.c:265-279) in k_quantize's layout: 16 lanes per
-        // group of 64, four values a lane; waves past the 384 float4s sit out
-        const int T = threadIdx.x;
-        if (T < 384) {
+        // group of 64, four values a lane, the block's threads striding over
+        // the 384 float4s (a group's 16 lanes are always in one wave)
+        for (int T = threadIdx.x; T < 384; T += 64 * NW) {
             const float4 x = reinterpret_cast<const float4 *>(s_row)[T];
             float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
 #pragma unroll
@@ -835,7 +835,7 @@ void k_gemv_tail(GemvJob job, RowTailJob tj) {
     // in flight while the tail runs (more would stall the wave at issue: the
     // memory pipeline takes only so many requests, and the tail would then
     // start after the tiles' data instead of beside it); the rest after it
-    constexpr int PRE = NG < 8 ? NG : 8;
+    constexpr int PRE = NG < 4 ? NG : 4;
     RowTail<NW, TAIL != 3, TAIL != 3, TAIL != 2> tail;
     tail.load(tj);
     __builtin_amdgcn_sched_barrier(0);  // keep the tail's loads ahead of the tiles'
