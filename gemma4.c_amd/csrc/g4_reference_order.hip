@@ -1031,6 +1031,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
                                                      int cache_len, int full, int start_pos, int n,
                                                      const int *__restrict__ pos_dev, size_t stride,
                                                      float *__restrict__ scores) {
+    static_assert(KG >= 2, "the butterfly leaves 8 KG / 16 scores a lane: KG = 1 would store none");
     constexpr int S = HD / 16, SP = S + 4;  // +4 floats: the 16 lanes' 16-byte reads hit distinct banks
     __shared__ __attribute__((aligned(16))) float s_q[TQ * 8][16][SP];
     const int t0 = blockIdx.y * TQ;
@@ -1787,8 +1788,10 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
         return n > 4 && blocks > cap ? cap : blocks;
     };
     const unsigned nn = (unsigned)n;
-    // 4 keys per 16-lane group (8 would halve the query reads from LDS, but
-    // its 250 registers leave 2 waves a SIMD against 3).  One token per block
+    // 4 keys per 16-lane group in prefill (8 would halve the query reads from
+    // LDS, but its 250 registers leave 2 waves a SIMD against 3); 2 in decode
+    // over the window, where the 512 keys then span 16 blocks instead of 8.
+    // One token per block
     // in prefill: a block's waves run one chain of work each, so more blocks
     // (more waves a SIMD) hide more of its latencies than staging the keys
     // for more tokens saves.
@@ -1797,7 +1800,7 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
                        dim3(256), 0, s, q, key_cache, cache_len, full, start_pos, (int)n, pos_dev,  \
                        stride, scores)
     if (head_dim == 256) {
-        if (n <= 4) G4_SCORES(256, 6, 4);
+        if (n <= 4) G4_SCORES(256, 6, 2);  // decode: 32-key blocks, twice the blocks over the window
         else G4_SCORES(256, 1, 4);
     } else {
         G4_SCORES(512, 1, 4);
