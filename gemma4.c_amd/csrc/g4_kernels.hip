@@ -551,17 +551,17 @@ constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 //      wave 2's into padding).
 // k-slots: lane (l%16, l/16) covers k = 16 (l/16) + 0..15 -- for B that is
 // chunks 4 (l/16) .. + 3 of weight row l%16.
-// The fold takes two VALU operations per output: the int8 MFMAs accumulate
-// onto the bits of 1.5 * 2^23, so the sum read as a float is 1.5 * 2^23 + dot
-// exactly (|dot| <= 64 * 127 * 127 < 2^22) and one subtraction recovers the
-// dot (half the cost of an int-to-float conversion); the scale products
+// The fold takes two VALU operations per output: the int32 dot converted to
+// fp32 (exact: |dot| <= 64 * 127 * 127 < 2^24) and the fma -- both 4-byte
+// VOP1/VOP2 encodings (a subtraction of a 32-bit literal would be an 8-byte
+// instruction, measurably slower to issue); the scale products
 // xs[m] * ws[n] of the wave's four 16 x 16 tiles come from one fp32 MFMA with
 // K = 1 (16x16x1, four blocks), whose products are rounded exactly as a VALU
 // multiply, subnormals included.  Block b = 2 mi + ni takes its 16 row
 // scales and 16 column scales from lanes 16 b .. 16 b + 15, and its result
 // lands in the int8 MFMA's output layout (outputs 4 b .. 4 b + 3); a wave of
 // 32 x 16 uses blocks 0 and 2.
-template <int EPI, int WAVES, int NT = 4>
+template <int EPI, int WAVES, int NT = 4, int S = 4>
 __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out, size_t out_stride,
                                                          const int8_t *__restrict__ xq,
                                                          const float *__restrict__ xs,
@@ -590,12 +590,18 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
     };
     // One __shared__ object per stage: the compiler then tells a read of one
     // stage from the DMA writes still landing in the others (with one array
-    // it would wait for every DMA before every LDS read).
-    constexpr int S = 4;  // LDS stages
-    __shared__ Stage st0, st1, st2, st3;
+    // it would wait for every DMA before every LDS read).  S = 3 stages (K =
+    // 1536 only) for the gate/up pair: 45.6 KB of LDS, three blocks a CU
+    // instead of two, so its 768- and 1536-block grids run in whole rounds.
+    static_assert(S == 4 || (S == 3 && EPI == EPI_GELU_PAIR), "4 LDS stages, or 3 for the gate/up pair");
+    __shared__ Stage st0, st1, st2;
+    __shared__ typename std::conditional<S == 4, Stage, char>::type st3;
     __shared__ Scales sc0, sc1;
     auto stage = [&](int i) __attribute__((always_inline)) -> Stage & {
-        return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3;
+        if constexpr (S == 4)
+            return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3;
+        else
+            return i == 0 ? st0 : i == 1 ? st1 : st2;
     };
     const int groups = k >> 6;
     int bx = blockIdx.x;
@@ -612,8 +618,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / NWN, wn = wave % NWN, q = lane >> 4, l16 = lane & 15;
-    constexpr int MAGIC = 0x4B400000;  // 1.5 * 2^23
-    const v4i magic = {MAGIC, MAGIC, MAGIC, MAGIC};
+    const v4i zero4 = {0, 0, 0, 0};
     const v16f zero16 = {};
 
     // DMA sources (group 0, chunk 0); the builtin wants plain void pointers
@@ -699,7 +704,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
     // weight scale stays raw fp16 bits until the multiply step converts it).
     // (with NI = 1 only its blocks 0 and 2 are used)
     struct Dots {
-        v4i d[NB][2][NI];  // 1.5 * 2^23 + dot, as int bits
+        v4i d[NB][2][NI];  // the exact int32 group dots
         v16f c[NB];        // xs * ws, tile (mi, ni) at outputs 4 (2 mi + ni) ..
     };
     struct Frags {
@@ -729,7 +734,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
             for (int ni = 0; ni < NI; ni++)
 #pragma unroll
                 for (int mi = 0; mi < 2; mi++)
-                    o.d[ob][mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[mi], f.b[ob][ni], magic, 0, 0, 0);
+                    o.d[ob][mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.a[mi], f.b[ob][ni], zero4, 0, 0, 0);
             o.c[ob] = __builtin_amdgcn_mfma_f32_16x16x1f32(f.xs, half_bits_to_float(f.ws[ob]), zero16, 0, 0, 0);
         }
     };
@@ -742,7 +747,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
                 for (int mi = 0; mi < 2; mi++)
 #pragma unroll
                     for (int v = 0; v < 4; v++)
-                        acc[ob][mi][ni][v] = fmaf(__int_as_float(o.d[ob][mi][ni][v]) - 12582912.0f,
+                        acc[ob][mi][ni][v] = fmaf((float)o.d[ob][mi][ni][v],
                                                   o.c[ob][4 * (2 * mi + ni) + v], acc[ob][mi][ni][v]);
     };
 
@@ -783,31 +788,41 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
 #pragma unroll
         for (int ni = 0; ni < NI; ni++)
 #pragma unroll
-            for (int mi = 0; mi < 2; mi++) d1.d[ob][mi][ni] = magic;
+            for (int mi = 0; mi < 2; mi++) d1.d[ob][mi][ni] = zero4;
     }
     issue(0, st0, third);
     issue_scales(0, sc0);
 #pragma unroll
     for (int i = 1; i < S - 1; i++) issue(i, stage(i), third);
-    // 16 groups per pass so that every stage and scale buffer is a fixed
-    // object (group g in stage g % S; chunk c = g / 8 in sc0 for even c, sc1
-    // for odd c)
-    auto eight = [&](int g, Scales &sc_use, Scales &sc_next) __attribute__((always_inline)) {
-        step(g + 0, 0, stage((S - 1) % S), stage(0 % S), sc_use, sc_next, d0, d1, third);
-        step(g + 1, 1, stage((S + 0) % S), stage(1 % S), sc_use, sc_next, d1, d0, third);
-        step(g + 2, 2, stage((S + 1) % S), stage(2 % S), sc_use, sc_next, d0, d1, third);
-        step(g + 3, 3, stage((S + 2) % S), stage(3 % S), sc_use, sc_next, d1, d0, third);
-        step(g + 4, 4, stage((S + 3) % S), stage(4 % S), sc_use, sc_next, d0, d1, third);
-        step(g + 5, 5, stage((S + 4) % S), stage(5 % S), sc_use, sc_next, d1, d0, third);
-        step(g + 6, 6, stage((S + 5) % S), stage(6 % S), sc_use, sc_next, d0, d1, third);
-        step(g + 7, 7, stage((S + 6) % S), stage(7 % S), sc_use, sc_next, d1, d0, third);
+    // Passes of 16 groups (S = 4) or 24 (S = 3) so that every stage and
+    // scale buffer is a fixed object: group g in stage g % S (off = g % S at
+    // each call), chunk c = g / 8 in sc0 for even c, sc1 for odd c
+    auto eight = [&](int g, int off, Scales &sc_use, Scales &sc_next) __attribute__((always_inline)) {
+        step(g + 0, 0, stage((off + S - 1) % S), stage((off + 0) % S), sc_use, sc_next, d0, d1, third);
+        step(g + 1, 1, stage((off + S + 0) % S), stage((off + 1) % S), sc_use, sc_next, d1, d0, third);
+        step(g + 2, 2, stage((off + S + 1) % S), stage((off + 2) % S), sc_use, sc_next, d0, d1, third);
+        step(g + 3, 3, stage((off + S + 2) % S), stage((off + 3) % S), sc_use, sc_next, d1, d0, third);
+        step(g + 4, 4, stage((off + S + 3) % S), stage((off + 4) % S), sc_use, sc_next, d0, d1, third);
+        step(g + 5, 5, stage((off + S + 4) % S), stage((off + 5) % S), sc_use, sc_next, d1, d0, third);
+        step(g + 6, 6, stage((off + S + 5) % S), stage((off + 6) % S), sc_use, sc_next, d0, d1, third);
+        step(g + 7, 7, stage((off + S + 6) % S), stage((off + 7) % S), sc_use, sc_next, d1, d0, third);
     };
-    int g = 0;
-    for (; g + 16 <= groups; g += 16) {
-        eight(g, sc0, sc1);
-        eight(g + 8, sc1, sc0);
+    if constexpr (S == 3) {
+        // groups == 24 (the launcher's condition): one pass, written as a
+        // loop so that it stays one scheduling region of its own
+        for (int g = 0; g < groups; g += 24) {
+            eight(g, 0, sc0, sc1);
+            eight(g + 8, 2, sc1, sc0);
+            eight(g + 16, 1, sc0, sc1);
+        }
+    } else {
+        int g = 0;
+        for (; g + 16 <= groups; g += 16) {
+            eight(g, 0, sc0, sc1);
+            eight(g + 8, 0, sc1, sc0);
+        }
+        if (g < groups) eight(g, 0, sc0, sc1);  // uniform: groups % 16 == 8
     }
-    if (g < groups) eight(g, sc0, sc1);  // uniform: groups % 16 == 8
     fold(d1);  // the last group (groups % 8 == 0: it went to d1)
     };
     if (WAVES == 6 && wave == 0)
@@ -897,8 +912,11 @@ int launch_matmul_gelu(hipStream_t s, const int8_t *xq, const float *xs, const i
     if (rows <= 8 || k % 512 || n_out % 64 || (epi != EPI_GELU_PAIR && epi != EPI_GELU_MUL))
         return set_error(G4_ERR_ARG, "fused GEMM: shape %d x %d x %d does not fit", rows, n_out, k);
     const dim3 grid((unsigned)(n_out / 64), (unsigned)((rows + 63) / 64));
-    // the pair variant's 8 stages would take 104 KB: one block per CU
-    if (epi == EPI_GELU_PAIR)
+    // the pair at K = 1536 (every gate/up): 3 LDS stages, three blocks a CU
+    if (epi == EPI_GELU_PAIR && k == 1536)
+        hipLaunchKernelGGL((k_gemm_dma<EPI_GELU_PAIR, 4, 4, 3>), grid, dim3(256), 0, s, nullptr, (size_t)0,
+                           xq, xs, w, ws, rows, n_out, k, ep);
+    else if (epi == EPI_GELU_PAIR)
         hipLaunchKernelGGL((k_gemm_dma<EPI_GELU_PAIR, 4>), grid, dim3(256), 0, s, nullptr, (size_t)0,
                            xq, xs, w, ws, rows, n_out, k, ep);
     else if (small_grid(grid.x * grid.y))
