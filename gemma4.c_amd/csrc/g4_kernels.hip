@@ -1521,6 +1521,13 @@ __global__ __launch_bounds__(256) void k_attn_combine(float *__restrict__ out,
     }
 }
 
+size_t attend_scratch_bytes(size_t n, int last_pos) {
+    const size_t keys = (size_t)last_pos + 1, heads = 8;
+    const size_t scores = n * heads * ((keys + 63) & ~(size_t)63);               // reference order
+    const size_t partials = n * ((keys + kAttnChunk - 1) / kAttnChunk) * heads * (512 + 2);  // parallel
+    return (scores > partials ? scores : partials) * sizeof(float);
+}
+
 int launch_attend_parallel(hipStream_t s, float *out, const float *q, const float *key_cache,
                            const float *value_cache, int cache_len, int head_dim, int heads,
                            int full, int start_pos, size_t n, const FixedScratch *fixed) {

@@ -4,7 +4,7 @@
 // Weights are uploaded once into one HBM arena in the exporter's packed layout
 // (the same bytes as the .bin); the fp32 KV rings (3 global owners x 512
 // channels, growing from 4096 to at most 131072 positions with the context;
-// 12 sliding owners x 1024 x 256; keys then values) and every activation live
+// 12 sliding owners x 2048 x 256; keys then values) and every activation live
 // on the device, so a token step moves only token ids in and one logits row
 // (or one sampled token) out.
 #include <stdarg.h>
@@ -46,6 +46,20 @@ struct Context {
     bool ready = false;
     int device = 0;
     hipStream_t stream = nullptr;
+    // Lane 1 (struct Lane): the second stream of consecutive many-token passes
+    // and its own activation buffers; kv_written[lane][l] is recorded once a
+    // lane's pass has written layer l's key/value rows.
+    hipStream_t lane_stream = nullptr;
+    hipEvent_t kv_written[2][15] = {};
+    float *residual1 = nullptr, *hidden1 = nullptr, *aux1 = nullptr, *ple1 = nullptr;
+    float *k_new1 = nullptr, *v_new1 = nullptr, *qs1 = nullptr, *qsb1 = nullptr;
+    int8_t *q81 = nullptr, *q8b1 = nullptr;
+    int *tokens_dev1 = nullptr, *tokens_pinned1 = nullptr;
+    void *lane_attn[2] = {};  // each lane's attention scratch (lane_attn_bytes each)
+    size_t lane_attn_bytes = 0;
+    int pending = -1;    // the lane whose last pass may still run (-1: none)
+    int next_pos = 0;    // the position after that pass
+    int last_lane = 0;   // the lane holding the last pass's residual rows
     char *arena = nullptr;
     Layer layers[G4_LAYERS];
     Weight embed, embed_ple, ple_model_proj;
@@ -79,6 +93,14 @@ static Context g_ctx;
 
 // Initial positions of a global-attention ring (a power of two).
 constexpr int kGlobalStart = 4096;
+// Positions of a sliding-window ring: a pass of G4_BATCH tokens reads the
+// G4_WINDOW - 1 positions before it, and the pass after it may write its own
+// G4_BATCH positions meanwhile (the two run concurrently, struct Lane), so
+// 2 * G4_BATCH + G4_WINDOW - 1 positions must not share a slot (rounded up to a
+// power of two for the ring mask).
+constexpr int kWindowRing = 2048;
+static_assert(kWindowRing >= 2 * G4_BATCH + G4_WINDOW - 1 && (kWindowRing & (kWindowRing - 1)) == 0,
+              "sliding ring too short for two passes in flight");
 
 static size_t record_bytes(const g4_tensor &t, int index, size_t *scale_bytes) {
     *scale_bytes = 0;
@@ -99,7 +121,9 @@ static void release(void *p) {
 }
 
 static void free_all(Context &c) {
+    if (c.lane_stream) (void)hipStreamSynchronize(c.lane_stream);
     if (c.stream) (void)hipStreamSynchronize(c.stream);
+    for (void *p : c.lane_attn) release(p);
     release(c.arena);
     release(c.residual);
     release(c.residual_alt);
@@ -121,6 +145,16 @@ static void free_all(Context &c) {
     if (c.tokens_pinned) (void)hipHostFree(c.tokens_pinned);
     if (c.pos_pinned) (void)hipHostFree(c.pos_pinned);
     if (c.decode_graph) (void)hipGraphExecDestroy(c.decode_graph);
+    if (c.lane_stream) (void)hipStreamSynchronize(c.lane_stream);
+    for (auto &lane : c.kv_written)
+        for (hipEvent_t e : lane)
+            if (e) (void)hipEventDestroy(e);
+    if (c.lane_stream) (void)hipStreamDestroy(c.lane_stream);
+    for (float *p : {c.residual1, c.hidden1, c.aux1, c.ple1, c.k_new1, c.v_new1, c.qs1, c.qsb1}) release(p);
+    release(c.q81);
+    release(c.q8b1);
+    release(c.tokens_dev1);
+    if (c.tokens_pinned1) (void)hipHostFree(c.tokens_pinned1);
     if (c.stream) (void)hipStreamDestroy(c.stream);
     scratch_release();  // the model's reservation (and anything per-op calls grew)
     layer_buffers_release();
@@ -201,6 +235,9 @@ static int init(const g4_tensor *records, int device) {
     c.device = device;
     G4_HIP(hipSetDevice(device));
     G4_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+    G4_HIP(hipStreamCreateWithFlags(&c.lane_stream, hipStreamNonBlocking));
+    for (auto &lane : c.kv_written)
+        for (hipEvent_t &e : lane) G4_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
 
     // One arena for all weights; records that share host data (the RoPE
     // tables) share device data.
@@ -295,7 +332,7 @@ static int init(const g4_tensor *records, int device) {
         if (!records[2 + l * 19 + 11].data) continue;
         const int full = l % 5 == 4;
         // global rings start at kGlobalStart positions and grow on demand
-        c.cache_len[l] = full ? kGlobalStart : G4_WINDOW + G4_BATCH;
+        c.cache_len[l] = full ? kGlobalStart : kWindowRing;
         c.cache_dim[l] = full ? 512 : 256;
         const size_t bytes = 2 * (size_t)c.cache_len[l] * c.cache_dim[l] * sizeof(float);
         G4_HIP(hipMalloc(&c.cache[l], bytes));
@@ -311,6 +348,19 @@ static int init(const g4_tensor *records, int device) {
     // captured decode step never needs a larger buffer.
     G4_TRY(scratch_reserve((size_t)G4_VOCAB * (G4_HIDDEN / 64) * sizeof(int32_t),
                            (size_t)G4_MAX_CONTEXT * 8 * sizeof(float)));
+    // lane 1's buffers (struct Lane)
+    G4_HIP(hipMalloc(&c.residual1, (size_t)G4_BATCH * G4_HIDDEN * sizeof(float)));
+    G4_HIP(hipMalloc(&c.hidden1, wide * sizeof(float)));
+    G4_HIP(hipMalloc(&c.aux1, wide * sizeof(float)));
+    G4_HIP(hipMalloc(&c.ple1, (size_t)G4_BATCH * G4_LAYERS * G4_PLE * sizeof(float)));
+    G4_HIP(hipMalloc(&c.k_new1, (size_t)G4_BATCH * 512 * sizeof(float)));
+    G4_HIP(hipMalloc(&c.v_new1, (size_t)G4_BATCH * 512 * sizeof(float)));
+    G4_HIP(hipMalloc(&c.q81, wide));
+    G4_HIP(hipMalloc(&c.qs1, wide / 64 * sizeof(float)));
+    G4_HIP(hipMalloc(&c.q8b1, wide));
+    G4_HIP(hipMalloc(&c.qsb1, wide / 64 * sizeof(float)));
+    G4_HIP(hipMalloc(&c.tokens_dev1, G4_BATCH * sizeof(int)));
+    G4_HIP(hipHostMalloc((void **)&c.tokens_pinned1, G4_BATCH * sizeof(int), hipHostMallocDefault));
     G4_HIP(hipDeviceSynchronize());
     c.ready = true;
     return G4_OK;
@@ -322,22 +372,76 @@ static int matmul(Context &c, float *out, size_t stride, const Weight &w, int ro
                          w.data, w.scales, w.n, w.k, rows);
 }
 
+// A stream and the activation buffers one forward pass runs on.  Lane 0 is
+// c.stream with the context's first set of buffers (every one-token step and
+// every other entry point uses it); lane 1 is c.lane_stream with the second
+// set.  Consecutive many-token passes over consecutive positions (the chunks
+// of a long prefill, gemma4.c:563-566) alternate lanes and run concurrently:
+// a pass's attention at layer l reads the key/value rows the pass before it
+// wrote at layer l, so it waits for them (wait_kv[l]), and its own rows are
+// announced to the pass after it (record_kv[l]).  Every other op is local to
+// the pass's rows.  The window rings are long enough that the two passes'
+// rows never share a slot (kWindowRing).
+struct Lane {
+    hipStream_t stream = nullptr;
+    float *residual = nullptr, *hidden = nullptr, *aux = nullptr, *ple = nullptr;
+    float *k_new = nullptr, *v_new = nullptr;
+    int8_t *q8 = nullptr, *q8b = nullptr;
+    float *qs = nullptr, *qsb = nullptr;
+    int *tokens_dev = nullptr, *tokens_pinned = nullptr;
+    const FixedScratch *attn_scratch = nullptr;  // null: the library's attention scratch
+    hipEvent_t *record_kv = nullptr;             // record [l] after layer l's key/value rows
+    hipEvent_t *wait_kv = nullptr;               // wait for [l] before layer l's attention
+};
+
+static Lane make_lane(Context &c, int index) {
+    Lane ln;
+    if (index == 0) {
+        ln.stream = c.stream;
+        ln.residual = c.residual, ln.hidden = c.hidden, ln.aux = c.aux, ln.ple = c.ple;
+        ln.k_new = c.k_new, ln.v_new = c.v_new;
+        ln.q8 = c.q8, ln.q8b = c.q8b, ln.qs = c.qs, ln.qsb = c.qsb;
+        ln.tokens_dev = c.tokens_dev, ln.tokens_pinned = c.tokens_pinned;
+    } else {
+        ln.stream = c.lane_stream;
+        ln.residual = c.residual1, ln.hidden = c.hidden1, ln.aux = c.aux1, ln.ple = c.ple1;
+        ln.k_new = c.k_new1, ln.v_new = c.v_new1;
+        ln.q8 = c.q81, ln.q8b = c.q8b1, ln.qs = c.qs1, ln.qsb = c.qsb1;
+        ln.tokens_dev = c.tokens_dev1, ln.tokens_pinned = c.tokens_pinned1;
+    }
+    return ln;
+}
+
+// Wait for both lanes; afterwards lane 0's buffers and stream serve any call.
+static int drain(Context &c) {
+    if (c.pending < 0) return G4_OK;
+    c.pending = -1;
+    G4_HIP(hipStreamSynchronize(c.lane_stream));
+    G4_HIP(hipStreamSynchronize(c.stream));
+    return G4_OK;
+}
+
 // The sequence of gemma4.c:463-509 (attention: 411-461) for the n tokens in
-// c.tokens_dev, as launches on c.stream.  With pos_dev non-null (n == 1) the
+// ln.tokens_dev (at positions from start_pos), as launches on ln.stream over
+// the lane's buffers.  With pos_dev non-null (n == 1) the
 // position-dependent kernels read the position from the device, so the
 // launches can be captured once and replayed at every position.
-static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev) {
-    hipStream_t s = c.stream;
+static int enqueue_forward(Context &c, const Lane &ln, int n, int start_pos, const int *pos_dev) {
+    hipStream_t s = ln.stream;
+    auto matmul = [&](float *out, size_t stride, const Weight &w, int rows, bool second = false) {
+        return launch_matmul(s, out, stride, second ? ln.q8b : ln.q8, second ? ln.qsb : ln.qs, w.data,
+                             w.scales, w.n, w.k, rows);
+    };
     const int ple_width = G4_LAYERS * G4_PLE;
 
-    launch_embedding(s, c.residual, c.embed.data, c.embed.scales, G4_HIDDEN, c.embed.n, c.tokens_dev,
+    launch_embedding(s, ln.residual, c.embed.data, c.embed.scales, G4_HIDDEN, c.embed.n, ln.tokens_dev,
                      n, sqrtf((float)G4_HIDDEN));
-    launch_quantize(s, c.q8, c.qs, c.residual, (size_t)n * G4_HIDDEN / 64);
-    G4_TRY(matmul(c, c.ple, ple_width, c.ple_model_proj, n));
-    launch_rmsnorm(s, c.ple, c.ple, c.ple_norm, G4_PLE, 1e-6f * G4_HIDDEN, (size_t)n * G4_LAYERS);
-    launch_embedding(s, c.hidden, c.embed_ple.data, c.embed_ple.scales, ple_width, c.embed_ple.n,
-                     c.tokens_dev, n, sqrtf((float)G4_PLE));
-    launch_add_and_scale(s, c.ple, c.hidden, (size_t)n * ple_width, 1.0f / sqrtf(2.0f));
+    launch_quantize(s, ln.q8, ln.qs, ln.residual, (size_t)n * G4_HIDDEN / 64);
+    G4_TRY(matmul(ln.ple, ple_width, c.ple_model_proj, n));
+    launch_rmsnorm(s, ln.ple, ln.ple, c.ple_norm, G4_PLE, 1e-6f * G4_HIDDEN, (size_t)n * G4_LAYERS);
+    launch_embedding(s, ln.hidden, c.embed_ple.data, c.embed_ple.scales, ple_width, c.embed_ple.n,
+                     ln.tokens_dev, n, sqrtf((float)G4_PLE));
+    launch_add_and_scale(s, ln.ple, ln.hidden, (size_t)n * ple_width, 1.0f / sqrtf(2.0f));
 
     // In reference order the row-local ops between matmuls run fused
     // (launch_row_tail): the same arithmetic in one launch instead of up to four.
@@ -348,9 +452,9 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
     // the per-layer-embedding gate likewise, into q8b).  The tails alternate
     // two residual rows, since every block of a product reads the residual
     // that block 0 updates: 104 updates a step, so the step ends in
-    // c.residual again.
+    // ln.residual again.
     const bool one = fused && n == 1;
-    float *res[2] = {c.residual, c.residual_alt};
+    float *res[2] = {ln.residual, c.residual_alt};
     int p = 0;  // res[p] holds the residual
     auto tail_job = [&](const float *h, const float *w_in, float scale, const float *w_out) {
         RowTailJob tj{};
@@ -365,8 +469,8 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
         return tj;
     };
     if (fused && !one)  // layer 0's input norm + quantize
-        launch_row_tail(s, nullptr, nullptr, c.residual, 1.0f, c.layers[0].input_ln, nullptr, c.q8,
-                        c.qs, 1e-6f, n, 0, 0, 1, 1);
+        launch_row_tail(s, nullptr, nullptr, ln.residual, 1.0f, c.layers[0].input_ln, nullptr, ln.q8,
+                        ln.qs, 1e-6f, n, 0, 0, 1, 1);
     auto job_on = [&]() {
         GemvJob job{};
         job.gelu_table = c.gelu;
@@ -379,8 +483,8 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
         const Layer &L = c.layers[l];
         const int hd = L.head_dim, qw = L.query_width, heads = qw / hd;
         if (!fused) {
-            launch_rmsnorm(s, c.hidden, c.residual, L.input_ln, G4_HIDDEN, 1e-6f, n);
-            launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_HIDDEN / 64);
+            launch_rmsnorm(s, ln.hidden, ln.residual, L.input_ln, G4_HIDDEN, 1e-6f, n);
+            launch_quantize(s, ln.q8, ln.qs, ln.hidden, (size_t)n * G4_HIDDEN / 64);
         }
 
         // attention
@@ -390,60 +494,62 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
         if (one) {
             GemvJob job = job_on();
             job.k = G4_HIDDEN;
-            job.m[0] = GemvMat{L.q.data, L.q.scales, c.aux, qw / 16};
+            job.m[0] = GemvMat{L.q.data, L.q.scales, ln.aux, qw / 16};
             job.count = 1;
             if (L.k.data) {
-                job.m[1] = GemvMat{L.k.data, L.k.scales, c.k_new, hd / 16};
-                job.m[2] = GemvMat{L.v.data, L.v.scales, c.v_new, hd / 16};
+                job.m[1] = GemvMat{L.k.data, L.k.scales, ln.k_new, hd / 16};
+                job.m[2] = GemvMat{L.v.data, L.v.scales, ln.v_new, hd / 16};
                 job.count = 3;
             }
             // the previous layer's last tail + this layer's input norm (layer
             // 0: the input norm alone)
             const RowTailJob tj = l == 0 ? tail_job(nullptr, nullptr, 1.0f, L.input_ln)
-                                         : tail_job(c.hidden, c.layers[l - 1].post_ple_ln,
+                                         : tail_job(ln.hidden, c.layers[l - 1].post_ple_ln,
                                                     c.layers[l - 1].layer_scalar, L.input_ln);
             G4_TRY(launch_gemv_tail(s, job, EPI_PLAIN, tj, l == 0 ? 3 : 1));
         } else if (L.k.data && n > 8 && G4_HIDDEN % 512 == 0) {
             // q, k and v read the same rows: one launch fills the chip
             const int8_t *w[3] = {L.q.data, L.k.data, L.v.data};
             const uint16_t *ws[3] = {L.q.scales, L.k.scales, L.v.scales};
-            float *out[3] = {c.aux, c.k_new, c.v_new};
+            float *out[3] = {ln.aux, ln.k_new, ln.v_new};
             const size_t strides[3] = {(size_t)qw, (size_t)hd, (size_t)hd};
             const int ns[3] = {L.q.n, L.k.n, L.v.n};
-            G4_TRY(launch_matmul_group(s, c.q8, c.qs, n, G4_HIDDEN, 3, w, ws, out, strides, ns));
+            G4_TRY(launch_matmul_group(s, ln.q8, ln.qs, n, G4_HIDDEN, 3, w, ws, out, strides, ns));
         } else {
-            G4_TRY(matmul(c, c.aux, qw, L.q, n));
+            G4_TRY(matmul(ln.aux, qw, L.q, n));
             if (L.k.data) {
-                G4_TRY(matmul(c, c.k_new, hd, L.k, n));
-                G4_TRY(matmul(c, c.v_new, hd, L.v, n));
+                G4_TRY(matmul(ln.k_new, hd, L.k, n));
+                G4_TRY(matmul(ln.v_new, hd, L.v, n));
             }
         }
         if (fused) {  // query norms + RoPE and the new key/value rows: one launch
-            launch_qkv_finish(s, c.aux, heads, L.q_norm, L.k.data ? c.k_new : nullptr, c.v_new,
+            launch_qkv_finish(s, ln.aux, heads, L.q_norm, L.k.data ? ln.k_new : nullptr, ln.v_new,
                               L.k_norm, keys, values, L.rope_cos, L.rope_sin, L.pairs, hd, cache_len,
                               start_pos, pos_dev, n);
         } else {
-            launch_rmsnorm(s, c.aux, c.aux, L.q_norm, hd, 1e-6f, (size_t)n * heads);
-            launch_rope(s, L.rope_cos, L.rope_sin, L.pairs, c.aux, heads, hd, start_pos, pos_dev, n);
+            launch_rmsnorm(s, ln.aux, ln.aux, L.q_norm, hd, 1e-6f, (size_t)n * heads);
+            launch_rope(s, L.rope_cos, L.rope_sin, L.pairs, ln.aux, heads, hd, start_pos, pos_dev, n);
             if (L.k.data)
-                launch_kv_finish(s, keys, values, c.k_new, c.v_new, L.k_norm, L.rope_cos, L.rope_sin,
+                launch_kv_finish(s, keys, values, ln.k_new, ln.v_new, L.k_norm, L.rope_cos, L.rope_sin,
                                  L.pairs, hd, cache_len, start_pos, pos_dev, n);
         }
-        G4_TRY(launch_attend(s, c.hidden, c.aux, keys, values, cache_len, hd, heads, L.full,
-                             start_pos, pos_dev, n, c.q8, c.qs));
-        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.o, n));
+        if (L.k.data && ln.record_kv) G4_HIP(hipEventRecord(ln.record_kv[l], s));
+        if (L.k.data && ln.wait_kv) G4_HIP(hipStreamWaitEvent(s, ln.wait_kv[l], 0));
+        G4_TRY(launch_attend(s, ln.hidden, ln.aux, keys, values, cache_len, hd, heads, L.full,
+                             start_pos, pos_dev, n, ln.q8, ln.qs, ln.attn_scratch));
+        G4_TRY(matmul(ln.hidden, G4_HIDDEN, L.o, n));
 
         // feed-forward
         if (one) {
             // the tail runs inside the gate/up product below
         } else if (fused) {
-            launch_row_tail(s, c.hidden, L.post_attn_ln, c.residual, 1.0f, L.pre_ffn_ln, nullptr,
-                            c.q8, c.qs, 1e-6f, n, 1, 1, 1, 1);
+            launch_row_tail(s, ln.hidden, L.post_attn_ln, ln.residual, 1.0f, L.pre_ffn_ln, nullptr,
+                            ln.q8, ln.qs, 1e-6f, n, 1, 1, 1, 1);
         } else {
-            launch_rmsnorm(s, c.hidden, c.hidden, L.post_attn_ln, G4_HIDDEN, 1e-6f, n);
-            launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, 1.0f);
-            launch_rmsnorm(s, c.hidden, c.residual, L.pre_ffn_ln, G4_HIDDEN, 1e-6f, n);
-            launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_HIDDEN / 64);
+            launch_rmsnorm(s, ln.hidden, ln.hidden, L.post_attn_ln, G4_HIDDEN, 1e-6f, n);
+            launch_add_and_scale(s, ln.residual, ln.hidden, (size_t)n * G4_HIDDEN, 1.0f);
+            launch_rmsnorm(s, ln.hidden, ln.residual, L.pre_ffn_ln, G4_HIDDEN, 1e-6f, n);
+            launch_quantize(s, ln.q8, ln.qs, ln.hidden, (size_t)n * G4_HIDDEN / 64);
         }
         // many rows: gate and up in one GEMM whose epilogue applies geglu and
         // quantizes (into q8b)
@@ -454,15 +560,15 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
             ep.gelu_size = c.gelu_size;
             ep.gelu_lower = c.gelu_lower;
             ep.gelu_upper = c.gelu_upper;
-            ep.q_out = c.q8b;
-            ep.qs_out = c.qsb;
+            ep.q_out = ln.q8b;
+            ep.qs_out = ln.qsb;
             return ep;
         };
         if (gemm_fused) {
             GemmEpilogue ep = gelu_epilogue();
             ep.w2 = L.up.data;
             ep.ws2 = L.up.scales;
-            G4_TRY(launch_matmul_gelu(s, c.q8, c.qs, L.gate.data, L.gate.scales, L.ffn, G4_HIDDEN, n,
+            G4_TRY(launch_matmul_gelu(s, ln.q8, ln.qs, L.gate.data, L.gate.scales, L.ffn, G4_HIDDEN, n,
                                       EPI_GELU_PAIR, ep));
         } else if (one) {
             GemvJob job = job_on();
@@ -470,67 +576,67 @@ static int enqueue_forward(Context &c, int n, int start_pos, const int *pos_dev)
             job.m[0] = GemvMat{L.gate.data, L.gate.scales, nullptr, L.ffn / 16};
             job.m[1] = GemvMat{L.up.data, L.up.scales, nullptr, L.ffn / 16};
             job.count = 2;
-            job.q_out = c.q8b;
-            job.qs_out = c.qsb;
-            const RowTailJob tj = tail_job(c.hidden, L.post_attn_ln, 1.0f, L.pre_ffn_ln);
+            job.q_out = ln.q8b;
+            job.qs_out = ln.qsb;
+            const RowTailJob tj = tail_job(ln.hidden, L.post_attn_ln, 1.0f, L.pre_ffn_ln);
             G4_TRY(launch_gemv_tail(s, job, EPI_GELU_PAIR, tj, 1));
         } else {
-            G4_TRY(matmul(c, c.hidden, L.ffn, L.gate, n));
-            G4_TRY(matmul(c, c.aux, L.ffn, L.up, n));
-            launch_geglu(s, c.hidden, c.aux, n, L.ffn, L.ffn, c.gelu, c.gelu_size, c.gelu_lower,
+            G4_TRY(matmul(ln.hidden, L.ffn, L.gate, n));
+            G4_TRY(matmul(ln.aux, L.ffn, L.up, n));
+            launch_geglu(s, ln.hidden, ln.aux, n, L.ffn, L.ffn, c.gelu, c.gelu_size, c.gelu_lower,
                          c.gelu_upper);
-            launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * L.ffn / 64);
+            launch_quantize(s, ln.q8, ln.qs, ln.hidden, (size_t)n * L.ffn / 64);
         }
-        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.down, n, one || gemm_fused));
+        G4_TRY(matmul(ln.hidden, G4_HIDDEN, L.down, n, one || gemm_fused));
 
         // per-layer embedding
         if (one) {
             // the tail runs inside the per-layer-embedding gate below
         } else if (fused) {
-            launch_row_tail(s, c.hidden, L.post_ffn_ln, c.residual, 1.0f, nullptr, nullptr, c.q8,
-                            c.qs, 1e-6f, n, 1, 1, 0, 1);
+            launch_row_tail(s, ln.hidden, L.post_ffn_ln, ln.residual, 1.0f, nullptr, nullptr, ln.q8,
+                            ln.qs, 1e-6f, n, 1, 1, 0, 1);
         } else {
-            launch_rmsnorm(s, c.hidden, c.hidden, L.post_ffn_ln, G4_HIDDEN, 1e-6f, n);
-            launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, 1.0f);
-            launch_quantize(s, c.q8, c.qs, c.residual, (size_t)n * G4_HIDDEN / 64);
+            launch_rmsnorm(s, ln.hidden, ln.hidden, L.post_ffn_ln, G4_HIDDEN, 1e-6f, n);
+            launch_add_and_scale(s, ln.residual, ln.hidden, (size_t)n * G4_HIDDEN, 1.0f);
+            launch_quantize(s, ln.q8, ln.qs, ln.residual, (size_t)n * G4_HIDDEN / 64);
         }
         if (gemm_fused) {
             GemmEpilogue ep = gelu_epilogue();
-            ep.mul = c.ple + (size_t)l * G4_PLE;
+            ep.mul = ln.ple + (size_t)l * G4_PLE;
             ep.mul_stride = ple_width;
-            G4_TRY(launch_matmul_gelu(s, c.q8, c.qs, L.ple_gate.data, L.ple_gate.scales, G4_PLE,
+            G4_TRY(launch_matmul_gelu(s, ln.q8, ln.qs, L.ple_gate.data, L.ple_gate.scales, G4_PLE,
                                       G4_HIDDEN, n, EPI_GELU_MUL, ep));
         } else if (one) {
             GemvJob job = job_on();
             job.k = G4_HIDDEN;
             job.m[0] = GemvMat{L.ple_gate.data, L.ple_gate.scales, nullptr, G4_PLE / 16};
             job.count = 1;
-            job.mul = c.ple + (size_t)l * G4_PLE;
-            job.q_out = c.q8b;
-            job.qs_out = c.qsb;
-            const RowTailJob tj = tail_job(c.hidden, L.post_ffn_ln, 1.0f, nullptr);
+            job.mul = ln.ple + (size_t)l * G4_PLE;
+            job.q_out = ln.q8b;
+            job.qs_out = ln.qsb;
+            const RowTailJob tj = tail_job(ln.hidden, L.post_ffn_ln, 1.0f, nullptr);
             G4_TRY(launch_gemv_tail(s, job, EPI_GELU_MUL, tj, 2));
         } else {
-            G4_TRY(matmul(c, c.hidden, G4_PLE, L.ple_gate, n));
-            launch_geglu(s, c.hidden, c.ple + (size_t)l * G4_PLE, n, G4_PLE, ple_width, c.gelu,
+            G4_TRY(matmul(ln.hidden, G4_PLE, L.ple_gate, n));
+            launch_geglu(s, ln.hidden, ln.ple + (size_t)l * G4_PLE, n, G4_PLE, ple_width, c.gelu,
                          c.gelu_size, c.gelu_lower, c.gelu_upper);
-            launch_quantize(s, c.q8, c.qs, c.hidden, (size_t)n * G4_PLE / 64);
+            launch_quantize(s, ln.q8, ln.qs, ln.hidden, (size_t)n * G4_PLE / 64);
         }
-        G4_TRY(matmul(c, c.hidden, G4_HIDDEN, L.ple_proj, n, one || gemm_fused));
+        G4_TRY(matmul(ln.hidden, G4_HIDDEN, L.ple_proj, n, one || gemm_fused));
         if (one) {
             if (l + 1 == G4_LAYERS)  // the last tail, in place (the others run in the next q/k/v)
-                launch_row_tail(s, c.hidden, L.post_ple_ln, res[p], L.layer_scalar, nullptr, nullptr,
+                launch_row_tail(s, ln.hidden, L.post_ple_ln, res[p], L.layer_scalar, nullptr, nullptr,
                                 nullptr, nullptr, 1e-6f, n, 1, 1, 0, 0);
         } else if (fused) {
             if (l + 1 < G4_LAYERS)  // + the next layer's input norm and quantize
-                launch_row_tail(s, c.hidden, L.post_ple_ln, c.residual, L.layer_scalar,
-                                c.layers[l + 1].input_ln, nullptr, c.q8, c.qs, 1e-6f, n, 1, 1, 1, 1);
+                launch_row_tail(s, ln.hidden, L.post_ple_ln, ln.residual, L.layer_scalar,
+                                c.layers[l + 1].input_ln, nullptr, ln.q8, ln.qs, 1e-6f, n, 1, 1, 1, 1);
             else
-                launch_row_tail(s, c.hidden, L.post_ple_ln, c.residual, L.layer_scalar, nullptr,
+                launch_row_tail(s, ln.hidden, L.post_ple_ln, ln.residual, L.layer_scalar, nullptr,
                                 nullptr, nullptr, nullptr, 1e-6f, n, 1, 1, 0, 0);
         } else {
-            launch_rmsnorm(s, c.hidden, c.hidden, L.post_ple_ln, G4_HIDDEN, 1e-6f, n);
-            launch_add_and_scale(s, c.residual, c.hidden, (size_t)n * G4_HIDDEN, L.layer_scalar);
+            launch_rmsnorm(s, ln.hidden, ln.hidden, L.post_ple_ln, G4_HIDDEN, 1e-6f, n);
+            launch_add_and_scale(s, ln.residual, ln.hidden, (size_t)n * G4_HIDDEN, L.layer_scalar);
         }
     }
     if (p != 0) return set_error(G4_ERR_STATE, "one-token step ended in the alternate residual row");
@@ -546,7 +652,7 @@ static int capture_decode(Context &c) {
     }
     hipGraph_t graph = nullptr;
     G4_HIP(hipStreamBeginCapture(c.stream, hipStreamCaptureModeRelaxed));
-    const int rc = enqueue_forward(c, 1, 0, c.pos_dev);
+    const int rc = enqueue_forward(c, make_lane(c, 0), 1, 0, c.pos_dev);
     hipError_t end = hipStreamEndCapture(c.stream, &graph);
     if (rc) {
         if (graph) (void)hipGraphDestroy(graph);
@@ -575,6 +681,7 @@ static int ensure_kv(Context &c, int last_pos) {
     const int need = last_pos + G4_BATCH < G4_MAX_CONTEXT ? last_pos + G4_BATCH : G4_MAX_CONTEXT - 1;
     for (int l = 0; l < 15; l++) {
         if (!c.cache[l] || c.cache_dim[l] != 512 || need < c.cache_len[l]) continue;
+        G4_TRY(drain(c));  // a pass in flight may read the ring
         int len = c.cache_len[l];
         while (len <= need && len < G4_MAX_CONTEXT) len *= 2;
         const size_t hd = (size_t)c.cache_dim[l], old_len = (size_t)c.cache_len[l];
@@ -601,35 +708,91 @@ static int ensure_kv(Context &c, int last_pos) {
     return G4_OK;
 }
 
-static int forward(Context &c, const int *tokens, int n, int start_pos) {
-    hipStream_t s = c.stream;
-    G4_TRY(ensure_kv(c, start_pos + n - 1));
-    memcpy(c.tokens_pinned, tokens, (size_t)n * sizeof(int));
-    G4_HIP(hipMemcpyAsync(c.tokens_dev, c.tokens_pinned, (size_t)n * sizeof(int),
-                          hipMemcpyHostToDevice, s));
-    if (n == 1 && order() == G4_ORDER_REFERENCE) {
-        *c.pos_pinned = start_pos;
-        G4_HIP(hipMemcpyAsync(c.pos_dev, c.pos_pinned, sizeof(int), hipMemcpyHostToDevice, s));
-        if (!c.decode_graph || c.graph_generation != scratch().generation || c.graph_order != order() ||
-            c.graph_kv_generation != c.kv_generation)
-            G4_TRY(capture_decode(c));
-        G4_HIP(hipGraphLaunch(c.decode_graph, s));
-    } else {
-        G4_TRY(enqueue_forward(c, n, start_pos, nullptr));
+// Each lane's attention scratch, grown (both lanes drained first) to `bytes`.
+static int reserve_lane_attn(Context &c, size_t bytes) {
+    if (bytes <= c.lane_attn_bytes) return G4_OK;
+    G4_TRY(drain(c));
+    for (void *&p : c.lane_attn) {
+        release(p);
+        p = nullptr;
     }
-    G4_HIP(hipStreamSynchronize(s));
-    c.last_n = n;
+    c.lane_attn_bytes = 0;
+    for (void *&p : c.lane_attn) G4_HIP(hipMalloc(&p, bytes));
+    c.lane_attn_bytes = bytes;
     return G4_OK;
 }
 
+// gemma4.c:463 for n tokens at start_pos.  A pass of more than 8 tokens is
+// enqueued and left running on a lane (struct Lane): when it continues the
+// pass before it (start_pos where that one ended) the two run concurrently;
+// every entry point that reads results, and any other pass, waits first
+// (drain).  At most one pass per lane is in flight.  Shorter passes (decode
+// steps) run on lane 0 and return finished.
+static int forward(Context &c, const int *tokens, int n, int start_pos) {
+    const int last_pos = start_pos + n - 1;
+    if (n <= 8) {  // their products take the split-K GEMV, whose scratch is shared
+        G4_TRY(drain(c));
+        G4_TRY(ensure_kv(c, last_pos));
+        hipStream_t s = c.stream;
+        memcpy(c.tokens_pinned, tokens, (size_t)n * sizeof(int));
+        G4_HIP(hipMemcpyAsync(c.tokens_dev, c.tokens_pinned, (size_t)n * sizeof(int),
+                              hipMemcpyHostToDevice, s));
+        if (n == 1 && order() == G4_ORDER_REFERENCE) {
+            *c.pos_pinned = start_pos;
+            G4_HIP(hipMemcpyAsync(c.pos_dev, c.pos_pinned, sizeof(int), hipMemcpyHostToDevice, s));
+            if (!c.decode_graph || c.graph_generation != scratch().generation ||
+                c.graph_order != order() || c.graph_kv_generation != c.kv_generation)
+                G4_TRY(capture_decode(c));
+            G4_HIP(hipGraphLaunch(c.decode_graph, s));
+        } else {
+            G4_TRY(enqueue_forward(c, make_lane(c, 0), n, start_pos, nullptr));
+        }
+        G4_HIP(hipStreamSynchronize(s));
+        c.last_n = n;
+        c.last_lane = 0;
+        return G4_OK;
+    }
+    G4_TRY(ensure_kv(c, last_pos));  // these two drain before they move a buffer
+    G4_TRY(reserve_lane_attn(c, attend_scratch_bytes(G4_BATCH, last_pos)));
+    const bool follow = c.pending >= 0 && start_pos == c.next_pos;
+    if (!follow) G4_TRY(drain(c));
+    const int lane = follow ? c.pending ^ 1 : 0;
+    Lane ln = make_lane(c, lane);
+    G4_HIP(hipStreamSynchronize(ln.stream));  // the lane's previous pass: its buffers are free
+    const FixedScratch attn{c.lane_attn[lane], c.lane_attn_bytes};
+    ln.attn_scratch = &attn;
+    ln.record_kv = c.kv_written[lane];
+    ln.wait_kv = follow ? c.kv_written[lane ^ 1] : nullptr;
+    memcpy(ln.tokens_pinned, tokens, (size_t)n * sizeof(int));
+    G4_HIP(hipMemcpyAsync(ln.tokens_dev, ln.tokens_pinned, (size_t)n * sizeof(int), hipMemcpyHostToDevice,
+                          ln.stream));
+    c.pending = lane;
+    c.next_pos = start_pos + n;
+    c.last_lane = lane;
+    c.last_n = n;
+    const int rc = enqueue_forward(c, ln, n, start_pos, nullptr);
+    if (rc) {
+        char saved[sizeof(g_error)];
+        memcpy(saved, g_error, sizeof(saved));
+        (void)drain(c);
+        memcpy(g_error, saved, sizeof(saved));
+        c.last_n = 0;
+    }
+    return rc;
+}
+
 // gemma4.c:512-522 for `rows` consecutive rows starting at `row`, into dst.
+// The rows are the last pass's (on its lane); the work runs on lane 0 once
+// both lanes have finished.
 static int logits_rows(Context &c, float *dst, size_t row, int rows) {
+    G4_TRY(drain(c));
     hipStream_t s = c.stream;
+    float *residual = make_lane(c, c.last_lane).residual + row * G4_HIDDEN;
     if (order() == G4_ORDER_REFERENCE) {
-        launch_row_tail(s, nullptr, nullptr, c.residual + row * G4_HIDDEN, 1.0f, c.final_norm, nullptr,
-                        c.q8, c.qs, 1e-6f, rows, 0, 0, 1, 1);
+        launch_row_tail(s, nullptr, nullptr, residual, 1.0f, c.final_norm, nullptr, c.q8, c.qs, 1e-6f,
+                        rows, 0, 0, 1, 1);
     } else {
-        launch_rmsnorm(s, c.aux, c.residual + row * G4_HIDDEN, c.final_norm, G4_HIDDEN, 1e-6f, rows);
+        launch_rmsnorm(s, c.aux, residual, c.final_norm, G4_HIDDEN, 1e-6f, rows);
         launch_quantize(s, c.q8, c.qs, c.aux, (size_t)rows * G4_HIDDEN / 64);
     }
     G4_TRY(matmul(c, dst, G4_VOCAB, c.embed, rows));

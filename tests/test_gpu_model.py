@@ -248,6 +248,42 @@ def test_teacher_forced_dump_2388(pkg, model, image, oracle_lib):
     cpu.close()
 
 
+def test_pipelined_passes_match_drained_passes(pkg, model, image):
+    """Consecutive passes of more than 8 tokens over consecutive positions run
+    concurrently on two streams (the second's attention waiting for the
+    first's key/value rows layer by layer, the window rings long enough that
+    the two passes' rows never share a slot).  Their logits equal, bit for
+    bit, those of the same passes each finished before the next starts --
+    over 3622 tokens: the window rings wrap, a ragged pass (300 tokens) runs
+    beside a full one, and the global rings grow (from 4096 positions, after a
+    fresh g4_init) at the last pass, which first waits for the one in flight."""
+    model.g4_shutdown()
+    pkg.check(model.g4_init(image.records, 0))
+    tokens = rng(83).integers(0, pkg.VOCAB, 3622).astype(np.int32)
+    sizes = [512] * 6 + [300, 250]
+    keep = {2: 512, 6: 300, 7: 250}
+
+    def logits_all(n):
+        out = np.empty((n, pkg.VOCAB), np.float32)
+        pkg.check(model.g4_logits_all(out.ctypes.data))
+        return out
+
+    pipelined, pos = {}, 0
+    for i, size in enumerate(sizes):
+        gpu_forward(pkg, model, tokens[pos:pos + size], pos)
+        pos += size
+        if i in keep:  # reading results waits for both streams
+            pipelined[i] = logits_all(size)
+    pos = 0
+    for i, size in enumerate(sizes):
+        gpu_forward(pkg, model, tokens[pos:pos + size], pos)
+        pos += size
+        if i in keep:
+            assert np.array_equal(logits_all(size), pipelined[i]), i
+        else:
+            gpu_argmax(pkg, model, 0)  # waits for the pass
+
+
 def test_logits_all_matches_rows(pkg, model):
     tokens = rng(61).integers(0, pkg.VOCAB, 24).astype(np.int32)
     gpu_forward(pkg, model, tokens, 0)
