@@ -106,7 +106,8 @@ def test_matmul_row_counts_bitexact(pkg, g4lib, torch_gpu, ok, rows):
 # Prefill products of a layer: grids of up to 256 blocks take 8-wave blocks,
 # larger ones 4-wave blocks (launch_matmul).
 @pytest.mark.parametrize("rows,n,k", [(512, 256, 1536), (512, 2048, 1536), (200, 1536, 6144),
-                                      (64, 1536, 12288), (1000, 512, 1536)])
+                                      (64, 1536, 12288), (1000, 512, 1536), (512, 1536, 2048),
+                                      (300, 1536, 4096)])
 def test_matmul_prefill_shapes_bitexact(pkg, g4lib, torch_gpu, ok, rows, n, k):
     g = rng(rows * 7 + n + k)
     w, s = random_weight(g, n, k)
