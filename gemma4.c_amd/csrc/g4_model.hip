@@ -42,20 +42,28 @@ struct Layer {
     float layer_scalar;
 };
 
+// Many-token passes in flight at once (struct Lane).
+constexpr int kLanes = 3;
+
+// The activation buffers of a lane beyond the first.
+struct LaneBuffers {
+    hipStream_t stream = nullptr;
+    float *residual = nullptr, *hidden = nullptr, *aux = nullptr, *ple = nullptr;
+    float *k_new = nullptr, *v_new = nullptr, *qs = nullptr, *qsb = nullptr;
+    int8_t *q8 = nullptr, *q8b = nullptr;
+    int *tokens_dev = nullptr, *tokens_pinned = nullptr;
+};
+
 struct Context {
     bool ready = false;
     int device = 0;
     hipStream_t stream = nullptr;
-    // Lane 1 (struct Lane): the second stream of consecutive many-token passes
-    // and its own activation buffers; kv_written[lane][l] is recorded once a
-    // lane's pass has written layer l's key/value rows.
-    hipStream_t lane_stream = nullptr;
-    hipEvent_t kv_written[2][15] = {};
-    float *residual1 = nullptr, *hidden1 = nullptr, *aux1 = nullptr, *ple1 = nullptr;
-    float *k_new1 = nullptr, *v_new1 = nullptr, *qs1 = nullptr, *qsb1 = nullptr;
-    int8_t *q81 = nullptr, *q8b1 = nullptr;
-    int *tokens_dev1 = nullptr, *tokens_pinned1 = nullptr;
-    void *lane_attn[2] = {};  // each lane's attention scratch (lane_attn_bytes each)
+    // Lanes 1 .. kLanes - 1 (struct Lane): the streams and activation buffers
+    // of the passes that run beside lane 0's; kv_written[lane][l] is recorded
+    // once a lane's pass has written layer l's key/value rows.
+    LaneBuffers extra[kLanes - 1];
+    hipEvent_t kv_written[kLanes][15] = {};
+    void *lane_attn[kLanes] = {};  // each lane's attention scratch (lane_attn_bytes each)
     size_t lane_attn_bytes = 0;
     int pending = -1;    // the lane whose last pass may still run (-1: none)
     int next_pos = 0;    // the position after that pass
@@ -94,13 +102,13 @@ static Context g_ctx;
 // Initial positions of a global-attention ring (a power of two).
 constexpr int kGlobalStart = 4096;
 // Positions of a sliding-window ring: a pass of G4_BATCH tokens reads the
-// G4_WINDOW - 1 positions before it, and the pass after it may write its own
-// G4_BATCH positions meanwhile (the two run concurrently, struct Lane), so
-// 2 * G4_BATCH + G4_WINDOW - 1 positions must not share a slot (rounded up to a
-// power of two for the ring mask).
+// G4_WINDOW - 1 positions before it, and the kLanes - 1 passes after it may
+// write their own G4_BATCH positions meanwhile (they run concurrently, struct
+// Lane), so kLanes * G4_BATCH + G4_WINDOW - 1 positions must not share a slot
+// (rounded up to a power of two for the ring mask).
 constexpr int kWindowRing = 2048;
-static_assert(kWindowRing >= 2 * G4_BATCH + G4_WINDOW - 1 && (kWindowRing & (kWindowRing - 1)) == 0,
-              "sliding ring too short for two passes in flight");
+static_assert(kWindowRing >= kLanes * G4_BATCH + G4_WINDOW - 1 && (kWindowRing & (kWindowRing - 1)) == 0,
+              "sliding ring too short for the passes in flight");
 
 static size_t record_bytes(const g4_tensor &t, int index, size_t *scale_bytes) {
     *scale_bytes = 0;
@@ -121,7 +129,8 @@ static void release(void *p) {
 }
 
 static void free_all(Context &c) {
-    if (c.lane_stream) (void)hipStreamSynchronize(c.lane_stream);
+    for (LaneBuffers &b : c.extra)
+        if (b.stream) (void)hipStreamSynchronize(b.stream);
     if (c.stream) (void)hipStreamSynchronize(c.stream);
     for (void *p : c.lane_attn) release(p);
     release(c.arena);
@@ -145,16 +154,17 @@ static void free_all(Context &c) {
     if (c.tokens_pinned) (void)hipHostFree(c.tokens_pinned);
     if (c.pos_pinned) (void)hipHostFree(c.pos_pinned);
     if (c.decode_graph) (void)hipGraphExecDestroy(c.decode_graph);
-    if (c.lane_stream) (void)hipStreamSynchronize(c.lane_stream);
     for (auto &lane : c.kv_written)
         for (hipEvent_t e : lane)
             if (e) (void)hipEventDestroy(e);
-    if (c.lane_stream) (void)hipStreamDestroy(c.lane_stream);
-    for (float *p : {c.residual1, c.hidden1, c.aux1, c.ple1, c.k_new1, c.v_new1, c.qs1, c.qsb1}) release(p);
-    release(c.q81);
-    release(c.q8b1);
-    release(c.tokens_dev1);
-    if (c.tokens_pinned1) (void)hipHostFree(c.tokens_pinned1);
+    for (LaneBuffers &b : c.extra) {
+        if (b.stream) (void)hipStreamDestroy(b.stream);
+        for (float *p : {b.residual, b.hidden, b.aux, b.ple, b.k_new, b.v_new, b.qs, b.qsb}) release(p);
+        release(b.q8);
+        release(b.q8b);
+        release(b.tokens_dev);
+        if (b.tokens_pinned) (void)hipHostFree(b.tokens_pinned);
+    }
     if (c.stream) (void)hipStreamDestroy(c.stream);
     scratch_release();  // the model's reservation (and anything per-op calls grew)
     layer_buffers_release();
@@ -235,7 +245,7 @@ static int init(const g4_tensor *records, int device) {
     c.device = device;
     G4_HIP(hipSetDevice(device));
     G4_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
-    G4_HIP(hipStreamCreateWithFlags(&c.lane_stream, hipStreamNonBlocking));
+    for (LaneBuffers &b : c.extra) G4_HIP(hipStreamCreateWithFlags(&b.stream, hipStreamNonBlocking));
     for (auto &lane : c.kv_written)
         for (hipEvent_t &e : lane) G4_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
 
@@ -348,19 +358,21 @@ static int init(const g4_tensor *records, int device) {
     // captured decode step never needs a larger buffer.
     G4_TRY(scratch_reserve((size_t)G4_VOCAB * (G4_HIDDEN / 64) * sizeof(int32_t),
                            (size_t)G4_MAX_CONTEXT * 8 * sizeof(float)));
-    // lane 1's buffers (struct Lane)
-    G4_HIP(hipMalloc(&c.residual1, (size_t)G4_BATCH * G4_HIDDEN * sizeof(float)));
-    G4_HIP(hipMalloc(&c.hidden1, wide * sizeof(float)));
-    G4_HIP(hipMalloc(&c.aux1, wide * sizeof(float)));
-    G4_HIP(hipMalloc(&c.ple1, (size_t)G4_BATCH * G4_LAYERS * G4_PLE * sizeof(float)));
-    G4_HIP(hipMalloc(&c.k_new1, (size_t)G4_BATCH * 512 * sizeof(float)));
-    G4_HIP(hipMalloc(&c.v_new1, (size_t)G4_BATCH * 512 * sizeof(float)));
-    G4_HIP(hipMalloc(&c.q81, wide));
-    G4_HIP(hipMalloc(&c.qs1, wide / 64 * sizeof(float)));
-    G4_HIP(hipMalloc(&c.q8b1, wide));
-    G4_HIP(hipMalloc(&c.qsb1, wide / 64 * sizeof(float)));
-    G4_HIP(hipMalloc(&c.tokens_dev1, G4_BATCH * sizeof(int)));
-    G4_HIP(hipHostMalloc((void **)&c.tokens_pinned1, G4_BATCH * sizeof(int), hipHostMallocDefault));
+    // the other lanes' buffers (struct Lane)
+    for (LaneBuffers &b : c.extra) {
+        G4_HIP(hipMalloc(&b.residual, (size_t)G4_BATCH * G4_HIDDEN * sizeof(float)));
+        G4_HIP(hipMalloc(&b.hidden, wide * sizeof(float)));
+        G4_HIP(hipMalloc(&b.aux, wide * sizeof(float)));
+        G4_HIP(hipMalloc(&b.ple, (size_t)G4_BATCH * G4_LAYERS * G4_PLE * sizeof(float)));
+        G4_HIP(hipMalloc(&b.k_new, (size_t)G4_BATCH * 512 * sizeof(float)));
+        G4_HIP(hipMalloc(&b.v_new, (size_t)G4_BATCH * 512 * sizeof(float)));
+        G4_HIP(hipMalloc(&b.q8, wide));
+        G4_HIP(hipMalloc(&b.qs, wide / 64 * sizeof(float)));
+        G4_HIP(hipMalloc(&b.q8b, wide));
+        G4_HIP(hipMalloc(&b.qsb, wide / 64 * sizeof(float)));
+        G4_HIP(hipMalloc(&b.tokens_dev, G4_BATCH * sizeof(int)));
+        G4_HIP(hipHostMalloc((void **)&b.tokens_pinned, G4_BATCH * sizeof(int), hipHostMallocDefault));
+    }
     G4_HIP(hipDeviceSynchronize());
     c.ready = true;
     return G4_OK;
@@ -374,14 +386,15 @@ static int matmul(Context &c, float *out, size_t stride, const Weight &w, int ro
 
 // A stream and the activation buffers one forward pass runs on.  Lane 0 is
 // c.stream with the context's first set of buffers (every one-token step and
-// every other entry point uses it); lane 1 is c.lane_stream with the second
-// set.  Consecutive many-token passes over consecutive positions (the chunks
-// of a long prefill, gemma4.c:563-566) alternate lanes and run concurrently:
-// a pass's attention at layer l reads the key/value rows the pass before it
-// wrote at layer l, so it waits for them (wait_kv[l]), and its own rows are
-// announced to the pass after it (record_kv[l]).  Every other op is local to
-// the pass's rows.  The window rings are long enough that the two passes'
-// rows never share a slot (kWindowRing).
+// every other entry point uses it); lanes 1 .. kLanes - 1 have their own
+// streams and sets (c.extra).  Consecutive many-token passes over consecutive
+// positions (the chunks of a long prefill, gemma4.c:563-566) take the lanes
+// in turn and run concurrently: a pass's attention at layer l reads the
+// key/value rows the passes before it wrote at layer l, so it waits for the
+// previous pass's event (wait_kv[l]) and then records its own (record_kv[l]),
+// which thereby covers every earlier pass too.  Every other op is local to
+// the pass's rows.  The window rings are long enough that the passes in
+// flight never share a slot (kWindowRing).
 struct Lane {
     hipStream_t stream = nullptr;
     float *residual = nullptr, *hidden = nullptr, *aux = nullptr, *ple = nullptr;
@@ -403,11 +416,12 @@ static Lane make_lane(Context &c, int index) {
         ln.q8 = c.q8, ln.q8b = c.q8b, ln.qs = c.qs, ln.qsb = c.qsb;
         ln.tokens_dev = c.tokens_dev, ln.tokens_pinned = c.tokens_pinned;
     } else {
-        ln.stream = c.lane_stream;
-        ln.residual = c.residual1, ln.hidden = c.hidden1, ln.aux = c.aux1, ln.ple = c.ple1;
-        ln.k_new = c.k_new1, ln.v_new = c.v_new1;
-        ln.q8 = c.q81, ln.q8b = c.q8b1, ln.qs = c.qs1, ln.qsb = c.qsb1;
-        ln.tokens_dev = c.tokens_dev1, ln.tokens_pinned = c.tokens_pinned1;
+        const LaneBuffers &b = c.extra[index - 1];
+        ln.stream = b.stream;
+        ln.residual = b.residual, ln.hidden = b.hidden, ln.aux = b.aux, ln.ple = b.ple;
+        ln.k_new = b.k_new, ln.v_new = b.v_new;
+        ln.q8 = b.q8, ln.q8b = b.q8b, ln.qs = b.qs, ln.qsb = b.qsb;
+        ln.tokens_dev = b.tokens_dev, ln.tokens_pinned = b.tokens_pinned;
     }
     return ln;
 }
@@ -416,7 +430,7 @@ static Lane make_lane(Context &c, int index) {
 static int drain(Context &c) {
     if (c.pending < 0) return G4_OK;
     c.pending = -1;
-    G4_HIP(hipStreamSynchronize(c.lane_stream));
+    for (LaneBuffers &b : c.extra) G4_HIP(hipStreamSynchronize(b.stream));
     G4_HIP(hipStreamSynchronize(c.stream));
     return G4_OK;
 }
@@ -533,8 +547,10 @@ static int enqueue_forward(Context &c, const Lane &ln, int n, int start_pos, con
                 launch_kv_finish(s, keys, values, ln.k_new, ln.v_new, L.k_norm, L.rope_cos, L.rope_sin,
                                  L.pairs, hd, cache_len, start_pos, pos_dev, n);
         }
-        if (L.k.data && ln.record_kv) G4_HIP(hipEventRecord(ln.record_kv[l], s));
+        // after the wait: the event then also stands for every earlier pass's
+        // rows of this layer (a pass two back is on another stream)
         if (L.k.data && ln.wait_kv) G4_HIP(hipStreamWaitEvent(s, ln.wait_kv[l], 0));
+        if (L.k.data && ln.record_kv) G4_HIP(hipEventRecord(ln.record_kv[l], s));
         G4_TRY(launch_attend(s, ln.hidden, ln.aux, keys, values, cache_len, hd, heads, L.full,
                              start_pos, pos_dev, n, ln.q8, ln.qs, ln.attn_scratch));
         G4_TRY(matmul(ln.hidden, G4_HIDDEN, L.o, n));
@@ -756,13 +772,13 @@ static int forward(Context &c, const int *tokens, int n, int start_pos) {
     G4_TRY(reserve_lane_attn(c, attend_scratch_bytes(G4_BATCH, last_pos)));
     const bool follow = c.pending >= 0 && start_pos == c.next_pos;
     if (!follow) G4_TRY(drain(c));
-    const int lane = follow ? c.pending ^ 1 : 0;
+    const int lane = follow ? (c.pending + 1) % kLanes : 0;
     Lane ln = make_lane(c, lane);
     G4_HIP(hipStreamSynchronize(ln.stream));  // the lane's previous pass: its buffers are free
     const FixedScratch attn{c.lane_attn[lane], c.lane_attn_bytes};
     ln.attn_scratch = &attn;
     ln.record_kv = c.kv_written[lane];
-    ln.wait_kv = follow ? c.kv_written[lane ^ 1] : nullptr;
+    ln.wait_kv = follow ? c.kv_written[c.pending] : nullptr;
     memcpy(ln.tokens_pinned, tokens, (size_t)n * sizeof(int));
     G4_HIP(hipMemcpyAsync(ln.tokens_dev, ln.tokens_pinned, (size_t)n * sizeof(int), hipMemcpyHostToDevice,
                           ln.stream));
