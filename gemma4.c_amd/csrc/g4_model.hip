@@ -43,7 +43,7 @@ struct Layer {
 };
 
 // Many-token passes in flight at once (struct Lane).
-constexpr int kLanes = 3;
+constexpr int kLanes = 4;
 
 // The activation buffers of a lane beyond the first.
 struct LaneBuffers {
@@ -106,7 +106,7 @@ constexpr int kGlobalStart = 4096;
 // write their own G4_BATCH positions meanwhile (they run concurrently, struct
 // Lane), so kLanes * G4_BATCH + G4_WINDOW - 1 positions must not share a slot
 // (rounded up to a power of two for the ring mask).
-constexpr int kWindowRing = 2048;
+constexpr int kWindowRing = 4096;
 static_assert(kWindowRing >= kLanes * G4_BATCH + G4_WINDOW - 1 && (kWindowRing & (kWindowRing - 1)) == 0,
               "sliding ring too short for the passes in flight");
 

@@ -74,8 +74,9 @@ int g4_init(const g4_tensor *records, int device);
  * before the call returns.  A pass of more than 8 tokens may still be running
  * on the device when it returns: the next pass, if it starts where this one
  * ended (the reference's prefill chunks, gemma4.c:563-566), runs concurrently
- * with it, and every other entry point below waits for both first.  Shorter
- * passes (decode steps) return finished. */
+ * with it (up to four passes at once), and every other entry point below
+ * waits for all of them first.  Shorter passes (decode steps) return
+ * finished. */
 int g4_forward(const int *tokens, size_t token_count, int start_pos);
 
 /* Replaces logits() (gemma4.c:512): final norm, tied lm_head and soft cap for
@@ -107,9 +108,9 @@ int g4_sample(size_t token, float temperature, uint64_t *rng_state, int *out_tok
 void g4_shutdown(void);
 
 /* The library's HIP stream (a hipStream_t) for timing with HIP events: the
- * stream of every entry point here except the concurrent second of two
- * consecutive many-token passes (g4_forward), which runs on a second stream;
- * the next g4_logits / g4_argmax / g4_sample / one-token g4_forward joins it. */
+ * stream of every entry point here, except that consecutive many-token passes
+ * (g4_forward) take this and three more streams in turn; the next
+ * g4_logits / g4_argmax / g4_sample / one-token g4_forward waits for all. */
 void *g4_stream(void);
 
 /* Summation order of rmsnorm and attention, for every later call (model and
