@@ -4,7 +4,7 @@
 // Weights are uploaded once into one HBM arena in the exporter's packed layout
 // (the same bytes as the .bin); the fp32 KV rings (3 global owners x 512
 // channels, growing from 4096 to at most 131072 positions with the context;
-// 12 sliding owners x 2048 x 256; keys then values) and every activation live
+// 12 sliding owners x 4096 x 256; keys then values) and every activation live
 // on the device, so a token step moves only token ids in and one logits row
 // (or one sampled token) out.
 #include <stdarg.h>

@@ -103,10 +103,10 @@ def test_prefill_512_and_128_greedy_steps(pkg, model, image, oracle_lib):
 
 
 def test_long_prefill_ring_wrap(pkg, model, image, oracle_lib):
-    """1100 tokens: the sliding rings wrap (positions >= 1024) and global
-    layers attend past 512; then 8 decode steps."""
+    """4200 tokens: the window rings wrap (positions >= 4096, their length)
+    and global layers attend past 512; then 8 decode steps."""
     cpu = oracle_lib.Model(image)
-    tokens = rng(59).integers(0, pkg.VOCAB, 1100).astype(np.int32)
+    tokens = rng(59).integers(0, pkg.VOCAB, 4200).astype(np.int32)
     row = prefill(pkg, model, cpu, tokens)
     for r in (0, 37, row):
         err = float(np.abs(gpu_logits(pkg, model, r) - cpu.logits(r)).max())
@@ -250,18 +250,19 @@ def test_teacher_forced_dump_2388(pkg, model, image, oracle_lib):
 
 def test_pipelined_passes_match_drained_passes(pkg, model, image):
     """Consecutive passes of more than 8 tokens over consecutive positions run
-    concurrently on two streams (the second's attention waiting for the
-    first's key/value rows layer by layer, the window rings long enough that
-    the two passes' rows never share a slot).  Their logits equal, bit for
-    bit, those of the same passes each finished before the next starts --
-    over 3622 tokens: the window rings wrap, a ragged pass (300 tokens) runs
-    beside a full one, and the global rings grow (from 4096 positions, after a
-    fresh g4_init) at the last pass, which first waits for the one in flight."""
+    concurrently on up to four streams (each pass's attention waiting for the
+    previous pass's key/value rows layer by layer, the window rings long
+    enough that the passes in flight never share a slot).  Their logits
+    equal, bit for bit, those of the same passes each finished before the
+    next starts -- over 4646 tokens: the window rings (4096 slots) wrap in
+    the ragged last two passes (300 and 250 tokens), and the global rings
+    grow (from 4096 positions, after a fresh g4_init) at pass 7, which first
+    waits for the passes in flight."""
     model.g4_shutdown()
     pkg.check(model.g4_init(image.records, 0))
-    tokens = rng(83).integers(0, pkg.VOCAB, 3622).astype(np.int32)
-    sizes = [512] * 6 + [300, 250]
-    keep = {2: 512, 6: 300, 7: 250}
+    tokens = rng(83).integers(0, pkg.VOCAB, 4646).astype(np.int32)
+    sizes = [512] * 8 + [300, 250]
+    keep = {2: 512, 8: 300, 9: 250}
 
     def logits_all(n):
         out = np.empty((n, pkg.VOCAB), np.float32)
@@ -272,7 +273,7 @@ def test_pipelined_passes_match_drained_passes(pkg, model, image):
     for i, size in enumerate(sizes):
         gpu_forward(pkg, model, tokens[pos:pos + size], pos)
         pos += size
-        if i in keep:  # reading results waits for both streams
+        if i in keep:  # reading results waits for every stream
             pipelined[i] = logits_all(size)
     pos = 0
     for i, size in enumerate(sizes):
