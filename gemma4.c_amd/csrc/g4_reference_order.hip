@@ -1747,6 +1747,168 @@ __global__ __launch_bounds__(QUANT ? 256 : 64) void k_attn_values_decode(float *
     }
 }
 
+// k_attn_values_decode over a global layer (FULL, fp32 out) with the tile
+// staging on a second wave.  Wave 1 (the producer, on another SIMD) loads the
+// 64-key V tiles of its 16 channels DEPTH tiles ahead in registers and
+// writes each, transposed and permuted as above, into LDS slot tile & 1;
+// wave 0 (the chain) only reads each tile's column and runs its 64 DPP fmas,
+// so the staging no longer takes the chain's issue slots.  One barrier a
+// tile: before barrier u the producer has written tile u + 1, and the chain
+// has waited for its reads of tile u (it reads tile u during the chain of
+// tile u - 1); after it the chain reads tile u + 1 while it runs tile u,
+// and the producer overwrites tile u's slot with tile u + 2.  Both waves pass
+// the same 1 + tiles barriers.
+constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0), vmcnt and expcnt untouched
+
+template <int HD, int DEPTH>
+__global__ __launch_bounds__(128) void k_attn_values_decode_pc(float *__restrict__ out,
+                                                               const float *__restrict__ probs,
+                                                               const float *__restrict__ value_cache,
+                                                               int cache_len, int start_pos,
+                                                               const int *__restrict__ pos_dev,
+                                                               size_t stride) {
+    __shared__ __attribute__((aligned(16))) float s_v[2][16][68];  // [slot][channel][position]
+    if (pos_dev) start_pos = *pos_dev;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, r = lane >> 4, j = lane & 15;
+    const int c0 = blockIdx.x * 16, t = blockIdx.z;
+    const int pos = start_pos + t, keys = pos + 1, tiles = (keys + 63) / 64;
+    constexpr uint32_t ROW = HD * 4, TILE = 64 * ROW;  // bytes
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    auto load16 = [](__amdgpu_buffer_rsrc_t d, uint32_t offset) __attribute__((always_inline)) {
+        return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(d, offset, 0, 0));
+    };
+    static_assert(DEPTH == 8, "the steps below are written out for 8 ring slots");
+    if (wave == 1) {
+        // V loads: lane (kq, cc) takes keys 4 kq .. 4 kq + 3 of channels
+        // c0 + 4 cc .. + 3; the descriptor ends at row `keys`, so rows past
+        // the end (and whole tiles past the last) read as 0
+        const int kq = lane >> 2, cc = lane & 3;
+        const uint32_t chan = (uint32_t)(c0 + 4 * cc) * 4;
+        const int v_rows = min(keys, cache_len);
+        const __amdgpu_buffer_rsrc_t v_desc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(value_cache), 0, (int)((uint32_t)v_rows * ROW), 0x00020000);
+        struct VTile {
+            f4 v[4];
+        };
+        auto load_v = [&](int tile, VTile &st) __attribute__((always_inline)) {
+            const uint32_t base = (uint32_t)(4 * kq) * ROW + chan + (uint32_t)tile * TILE;
+#pragma unroll
+            for (int i = 0; i < 4; i++) st.v[i] = load16(v_desc, base + i * ROW);
+        };
+        auto store_v = [&](int slot, const VTile &st) __attribute__((always_inline)) {
+            float *row = &s_v[slot][4 * cc][kq];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) row[e * 68 + 16 * i] = st.v[i][e];
+        };
+        VTile ring[DEPTH];  // tile u in ring[u % DEPTH]
+#pragma unroll
+        for (int s = 0; s < DEPTH; s++) load_v(s, ring[s]);
+        store_v(0, ring[0]);
+        load_v(DEPTH, ring[0]);
+        __syncthreads();
+        // step u: tile u + 1 into slot (u + 1) & 1, its ring slot refilled
+        // with tile u + 1 + DEPTH
+        auto step = [&](int u, VTile &next) __attribute__((always_inline)) {
+            store_v((u + 1) & 1, next);
+            load_v(u + 1 + DEPTH, next);
+            __syncthreads();
+        };
+        for (int u = 0; u < tiles; u += DEPTH) {
+            step(u + 0, ring[1]);
+            if (u + 1 >= tiles) break;
+            step(u + 1, ring[2]);
+            if (u + 2 >= tiles) break;
+            step(u + 2, ring[3]);
+            if (u + 3 >= tiles) break;
+            step(u + 3, ring[4]);
+            if (u + 4 >= tiles) break;
+            step(u + 4, ring[5]);
+            if (u + 5 >= tiles) break;
+            step(u + 5, ring[6]);
+            if (u + 6 >= tiles) break;
+            step(u + 6, ring[7]);
+            if (u + 7 >= tiles) break;
+            step(u + 7, ring[0]);
+        }
+        return;
+    }
+    // the chain: probabilities of heads 4 y .. 4 y + 3 (rows `stride` floats
+    // apart), up to the last tile of the fourth, DEPTH tiles ahead
+    const float *prows = probs + ((size_t)t * 8 + 4 * blockIdx.y) * stride;
+    const __amdgpu_buffer_rsrc_t p_desc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(prows), 0, (int)((3 * stride + (size_t)tiles * 64) * 4), 0x00020000);
+    const uint32_t p_lane = (uint32_t)((r * stride + 4 * j) * 4);
+    auto load_p = [&](int tile) __attribute__((always_inline)) {
+        return load16(p_desc, p_lane + (uint32_t)min(tile, tiles - 1) * 256);
+    };
+    float o = 0.0f;
+#define G4_PV_FMA(J, E, C) \
+    "v_fmac_f32_dpp %0, %" #E ", %" #C " row_newbcast:" #J " row_mask:0xf bank_mask:0xf\n"
+#define G4_PV_KEYS(J, A, B, C, D) G4_PV_FMA(J, 1, A) G4_PV_FMA(J, 2, B) G4_PV_FMA(J, 3, C) G4_PV_FMA(J, 4, D)
+#define G4_PV_COL(M) "v"(col[M].x), "v"(col[M].y), "v"(col[M].z), "v"(col[M].w)
+    auto chain64 = [&](const f4 (&col)[16], f4 p) __attribute__((always_inline)) {
+        asm volatile("s_nop 1\n"
+                     G4_PV_KEYS(0, 5, 21, 37, 53) G4_PV_KEYS(1, 6, 22, 38, 54)
+                     G4_PV_KEYS(2, 7, 23, 39, 55) G4_PV_KEYS(3, 8, 24, 40, 56)
+                     G4_PV_KEYS(4, 9, 25, 41, 57) G4_PV_KEYS(5, 10, 26, 42, 58)
+                     G4_PV_KEYS(6, 11, 27, 43, 59) G4_PV_KEYS(7, 12, 28, 44, 60)
+                     G4_PV_KEYS(8, 13, 29, 45, 61) G4_PV_KEYS(9, 14, 30, 46, 62)
+                     G4_PV_KEYS(10, 15, 31, 47, 63) G4_PV_KEYS(11, 16, 32, 48, 64)
+                     G4_PV_KEYS(12, 17, 33, 49, 65) G4_PV_KEYS(13, 18, 34, 50, 66)
+                     G4_PV_KEYS(14, 19, 35, 51, 67) G4_PV_KEYS(15, 20, 36, 52, 68)
+                     : "+v"(o)
+                     : "v"(p.x), "v"(p.y), "v"(p.z), "v"(p.w), G4_PV_COL(0), G4_PV_COL(1),
+                       G4_PV_COL(2), G4_PV_COL(3), G4_PV_COL(4), G4_PV_COL(5), G4_PV_COL(6),
+                       G4_PV_COL(7), G4_PV_COL(8), G4_PV_COL(9), G4_PV_COL(10), G4_PV_COL(11),
+                       G4_PV_COL(12), G4_PV_COL(13), G4_PV_COL(14), G4_PV_COL(15));
+    };
+#undef G4_PV_COL
+#undef G4_PV_KEYS
+#undef G4_PV_FMA
+    f4 p_ring[DEPTH];  // tile u's probabilities in p_ring[u % DEPTH]
+#pragma unroll
+    for (int s = 0; s < DEPTH; s++) p_ring[s] = load_p(s);
+    auto read_col = [&](int slot, f4 (&col)[16]) __attribute__((always_inline)) {
+        const f4 *src = reinterpret_cast<const f4 *>(&s_v[slot][j][0]);
+#pragma unroll
+        for (int i = 0; i < 16; i++) col[i] = src[i];
+    };
+    f4 col_a[16], col_b[16];  // tile u's column: col_a for even u, col_b for odd
+    __syncthreads();  // tile 0 is in slot 0
+    read_col(0, col_a);
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    // step u: after barrier u, read tile u + 1 while tile u's chain runs, then
+    // wait for those reads (before the next barrier)
+    auto step = [&](int u, const f4 (&cur)[16], f4 (&next)[16], f4 &p) __attribute__((always_inline)) {
+        __syncthreads();
+        read_col((u + 1) & 1, next);
+        chain64(cur, p);
+        p = load_p(u + DEPTH);
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    };
+    for (int u = 0; u < tiles; u += DEPTH) {
+        step(u + 0, col_a, col_b, p_ring[0]);
+        if (u + 1 >= tiles) break;
+        step(u + 1, col_b, col_a, p_ring[1]);
+        if (u + 2 >= tiles) break;
+        step(u + 2, col_a, col_b, p_ring[2]);
+        if (u + 3 >= tiles) break;
+        step(u + 3, col_b, col_a, p_ring[3]);
+        if (u + 4 >= tiles) break;
+        step(u + 4, col_a, col_b, p_ring[4]);
+        if (u + 5 >= tiles) break;
+        step(u + 5, col_b, col_a, p_ring[5]);
+        if (u + 6 >= tiles) break;
+        step(u + 6, col_a, col_b, p_ring[6]);
+        if (u + 7 >= tiles) break;
+        step(u + 7, col_b, col_a, p_ring[7]);
+    }
+    out[((size_t)t * 8 + 4 * blockIdx.y + r) * HD + c0 + j] = o;
+}
+
 int launch_attend_reference(hipStream_t s, float *out, const float *q, const float *key_cache,
                             const float *value_cache, int cache_len, int head_dim, int heads,
                             int full, int start_pos, const int *pos_dev, size_t n, int8_t *q8,
@@ -1830,13 +1992,18 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
         G4_PV_DECODE(HD, FULL, true); \
     else                          \
         G4_PV_DECODE(HD, FULL, false)
+        // a global layer: the staging on a second wave of each block
+#define G4_PV_DECODE_PC(HD)                                                                        \
+    hipLaunchKernelGGL((k_attn_values_decode_pc<HD, 8>), dim3((unsigned)(head_dim / 16), 2, nn),    \
+                       dim3(128), 0, s, out, scores, value_cache, cache_len, start_pos, pos_dev, stride)
         if (head_dim == 256) {
-            if (full) G4_PV_DECODE(256, true, false);
+            if (full) G4_PV_DECODE_PC(256);
             else G4_PV_DECODE_Q(256, false);
         } else {
-            if (full) G4_PV_DECODE(512, true, false);
+            if (full) G4_PV_DECODE_PC(512);
             else G4_PV_DECODE_Q(512, false);
         }
+#undef G4_PV_DECODE_PC
 #undef G4_PV_DECODE_Q
 #undef G4_PV_DECODE
         if (q8 && !fuse) launch_quantize(s, q8, qs, out, n * heads * head_dim / 64);
