@@ -239,7 +239,7 @@ int launch_attend(hipStream_t s, float *out, const float *q, const float *key_ca
                   int start_pos, const int *pos_dev, size_t n, int8_t *q8 = nullptr,
                   float *qs = nullptr, const FixedScratch *fixed = nullptr);
 // Scratch bytes launch_attend needs for n query rows (8 heads, head_dim <= 512)
-// whose last position is last_pos, in either order.
+// whose last position is last_pos, in the current summation order.
 size_t attend_scratch_bytes(size_t n, int last_pos);
 int launch_attend_parallel(hipStream_t s, float *out, const float *q, const float *key_cache,
                            const float *value_cache, int cache_len, int head_dim, int heads,

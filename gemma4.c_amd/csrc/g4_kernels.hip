@@ -1523,9 +1523,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(float *__restrict__ out,
 
 size_t attend_scratch_bytes(size_t n, int last_pos) {
     const size_t keys = (size_t)last_pos + 1, heads = 8;
-    const size_t scores = n * heads * ((keys + 63) & ~(size_t)63);               // reference order
-    const size_t partials = n * ((keys + kAttnChunk - 1) / kAttnChunk) * heads * (512 + 2);  // parallel
-    return (scores > partials ? scores : partials) * sizeof(float);
+    if (order() == G4_ORDER_REFERENCE) return n * heads * ((keys + 63) & ~(size_t)63) * sizeof(float);
+    return n * ((keys + kAttnChunk - 1) / kAttnChunk) * heads * (512 + 2) * sizeof(float);  // partials
 }
 
 int launch_attend_parallel(hipStream_t s, float *out, const float *q, const float *key_cache,
