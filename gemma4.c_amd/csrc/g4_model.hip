@@ -738,18 +738,22 @@ static int reserve_lane_attn(Context &c, size_t bytes) {
     return G4_OK;
 }
 
-// gemma4.c:463 for n tokens at start_pos.  A pass of more than 8 tokens is
-// enqueued and left running on a lane (struct Lane): when it continues the
-// pass before it (start_pos where that one ended) the two run concurrently;
-// every entry point that reads results, and any other pass, waits first
-// (drain).  At most one pass per lane is in flight.  Shorter passes (decode
-// steps) run on lane 0 and return finished.
+// gemma4.c:463 for n tokens at start_pos, enqueued and left running.  A
+// pass of more than 8 tokens runs on a lane (struct Lane): when it continues
+// the pass before it (start_pos where that one ended) the two run
+// concurrently; every entry point that reads results, and any other pass,
+// waits for the lanes first (drain).  At most one pass per lane is in
+// flight.  Shorter passes (decode steps) run on lane 0 (c.stream), where the
+// logits, argmax and sampling that read them follow in stream order.
 static int forward(Context &c, const int *tokens, int n, int start_pos) {
     const int last_pos = start_pos + n - 1;
     if (n <= 8) {  // their products take the split-K GEMV, whose scratch is shared
         G4_TRY(drain(c));
         G4_TRY(ensure_kv(c, last_pos));
         hipStream_t s = c.stream;
+        // the previous short pass's copies out of the pinned buffers are done
+        // (normally its logits already waited for the stream)
+        G4_HIP(hipStreamSynchronize(s));
         memcpy(c.tokens_pinned, tokens, (size_t)n * sizeof(int));
         G4_HIP(hipMemcpyAsync(c.tokens_dev, c.tokens_pinned, (size_t)n * sizeof(int),
                               hipMemcpyHostToDevice, s));
@@ -763,7 +767,8 @@ static int forward(Context &c, const int *tokens, int n, int start_pos) {
         } else {
             G4_TRY(enqueue_forward(c, make_lane(c, 0), n, start_pos, nullptr));
         }
-        G4_HIP(hipStreamSynchronize(s));
+        // left running: every entry point that reads its results runs on
+        // c.stream after it
         c.last_n = n;
         c.last_lane = 0;
         return G4_OK;
