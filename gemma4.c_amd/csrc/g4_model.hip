@@ -426,7 +426,7 @@ static Lane make_lane(Context &c, int index) {
     return ln;
 }
 
-// Wait for both lanes; afterwards lane 0's buffers and stream serve any call.
+// Wait for every lane; afterwards lane 0's buffers and stream serve any call.
 static int drain(Context &c) {
     if (c.pending < 0) return G4_OK;
     c.pending = -1;
@@ -724,7 +724,7 @@ static int ensure_kv(Context &c, int last_pos) {
     return G4_OK;
 }
 
-// Each lane's attention scratch, grown (both lanes drained first) to `bytes`.
+// Each lane's attention scratch, grown (every lane drained first) to `bytes`.
 static int reserve_lane_attn(Context &c, size_t bytes) {
     if (bytes <= c.lane_attn_bytes) return G4_OK;
     G4_TRY(drain(c));
@@ -738,22 +738,18 @@ static int reserve_lane_attn(Context &c, size_t bytes) {
     return G4_OK;
 }
 
-// gemma4.c:463 for n tokens at start_pos, enqueued and left running.  A
-// pass of more than 8 tokens runs on a lane (struct Lane): when it continues
-// the pass before it (start_pos where that one ended) the two run
-// concurrently; every entry point that reads results, and any other pass,
-// waits for the lanes first (drain).  At most one pass per lane is in
-// flight.  Shorter passes (decode steps) run on lane 0 (c.stream), where the
-// logits, argmax and sampling that read them follow in stream order.
+// gemma4.c:463 for n tokens at start_pos.  A pass of more than 8 tokens is
+// enqueued and left running on a lane (struct Lane): when it continues the
+// pass before it (start_pos where that one ended) the two run concurrently;
+// every entry point that reads results, and any other pass, waits for the
+// lanes first (drain).  At most one pass per lane is in flight.  Shorter
+// passes (decode steps) run on lane 0 and return finished.
 static int forward(Context &c, const int *tokens, int n, int start_pos) {
     const int last_pos = start_pos + n - 1;
     if (n <= 8) {  // their products take the split-K GEMV, whose scratch is shared
         G4_TRY(drain(c));
         G4_TRY(ensure_kv(c, last_pos));
         hipStream_t s = c.stream;
-        // the previous short pass's copies out of the pinned buffers are done
-        // (normally its logits already waited for the stream)
-        G4_HIP(hipStreamSynchronize(s));
         memcpy(c.tokens_pinned, tokens, (size_t)n * sizeof(int));
         G4_HIP(hipMemcpyAsync(c.tokens_dev, c.tokens_pinned, (size_t)n * sizeof(int),
                               hipMemcpyHostToDevice, s));
@@ -767,8 +763,10 @@ static int forward(Context &c, const int *tokens, int n, int start_pos) {
         } else {
             G4_TRY(enqueue_forward(c, make_lane(c, 0), n, start_pos, nullptr));
         }
-        // left running: every entry point that reads its results runs on
-        // c.stream after it
+        // finished before returning: these passes use the library's shared
+        // scratch (split-K dots, one-token attention rows), which the per-op
+        // entry points also use, on the caller's streams
+        G4_HIP(hipStreamSynchronize(s));
         c.last_n = n;
         c.last_lane = 0;
         return G4_OK;
@@ -804,7 +802,7 @@ static int forward(Context &c, const int *tokens, int n, int start_pos) {
 
 // gemma4.c:512-522 for `rows` consecutive rows starting at `row`, into dst.
 // The rows are the last pass's (on its lane); the work runs on lane 0 once
-// both lanes have finished.
+// every lane has finished.
 static int logits_rows(Context &c, float *dst, size_t row, int rows) {
     G4_TRY(drain(c));
     hipStream_t s = c.stream;

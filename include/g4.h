@@ -71,12 +71,12 @@ int g4_init(const g4_tensor *records, int device);
 /* Replaces forward() (gemma4.c:463): runs token_count (1..G4_BATCH) tokens at
  * positions start_pos.. through all 35 layers, updating the device KV caches.
  * Requires start_pos + token_count <= G4_MAX_CONTEXT.  `tokens` is copied
- * before the call returns, but the pass may still be running on the device:
- * the entry points below see its results (they run after it).  A pass of
- * more than 8 tokens that starts where the previous one ended (the
- * reference's prefill chunks, gemma4.c:563-566) runs concurrently with it (up
- * to four passes at once); the entry points below wait for all of them.
- * Errors the device raises during a pass surface at a later call. */
+ * before the call returns.  A pass of more than 8 tokens may still be running
+ * on the device when it returns: the next pass, if it starts where this one
+ * ended (the reference's prefill chunks, gemma4.c:563-566), runs concurrently
+ * with it (up to four passes at once), and every other entry point below
+ * waits for all of them first; errors the device raises in such a pass
+ * surface at a later call.  Shorter passes (decode steps) return finished. */
 int g4_forward(const int *tokens, size_t token_count, int start_pos);
 
 /* Replaces logits() (gemma4.c:512): final norm, tied lm_head and soft cap for
