@@ -248,11 +248,13 @@ def test_teacher_forced_dump_2388(pkg, model, image, oracle_lib):
     cpu.close()
 
 
-def test_pipelined_passes_match_drained_passes(pkg, model, image):
-    """Consecutive passes of more than 8 tokens over consecutive positions run
-    concurrently on up to four streams (each pass's attention waiting for the
-    previous pass's key/value rows layer by layer, the window rings long
-    enough that the passes in flight never share a slot).  Their logits
+@pytest.mark.parametrize("order_name", ["ORDER_REFERENCE", "ORDER_PARALLEL"])
+def test_pipelined_passes_match_drained_passes(pkg, model, image, order_name):
+    """In either summation order (each sizes the lanes' attention scratch
+    its own way): consecutive passes of more than 8 tokens over consecutive
+    positions run concurrently on up to four streams (each pass's attention
+    waiting for the previous pass's key/value rows layer by layer, the window
+    rings long enough that the passes in flight never share a slot).  Their logits
     equal, bit for bit, those of the same passes each finished before the
     next starts -- over 4646 tokens: the window rings (4096 slots) wrap in
     the ragged last two passes (300 and 250 tokens), and the global rings
@@ -260,6 +262,7 @@ def test_pipelined_passes_match_drained_passes(pkg, model, image):
     waits for the passes in flight."""
     model.g4_shutdown()
     pkg.check(model.g4_init(image.records, 0))
+    previous = model.g4_set_order(getattr(pkg, order_name))
     tokens = rng(83).integers(0, pkg.VOCAB, 4646).astype(np.int32)
     sizes = [512] * 8 + [300, 250]
     keep = {2: 512, 8: 300, 9: 250}
@@ -280,9 +283,10 @@ def test_pipelined_passes_match_drained_passes(pkg, model, image):
         gpu_forward(pkg, model, tokens[pos:pos + size], pos)
         pos += size
         if i in keep:
-            assert np.array_equal(logits_all(size), pipelined[i]), i
+            assert np.array_equal(logits_all(size), pipelined[i]), (order_name, i)
         else:
             gpu_argmax(pkg, model, 0)  # waits for the pass
+    model.g4_set_order(previous)
 
 
 def test_logits_all_matches_rows(pkg, model):
