@@ -84,6 +84,7 @@ struct Context {
     int *tokens_dev = nullptr, *argmax_dev = nullptr;
     int *tokens_pinned = nullptr;
     int *pos_dev = nullptr, *pos_pinned = nullptr;
+    float *logits_pinned = nullptr;  // one logits row: the copy out is a direct DMA
     int last_n = 0;
     // One-token steps replay a captured graph of the whole forward pass; the
     // position is read from pos_dev.  Recaptured when the scratch buffers move
@@ -153,6 +154,7 @@ static void free_all(Context &c) {
     release(c.pos_dev);
     if (c.tokens_pinned) (void)hipHostFree(c.tokens_pinned);
     if (c.pos_pinned) (void)hipHostFree(c.pos_pinned);
+    if (c.logits_pinned) (void)hipHostFree(c.logits_pinned);
     if (c.decode_graph) (void)hipGraphExecDestroy(c.decode_graph);
     for (auto &lane : c.kv_written)
         for (hipEvent_t e : lane)
@@ -353,6 +355,7 @@ static int init(const g4_tensor *records, int device) {
     G4_HIP(hipHostMalloc((void **)&c.tokens_pinned, G4_BATCH * sizeof(int), hipHostMallocDefault));
     G4_HIP(hipMalloc(&c.pos_dev, sizeof(int)));
     G4_HIP(hipHostMalloc((void **)&c.pos_pinned, sizeof(int), hipHostMallocDefault));
+    G4_HIP(hipHostMalloc((void **)&c.logits_pinned, G4_VOCAB * sizeof(float), hipHostMallocDefault));
     // Split-K scratch for the widest few-row product (1536 x 12288), and the
     // one-token attention scratch at full context (8 score rows), so that a
     // captured decode step never needs a larger buffer.
@@ -863,8 +866,10 @@ extern "C" int g4_logits(size_t token, float *out) {
              c.last_n);
     G4_HIP(hipSetDevice(c.device));
     G4_TRY(logits_rows(c, c.logits, token, 1));
-    G4_HIP(hipMemcpyAsync(out, c.logits, G4_VOCAB * sizeof(float), hipMemcpyDeviceToHost, c.stream));
+    G4_HIP(hipMemcpyAsync(c.logits_pinned, c.logits, G4_VOCAB * sizeof(float), hipMemcpyDeviceToHost,
+                          c.stream));
     G4_HIP(hipStreamSynchronize(c.stream));
+    memcpy(out, c.logits_pinned, G4_VOCAB * sizeof(float));
     return G4_OK;
 }
 
