@@ -85,6 +85,10 @@ struct Context {
     int *tokens_pinned = nullptr;
     int *pos_dev = nullptr, *pos_pinned = nullptr;
     float *logits_pinned = nullptr;  // one logits row: the copy out is a direct DMA
+    // many rows (g4_logits_all): pieces through two pinned buffers, the DMA of
+    // one overlapping the host copy of the other
+    char *pieces_pinned[2] = {};
+    hipEvent_t piece_done[2] = {};
     int last_n = 0;
     // One-token steps replay a captured graph of the whole forward pass; the
     // position is read from pos_dev.  Recaptured when the scratch buffers move
@@ -99,6 +103,9 @@ struct Context {
 };
 
 static Context g_ctx;
+
+// Bytes of one piece of a many-row logits copy (g4_logits_all).
+constexpr size_t kCopyPiece = (size_t)16 << 20;
 
 // Initial positions of a global-attention ring (a power of two).
 constexpr int kGlobalStart = 4096;
@@ -155,6 +162,10 @@ static void free_all(Context &c) {
     if (c.tokens_pinned) (void)hipHostFree(c.tokens_pinned);
     if (c.pos_pinned) (void)hipHostFree(c.pos_pinned);
     if (c.logits_pinned) (void)hipHostFree(c.logits_pinned);
+    for (char *p : c.pieces_pinned)
+        if (p) (void)hipHostFree(p);
+    for (hipEvent_t e : c.piece_done)
+        if (e) (void)hipEventDestroy(e);
     if (c.decode_graph) (void)hipGraphExecDestroy(c.decode_graph);
     for (auto &lane : c.kv_written)
         for (hipEvent_t e : lane)
@@ -356,6 +367,8 @@ static int init(const g4_tensor *records, int device) {
     G4_HIP(hipMalloc(&c.pos_dev, sizeof(int)));
     G4_HIP(hipHostMalloc((void **)&c.pos_pinned, sizeof(int), hipHostMallocDefault));
     G4_HIP(hipHostMalloc((void **)&c.logits_pinned, G4_VOCAB * sizeof(float), hipHostMallocDefault));
+    for (char *&p : c.pieces_pinned) G4_HIP(hipHostMalloc((void **)&p, kCopyPiece, hipHostMallocDefault));
+    for (hipEvent_t &e : c.piece_done) G4_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     // Split-K scratch for the widest few-row product (1536 x 12288), and the
     // one-token attention scratch at full context (8 score rows), so that a
     // captured decode step never needs a larger buffer.
@@ -880,9 +893,24 @@ extern "C" int g4_logits_all(float *out) {
     G4_HIP(hipSetDevice(c.device));
     if (!c.logits_all) G4_HIP(hipMalloc(&c.logits_all, (size_t)G4_BATCH * G4_VOCAB * sizeof(float)));
     G4_TRY(logits_rows(c, c.logits_all, 0, c.last_n));
-    G4_HIP(hipMemcpyAsync(out, c.logits_all, (size_t)c.last_n * G4_VOCAB * sizeof(float),
-                          hipMemcpyDeviceToHost, c.stream));
-    G4_HIP(hipStreamSynchronize(c.stream));
+    // piece i goes to pinned buffer i % 2 by DMA; while piece i + 1's DMA
+    // runs, the host copies piece i out (buffer i % 2 is reused only after
+    // that copy returned)
+    const size_t total = (size_t)c.last_n * G4_VOCAB * sizeof(float);
+    const size_t pieces = (total + kCopyPiece - 1) / kCopyPiece;
+    const char *src = (const char *)c.logits_all;
+    auto size_of = [&](size_t i) { return i + 1 < pieces ? kCopyPiece : total - i * kCopyPiece; };
+    G4_HIP(hipMemcpyAsync(c.pieces_pinned[0], src, size_of(0), hipMemcpyDeviceToHost, c.stream));
+    G4_HIP(hipEventRecord(c.piece_done[0], c.stream));
+    for (size_t i = 0; i < pieces; i++) {
+        if (i + 1 < pieces) {
+            G4_HIP(hipMemcpyAsync(c.pieces_pinned[(i + 1) & 1], src + (i + 1) * kCopyPiece, size_of(i + 1),
+                                  hipMemcpyDeviceToHost, c.stream));
+            G4_HIP(hipEventRecord(c.piece_done[(i + 1) & 1], c.stream));
+        }
+        G4_HIP(hipEventSynchronize(c.piece_done[i & 1]));
+        memcpy((char *)out + i * kCopyPiece, c.pieces_pinned[i & 1], size_of(i));
+    }
     return G4_OK;
 }
 
