@@ -1750,14 +1750,16 @@ __global__ __launch_bounds__(QUANT ? 256 : 64) void k_attn_values_decode(float *
 // k_attn_values_decode over a global layer (FULL, fp32 out) with the tile
 // staging on a second wave.  Wave 1 (the producer, on another SIMD) loads the
 // 64-key V tiles of its 16 channels DEPTH tiles ahead in registers and
-// writes each, transposed and permuted as above, into LDS slot tile & 1;
+// writes each, transposed and permuted as above, into LDS slot tile & 3;
 // wave 0 (the chain) only reads each tile's column and runs its 64 DPP fmas,
-// so the staging no longer takes the chain's issue slots.  One barrier a
-// tile: before barrier u the producer has written tile u + 1, and the chain
-// has waited for its reads of tile u (it reads tile u during the chain of
-// tile u - 1); after it the chain reads tile u + 1 while it runs tile u,
-// and the producer overwrites tile u's slot with tile u + 2.  Both waves pass
-// the same 1 + tiles barriers.
+// so the staging no longer takes the chain's issue slots.  The chain reads
+// tile u + 1 while it runs tile u.  One barrier every two tiles: before the
+// first the producer has written tiles 0-2, and the chain reads tile 0
+// between it and a second; barrier m + 2 comes after the chain's tiles 2m
+// and 2m + 1 (it then has read, and waited for, tiles up to 2m + 2), and the
+// producer writes tiles 2m + 3 and 2m + 4 before it, into the slots of
+// tiles 2m - 1 and 2m, which the chain finished reading before barrier
+// m + 1.  Both waves pass the same 2 + tiles / 2 barriers.
 constexpr int kWaitLgkm0 = 0xC07F;  // s_waitcnt lgkmcnt(0), vmcnt and expcnt untouched
 
 template <int HD, int DEPTH>
@@ -1767,7 +1769,7 @@ __global__ __launch_bounds__(128) void k_attn_values_decode_pc(float *__restrict
                                                                int cache_len, int start_pos,
                                                                const int *__restrict__ pos_dev,
                                                                size_t stride) {
-    __shared__ __attribute__((aligned(16))) float s_v[2][16][68];  // [slot][channel][position]
+    __shared__ __attribute__((aligned(16))) float s_v[4][16][68];  // [slot][channel][position]
     if (pos_dev) start_pos = *pos_dev;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, r = lane >> 4, j = lane & 15;
@@ -1806,32 +1808,33 @@ __global__ __launch_bounds__(128) void k_attn_values_decode_pc(float *__restrict
         VTile ring[DEPTH];  // tile u in ring[u % DEPTH]
 #pragma unroll
         for (int s = 0; s < DEPTH; s++) load_v(s, ring[s]);
-        store_v(0, ring[0]);
-        load_v(DEPTH, ring[0]);
-        __syncthreads();
-        // step u: tile u + 1 into slot (u + 1) & 1, its ring slot refilled
-        // with tile u + 1 + DEPTH
-        auto step = [&](int u, VTile &next) __attribute__((always_inline)) {
-            store_v((u + 1) & 1, next);
-            load_v(u + 1 + DEPTH, next);
-            __syncthreads();
+        // tile u into LDS slot u & 3, its ring slot refilled with tile u + DEPTH
+        auto put = [&](int slot, int u, VTile &st) __attribute__((always_inline)) {
+            store_v(slot, st);
+            load_v(u + DEPTH, st);
         };
-        for (int u = 0; u < tiles; u += DEPTH) {
-            step(u + 0, ring[1]);
-            if (u + 1 >= tiles) break;
-            step(u + 1, ring[2]);
-            if (u + 2 >= tiles) break;
-            step(u + 2, ring[3]);
-            if (u + 3 >= tiles) break;
-            step(u + 3, ring[4]);
-            if (u + 4 >= tiles) break;
-            step(u + 4, ring[5]);
-            if (u + 5 >= tiles) break;
-            step(u + 5, ring[6]);
-            if (u + 6 >= tiles) break;
-            step(u + 6, ring[7]);
-            if (u + 7 >= tiles) break;
-            step(u + 7, ring[0]);
+        put(0, 0, ring[0]);
+        put(1, 1, ring[1]);
+        put(2, 2, ring[2]);
+        __syncthreads();
+        __syncthreads();  // the chain has read tile 0: slot 0 is free
+        // m = 4 i + k: tiles 2m + 3 and 2m + 4 = 8 i + 2k + 3 and 8 i + 2k + 4
+        for (int m = 0; 2 * m + 1 < tiles; m += 4) {
+            put(3, 2 * m + 3, ring[3]);
+            put(0, 2 * m + 4, ring[4]);
+            __syncthreads();
+            if (2 * m + 3 >= tiles) break;
+            put(1, 2 * m + 5, ring[5]);
+            put(2, 2 * m + 6, ring[6]);
+            __syncthreads();
+            if (2 * m + 5 >= tiles) break;
+            put(3, 2 * m + 7, ring[7]);
+            put(0, 2 * m + 8, ring[0]);
+            __syncthreads();
+            if (2 * m + 7 >= tiles) break;
+            put(1, 2 * m + 9, ring[1]);
+            put(2, 2 * m + 10, ring[2]);
+            __syncthreads();
         }
         return;
     }
@@ -1876,35 +1879,50 @@ __global__ __launch_bounds__(128) void k_attn_values_decode_pc(float *__restrict
 #pragma unroll
         for (int i = 0; i < 16; i++) col[i] = src[i];
     };
+    // The reads of a column must be complete before the barrier that lets the
+    // producer overwrite its slot, and the compiler would otherwise sink LDS
+    // loads past a barrier to their first use: an empty asm that takes the
+    // registers keeps them (and the wait for them) ahead of it.
+    auto pin = [](f4 (&col)[16]) __attribute__((always_inline)) {
+        asm volatile("" : "+v"(col[0]), "+v"(col[1]), "+v"(col[2]), "+v"(col[3]), "+v"(col[4]), "+v"(col[5]),
+                          "+v"(col[6]), "+v"(col[7]), "+v"(col[8]), "+v"(col[9]), "+v"(col[10]), "+v"(col[11]),
+                          "+v"(col[12]), "+v"(col[13]), "+v"(col[14]), "+v"(col[15]));
+    };
     f4 col_a[16], col_b[16];  // tile u's column: col_a for even u, col_b for odd
-    __syncthreads();  // tile 0 is in slot 0
+    __syncthreads();  // tiles 0-2 are in slots 0-2
     read_col(0, col_a);
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    // step u: after barrier u, read tile u + 1 while tile u's chain runs, then
-    // wait for those reads (before the next barrier)
-    auto step = [&](int u, const f4 (&cur)[16], f4 (&next)[16], f4 &p) __attribute__((always_inline)) {
-        __syncthreads();
-        read_col((u + 1) & 1, next);
+    pin(col_a);
+    __syncthreads();  // slot 0 may take tile 4
+    // step u: read tile u + 1 (slot (u + 1) & 3) while tile u's chain runs,
+    // then wait for those reads; a barrier after each odd u
+    auto step = [&](int slot, int u, const f4 (&cur)[16], f4 (&next)[16], f4 &p) __attribute__((always_inline)) {
+        read_col(slot, next);
         chain64(cur, p);
         p = load_p(u + DEPTH);
         __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+        pin(next);
     };
     for (int u = 0; u < tiles; u += DEPTH) {
-        step(u + 0, col_a, col_b, p_ring[0]);
+        step(1, u + 0, col_a, col_b, p_ring[0]);
         if (u + 1 >= tiles) break;
-        step(u + 1, col_b, col_a, p_ring[1]);
+        step(2, u + 1, col_b, col_a, p_ring[1]);
+        __syncthreads();
         if (u + 2 >= tiles) break;
-        step(u + 2, col_a, col_b, p_ring[2]);
+        step(3, u + 2, col_a, col_b, p_ring[2]);
         if (u + 3 >= tiles) break;
-        step(u + 3, col_b, col_a, p_ring[3]);
+        step(0, u + 3, col_b, col_a, p_ring[3]);
+        __syncthreads();
         if (u + 4 >= tiles) break;
-        step(u + 4, col_a, col_b, p_ring[4]);
+        step(1, u + 4, col_a, col_b, p_ring[4]);
         if (u + 5 >= tiles) break;
-        step(u + 5, col_b, col_a, p_ring[5]);
+        step(2, u + 5, col_b, col_a, p_ring[5]);
+        __syncthreads();
         if (u + 6 >= tiles) break;
-        step(u + 6, col_a, col_b, p_ring[6]);
+        step(3, u + 6, col_a, col_b, p_ring[6]);
         if (u + 7 >= tiles) break;
-        step(u + 7, col_b, col_a, p_ring[7]);
+        step(0, u + 7, col_b, col_a, p_ring[7]);
+        __syncthreads();
     }
     out[((size_t)t * 8 + 4 * blockIdx.y + r) * HD + c0 + j] = o;
 }
