@@ -39,6 +39,14 @@ GEMV_SWEEP = [
 ]
 
 
+# Algorithmic HBM bytes of one decode step at 16384 positions of context: the
+# weights of every product (int8 + fp16 scales), the keys and values each of
+# the 7 global layers reads (16384 rows of 512 floats each), and those each of
+# the 28 window layers reads (512 rows of 256 floats each).
+DECODE16K_STEP_BYTES = (sum(count * (n * k + n * k // 32) for n, k, count in GEMV_SWEEP)
+                        + 7 * 16384 * 512 * 2 * 4 + 28 * 512 * 256 * 2 * 4)
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -170,10 +178,17 @@ def vendor_int8_gemm(torch, m: int = 512, n: int = 6144, k: int = 1536) -> dict:
 def probe(pkg, lib, torch, what: str, launches: int = 20) -> None:
     """Launch one kernel alone, for hardware-counter runs under rocprofv3 --pmc:
     `gemm` = the prefill GEMM above, `gemv` = the lm_head GEMV (262144 x 1536,
-    one token), `copy` = a 256 MiB device-to-device copy (the calibration
-    kernel: it reads and writes exactly 268,435,456 bytes)."""
+    one token), `kv` = one global layer's decode attention at 16384 keys
+    (scores, softmax, P.V), `copy` = a 256 MiB device-to-device copy (the
+    calibration kernel: it reads and writes exactly 268,435,456 bytes)."""
     gen = torch.Generator(device="cuda").manual_seed(4)
     stream = torch.cuda.current_stream().cuda_stream
+    if what == "kv":
+        q, out, caches = kv_inputs(torch, 6)
+        for i in range(launches):
+            attend_global(pkg, lib, stream, q, out, caches[i % 6])
+        torch.cuda.synchronize()
+        return
     if what == "copy":
         a = torch.empty(64 << 20, dtype=torch.float32, device="cuda")
         b = torch.empty_like(a)
@@ -247,6 +262,72 @@ def gemv_sweep(pkg, lib, torch) -> dict:
         "per_shape": {k: round(v["gbs"], 1) for k, v in per_shape.items()},
         "per_shape_us": {k: round(v["ms"] * 1e3, 2) for k, v in per_shape.items()},
     }
+
+
+KV_KEYS, KV_HEAD_DIM, KV_HEADS = 16384, 512, 8  # a global layer's decode attention at 16K context
+
+
+def kv_inputs(torch, copies: int):
+    """Query rows and `copies` key/value caches of a global layer at 16384
+    positions (N(0,1) rows, the scale of the model's normalized K/V rows)."""
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    q = torch.randn((1, KV_HEADS * KV_HEAD_DIM), device="cuda", generator=gen) * 0.25
+    out = torch.empty_like(q)
+    caches = [torch.randn((2, KV_KEYS, KV_HEAD_DIM), device="cuda", generator=gen) for _ in range(copies)]
+    return q, out, caches
+
+
+def attend_global(pkg, lib, stream, q, out, cache) -> None:
+    """gemma4.c:443-456 for one token at position 16383 of a global layer:
+    scores over keys 0..16383, softmax, P.V (reference order, as in the model's
+    decode step)."""
+    pkg.check(lib.g4_attend(stream, out.data_ptr(), q.data_ptr(), cache[0].data_ptr(), cache[1].data_ptr(),
+                            KV_KEYS, KV_HEAD_DIM, KV_HEADS, 1, KV_KEYS - 1, 1))
+
+
+def profile_figures(name: str) -> dict:
+    """`key: value` lines of a committed rocprofv3 summary under profiles/."""
+    figures = {}
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            for line in f:
+                key, sep, value = line.partition(":")
+                if sep and key.strip().endswith("_us"):
+                    try:
+                        figures[key.strip()] = float(value.split()[0])
+                    except (ValueError, IndexError):
+                        pass
+    except OSError:
+        pass
+    return figures
+
+
+def kv_roofline(pkg, lib, torch) -> dict:
+    """The KV-cache reads of one global layer's decode attention at 16384 keys
+    (head_dim 512, 8 query heads on the one KV head): K and V, 33.5 MB each,
+    read once per layer.  Six caches (403 MB) are rotated so that repeats come
+    from HBM, not the 256 MB Infinity Cache; timed by graph replay like the
+    GEMV sweep.  The split by kernel (scores read K, P.V reads V) comes from
+    the committed kernel trace of `bench.py --probe kv`."""
+    copies = 6
+    q, out, caches = kv_inputs(torch, copies)
+
+    def launch(i):
+        attend_global(pkg, lib, torch.cuda.current_stream().cuda_stream, q, out, caches[i % copies])
+
+    ms = graph_timed(torch, launch, 4 * copies, 10)
+    kv_bytes = 2 * KV_KEYS * KV_HEAD_DIM * 4
+    moved = kv_bytes + 2 * q.numel() * 4
+    res = {"ms": ms, "bytes": moved, "gbs": moved / (ms * 1e-3) / 1e9}
+    split = profile_figures("attend_global_16k_kernel_stats.txt")
+    if {"scores_us", "values_us"} <= split.keys():
+        half = kv_bytes / 2
+        res["k_read_gbs_scores"] = half / (split["scores_us"] * 1e-6) / 1e9
+        res["v_read_gbs_values"] = half / (split["values_us"] * 1e-6) / 1e9
+        res["split_us"] = split
+    del caches
+    torch.cuda.empty_cache()
+    return res
 
 
 def decode_probe(pkg, lib, np, context: int = 16384, steps: int = 32) -> None:
@@ -394,9 +475,10 @@ def cpu_baseline(pkg, image, np) -> dict:
       - prefill 8192 in 512-token chunks + logits: one run after the warmups
         (about 16 s on 16 Zen 5 cores);
       - decode at 16384 positions of context: forward + logits per step, 1
-        untimed and 4 timed steps, with KV rows 0..16383 filled with N(0,1)
-        values in place of a 16384-token prefill (the step's work does not
-        depend on them; the rows the model writes are RMS-normalized, so of
+        untimed and 16 timed steps, the rate from the median step, with KV
+        rows 0..16383 filled with N(0,1) values in place of a 16384-token
+        prefill (a synthetic-KV approximation: the step's work does not depend
+        on the values; the rows the model writes are RMS-normalized, so of
         that scale)."""
     import ctypes
 
@@ -449,7 +531,8 @@ def cpu_baseline(pkg, image, np) -> dict:
             model.fill_kv_random(16384, seed=5)
             model.forward(token, 16384)
             model.logits(0)
-            decode = 4 / timed(lambda: [(model.forward(token, 16384 + i), model.logits(0)) for i in range(4)])
+            steps = [timed(lambda i=i: (model.forward(token, 16384 + i), model.logits(0))) for i in range(16)]
+            decode = 1.0 / float(np.median(steps))
     finally:
         model.close()
         if old_env is None:
@@ -464,8 +547,8 @@ def cpu_baseline(pkg, image, np) -> dict:
     return {"value": rate, "unit": "tok/s", "cores": threads, "kind": kind,
             "sample": "gemma4.c forward()+logits() on the same synthetic model: 512-token prefill + "
                       "logits, 1 discarded warmup + mean of 3; prefill 8192 in 512-token chunks + logits, "
-                      "1 run; decode at 16384 positions (KV rows filled with N(0,1) in place of the "
-                      "prefill), 1 untimed + 4 timed steps of forward + logits",
+                      "1 run; decode at 16384 positions (synthetic KV: rows filled with N(0,1) in place "
+                      "of the prefill), 1 untimed + 16 timed steps of forward + logits, median step",
             "prefill512_tok_s_8_threads": prefill8, "prefill8192_tok_s": prefill8k,
             "decode16k_tok_s": decode,
             "host": {"nproc": nproc, "physical_cores": physical, "threads": threads}}
@@ -478,7 +561,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--order", choices=["reference", "parallel"], default="reference")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--probe", choices=["gemm", "gemv", "copy", "prefill", "decode"],
+    ap.add_argument("--probe", choices=["gemm", "gemv", "kv", "copy", "prefill", "decode"],
                     help="only launch one kernel 20 times (for rocprofv3 --pmc runs), or run "
                          "3 + 10 prefill-512 steps of the model (prefill), or fill 16384 "
                          "positions and run 32 decode steps (decode); no JSON")
@@ -525,6 +608,8 @@ def main() -> int:
     log(f"vendor int8 GEMM, same shape: {vendor}")
     sweep = gemv_sweep(pkg, lib, torch)
     log(f"decode GEMV sweep: {sweep['byte_weighted_gbs']:.0f} GB/s byte-weighted; {sweep['per_shape']}")
+    kv = kv_roofline(pkg, lib, torch)
+    log(f"global-layer decode attention at 16K keys: {kv['ms'] * 1e3:.1f} us, {kv['gbs']:.0f} GB/s of K+V")
     torch.cuda.empty_cache()
 
     t = time.perf_counter()
@@ -595,6 +680,23 @@ def main() -> int:
             "per_shape_gbs": sweep["per_shape"],
             "traffic": pmc_traffic("k_gemv_262144x1536_pmc.txt"),
             "traffic_source": "profiles/k_gemv_262144x1536_pmc.txt (HBM bytes per lm_head launch)",
+        },
+        "roofline_kv": {
+            "bound": "hbm",
+            "kernel": "global-layer decode attention over 16384 keys (scores read K, P.V reads V; hd 512, "
+                      "8 query heads, reference order)",
+            "achieved": round(kv["gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(kv["gbs"] / HBM_PEAK_GBS, 4),
+            "bytes_per_layer": kv["bytes"],
+            "us_per_layer": round(kv["ms"] * 1e3, 2),
+            "k_read_gbs_scores": kv.get("k_read_gbs_scores") and round(kv["k_read_gbs_scores"], 1),
+            "v_read_gbs_values": kv.get("v_read_gbs_values") and round(kv["v_read_gbs_values"], 1),
+            "split_source": "profiles/attend_global_16k_kernel_stats.txt (kernel trace of bench.py --probe kv)",
+            "decode_step_traffic": pmc_traffic("decode16k_step_pmc.txt"),
+            "decode_step_algorithmic_bytes": DECODE16K_STEP_BYTES,
+            "decode_step_traffic_source": "profiles/decode16k_step_pmc.txt (HBM bytes per decode step at 16K)",
         },
         "cpu_baseline": cpu,
     }

@@ -10,12 +10,15 @@ tensor 64-byte aligned in the exporter's cursor order; matrices quantized with
 its rule (absmax / 127 as an fp16 scale floored at 6.104e-5, rint, clip to
 +-127; exporter.py:267-273) and packed in 16-row x 64-column tiles
 (exporter.py:304-316); the shared RoPE tables and the GELU table from its
-formulas (exporter.py:73-92).
+formulas (exporter.py:73-92), evaluated with numpy's float32 functions in the
+exporter's operation order, so they are the exporter's bits.
 
-The layout, the quantize-and-pack step and the tables are libg4img.so's (the
-same code writes the seeded synthetic image), so a checkpoint holding the
-synthetic generator's values exports to the synthetic image exactly
-(tests/test_export.py).  This module reads the checkpoint without torch: the
+The layout and the quantize-and-pack step are libg4img.so's (the same code
+writes the seeded synthetic image), so a checkpoint holding the synthetic
+generator's values exports to the synthetic image exactly outside the tables
+(tests/test_export.py); the synthetic image computes its tables with the C
+library's powf/sinf/cosf/tanhf instead, which differ from numpy's in the last
+bits of some entries.  This module reads the checkpoint without torch: the
 safetensors header is JSON, the tensors are mapped from the file.
 """
 
@@ -181,6 +184,47 @@ def compile_tokenizer(data: dict) -> bytes:
 
 
 # ---------------------------------------------------------------------------
+# The computed tables (exporter.py:73-92), float32 throughout: numpy's
+# float32 tanh/cos/sin/power give the exporter's bits, which the C library's
+# functions do not always match.
+
+GELU_POINTS, GELU_LOWER, GELU_UPPER = 4096, -8.0, 8.0
+
+
+def gelu_values() -> np.ndarray:
+    """The tanh-form GELU at 4096 evenly spaced points of [-8, 8]; the
+    products are taken left to right, as the exporter writes them."""
+    x = np.linspace(GELU_LOWER, GELU_UPPER, GELU_POINTS, dtype=np.float32)
+    inner = x + np.float32(0.044715) * x * x * x
+    return (np.float32(0.5) * x * (np.float32(1.0) + np.tanh(np.float32(0.7978845608) * inner))).astype(np.float32)
+
+
+def rope_values(head_dim: int, rotary_fraction: float, theta: float, positions: int):
+    """(cos, sin) [positions x pairs] of angle = pos * theta^(-2j / head_dim)
+    over the first int(head_dim * rotary_fraction) / 2 pairs."""
+    pairs = int(head_dim * rotary_fraction) // 2
+    inverse = np.float32(1) / np.power(np.float32(theta),
+                                       np.arange(pairs, dtype=np.float32) * np.float32(2) / np.float32(head_dim))
+    angle = np.arange(positions, dtype=np.float32)[:, None] * inverse
+    return np.cos(angle), np.sin(angle)
+
+
+def table_values(it, text_config: dict) -> np.ndarray:
+    """The float32 values of a RoPE or GELU table item."""
+    if it.kind == _pkg.ITEM_GELU:
+        return gelu_values()
+    rope = text_config["rope_parameters"]
+    if it.global_rope:
+        full = rope["full_attention"]
+        cos, sin = rope_values(text_config["global_head_dim"], float(full["partial_rotary_factor"]),
+                               float(full["rope_theta"]), it.rows)
+    else:
+        cos, sin = rope_values(text_config["head_dim"], 1.0, float(rope["sliding_attention"]["rope_theta"]),
+                               it.rows)
+    return cos if it.kind == _pkg.ITEM_ROPE_COS else sin
+
+
+# ---------------------------------------------------------------------------
 # model.safetensors, mapped (no torch)
 
 _DTYPES = {"F32": (_pkg.DTYPE_F32, np.float32), "BF16": (_pkg.DTYPE_BF16, np.uint16),
@@ -226,7 +270,7 @@ class SafeTensors:
 def export(checkpoint: str, out_path: str, threads: int = 0) -> None:
     img = _pkg.img()
     with open(os.path.join(checkpoint, "config.json"), encoding="utf-8") as f:
-        check_config(json.load(f))
+        text_config = check_config(json.load(f))
     with open(os.path.join(checkpoint, "tokenizer.json"), encoding="utf-8") as f:
         tokenizer = compile_tokenizer(json.load(f))
     weights = SafeTensors(os.path.join(checkpoint, "model.safetensors"))
@@ -249,7 +293,10 @@ def export(checkpoint: str, out_path: str, threads: int = 0) -> None:
     for i in range(count):
         it = items[i]
         if it.kind in (_pkg.ITEM_ROPE_COS, _pkg.ITEM_ROPE_SIN, _pkg.ITEM_GELU):
-            check(img.g4img_fill_table(base, size, ctypes.byref(it), threads))
+            values = table_values(it, text_config)
+            if values.size != it.rows * it.cols:
+                raise ExportError(f"table item {i}: {values.size} values for {it.rows} x {it.cols}")
+            out[it.data:it.data + 4 * values.size] = values.reshape(-1).view(np.uint8)
             continue
         name = record_tensor(it.record)
         if it.kind == _pkg.ITEM_QUANT:

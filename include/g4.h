@@ -186,7 +186,11 @@ int g4_attend(void *stream, float *out, const float *q, const float *key_cache,
  * go to (start_pos + t) & (cache_len - 1).  head_dim is q_norm's length (256
  * or 512), 8 query heads; sliding layers (full_attention = 0) see the last
  * G4_WINDOW positions.  Grows library-owned device buffers (hipMalloc) when a
- * call has more rows than they hold; g4_shutdown frees them. */
+ * call has more rows than they hold; g4_shutdown frees them.  Those buffers
+ * (the query heads, the new key/value rows, the quantized activations) are
+ * one set for the process: calls that overlap in time, e.g. on two streams,
+ * race on them, so a caller orders its calls on one stream or waits between
+ * them. */
 int g4_attention_layer(void *stream, float *hidden, size_t n, int start_pos, const g4_tensor *layer,
                        float *cache, int cache_len, int full_attention);
 

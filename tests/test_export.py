@@ -1,10 +1,12 @@
 """The checkpoint writer (gemma4.c_amd/export.py, exporter.py's job): a
 fabricated Gemma-4-E2B-shaped checkpoint whose BF16 weights are the synthetic
-generator's seeded values exports to the synthetic image byte for byte (the
-generator with G4IMG_BF16_VALUES quantizes the same bf16-rounded values), and
-its tokenizer block is the reference's compile_tokenizer output for the same
-tokenizer.json (tests/golden/export_tokenizer.json, written by the reference's
-own function).  Plus the dtypes of the packing step and the writer's refusals.
+generator's seeded values exports to the synthetic image byte for byte outside
+the computed tables (the generator with G4IMG_BF16_VALUES quantizes the same
+bf16-rounded values).  Its tokenizer block, its quantize-and-pack step and its
+RoPE/GELU tables are the reference exporter's own output (golden vectors in
+tests/golden/ written by exporter.py's compile_tokenizer, quantize +
+write_tensor, rope_tables and gelu_table).  Plus the dtypes of the packing step
+and the writer's refusals.
 """
 
 from __future__ import annotations
@@ -85,6 +87,55 @@ def test_tokenizer_block_is_the_references(export):
     assert hashlib.sha256(block).hexdigest() == gold["sha256"]
 
 
+def test_pack_matrix_is_the_exporters(pkg):
+    """g4img_pack_matrix (the quantize-and-pack step of both writers) against
+    exporter.py's quantize + write_tensor on a 48 x 192 matrix with
+    bf16-rounded values, a zero group, a group under the fp16 scale floor, a
+    lone value, exact halves of the scale and a wide dynamic range: int8
+    bytes and fp16 scale bytes identical."""
+    with np.load(os.path.join(GOLDEN, "export_pack.npz"), allow_pickle=False) as z:
+        x, want_q, want_s = z["input"], z["packed"], z["scales"]
+    rows, cols = x.shape
+    q = np.zeros(rows * cols, np.int8)
+    s = np.zeros(rows * cols // 64, np.uint16)
+    assert pkg.img().g4img_pack_matrix(np.ascontiguousarray(x).ctypes.data, pkg.DTYPE_F32, rows, cols,
+                                       q.ctypes.data, s.ctypes.data, 2) == 0
+    assert np.array_equal(s, want_s), np.flatnonzero(s != want_s)[:8]
+    assert np.array_equal(q, want_q), np.flatnonzero(q != want_q)[:8]
+
+
+def test_pack_golden_catches_the_unrounded_scale():
+    """The fixture tells the exporter's rule (divide by the fp16-rounded scale)
+    from a plausible slip (divide by the fp32 scale before its rounding)."""
+    with np.load(os.path.join(GOLDEN, "export_pack.npz"), allow_pickle=False) as z:
+        x, want_q = z["input"], z["packed"]
+    groups = x.reshape(-1, 64)
+    scale = np.maximum(np.abs(groups).max(axis=1) / np.float32(127.0), np.float32(6.104e-05))
+    slip = np.rint(groups / scale[:, None]).clip(-127, 127).astype(np.int8)
+    blocks, ng = x.shape[0] // 16, x.shape[1] // 64
+    packed = slip.reshape(blocks, 16, ng, 16, 4).transpose(0, 2, 3, 1, 4).reshape(-1)
+    assert not np.array_equal(packed, want_q)
+
+
+def test_tables_are_the_exporters(export):
+    """export.py's GELU and RoPE tables against the SHA-256 of exporter.py's
+    gelu_table() and rope_tables() for the E2B configuration (the same numpy
+    float32 functions, so the same bits)."""
+    gold = json.load(open(os.path.join(GOLDEN, "export_tables.json")))
+    digest = lambda a: hashlib.sha256(np.ascontiguousarray(a, dtype=np.float32).tobytes()).hexdigest()
+    note = f"golden written with numpy {gold['numpy']}, this is {np.__version__}"
+    assert digest(export.gelu_values()) == gold["gelu"], note
+    t = fabricated_config()["text_config"]
+    rope = t["rope_parameters"]
+    tables = {"sliding": export.rope_values(t["head_dim"], 1.0, rope["sliding_attention"]["rope_theta"], 131072),
+              "global": export.rope_values(t["global_head_dim"], rope["full_attention"]["partial_rotary_factor"],
+                                           rope["full_attention"]["rope_theta"], 131072)}
+    for kind, (cos, sin) in tables.items():
+        assert list(cos.shape) == gold[f"{kind}_cos_shape"]
+        assert digest(cos) == gold[f"{kind}_cos"], (kind, note)
+        assert digest(sin) == gold[f"{kind}_sin"], (kind, note)
+
+
 def test_checkpoint_exports_to_the_synthetic_image(pkg, export):
     flags = pkg.BF16_VALUES
     size = pkg.img().g4img_size(flags)
@@ -99,10 +150,33 @@ def test_checkpoint_exports_to_the_synthetic_image(pkg, export):
         ref = np.frombuffer(synthetic.buf, dtype=np.uint8, count=size)
         t0, t1 = 4, 4 + pkg.TOKENIZER_SPAN
         assert bytes(out[:t0]) == bytes(ref[:t0]) == b"MOG\0"
-        # records and every tensor (4.97 GB): the same bytes, in 512 MiB pieces
-        step = 1 << 29
-        for at in range(t1, size, step):
-            assert np.array_equal(out[at:at + step], ref[at:at + step]), at
+        # the computed tables: the exporter's numpy values (pinned by
+        # test_tables_are_the_exporters) in the file.  The synthetic image's
+        # come from the C library (powf, cosf, sinf, tanhf): some RoPE
+        # frequencies differ from numpy's by an ulp, which a position of up to
+        # 131071 turns into angles up to ~2 ulp of 1 apart (|d| <= 2^-5 on
+        # cos/sin, measured 0.0156); the GELU entries within a few ulp
+        items = (pkg.ImageItem * 700)()
+        count = pkg.img().g4img_layout(flags, items, 700)
+        tables = []
+        for i in range(count):
+            it = items[i]
+            if it.kind in (pkg.ITEM_ROPE_COS, pkg.ITEM_ROPE_SIN, pkg.ITEM_GELU):
+                n = it.rows * it.cols
+                want = export.table_values(it, fabricated_config()["text_config"]).reshape(-1)
+                got = np.asarray(out[it.data:it.data + 4 * n]).view(np.float32)
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), i
+                syn = np.asarray(ref[it.data:it.data + 4 * n]).view(np.float32)
+                bound = 2.0 ** -5 if it.kind != pkg.ITEM_GELU else 4 * np.spacing(np.abs(want).max())
+                assert np.abs(syn - want).max() <= bound, (i, float(np.abs(syn - want).max()))
+                tables.append((it.data, it.data + 4 * n))
+        # records and every other tensor (4.77 GB): the same bytes, in 512 MiB pieces
+        step, at = 1 << 29, t1
+        for begin, end in sorted(tables) + [(size, size)]:
+            for piece in range(at, begin, step):
+                stop = min(piece + step, begin)
+                assert np.array_equal(out[piece:stop], ref[piece:stop]), piece
+            at = max(at, end)
         gold = json.load(open(os.path.join(GOLDEN, "export_tokenizer.json")))
         assert hashlib.sha256(out[t0:t1].tobytes()).hexdigest() == gold["sha256"]
         del out, ref, synthetic
