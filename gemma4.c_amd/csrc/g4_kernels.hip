@@ -319,6 +319,171 @@ __global__ __launch_bounds__(1024) void k_gemv_split(float *__restrict__ out, si
     }
 }
 
+// One token (M = 1) with every CU streaming weight tiles.  A block covers one
+// 16-row strip and GB = W * U consecutive groups of it -- all of its groups
+// (SPLIT false), or one of `parts` slices of them (SPLIT true) -- and wave
+// w takes U of those groups.  Each thread first loads its share of the
+// block's activation dwords (and, without SPLIT, of its (group, row) weight
+// and activation scales), then the wave issues its U tile
+// loads; the dwords and the scale products go to LDS while the tiles are in
+// flight (vector-memory loads complete in order, so the staging waits only
+// for the first loads).  The exact group dots (gemv_group_dots) then go to
+// LDS, and 16 threads fold the strip's groups in order (gemma4.c:216-218);
+// with SPLIT they go to dots [strip][group][16] and k_gemv1_fold folds them.
+// The scale product is the reference's f16(ws) * xs, one rounding.
+template <int W, int U, bool SPLIT>
+__global__ __launch_bounds__(64 * W) void k_gemv1(float *__restrict__ out, const int8_t *__restrict__ xq,
+                                                  const float *__restrict__ xs,
+                                                  const int8_t *__restrict__ w,
+                                                  const uint16_t *__restrict__ ws, int k, int parts,
+                                                  int32_t *__restrict__ dots) {
+    constexpr int GB = W * U, XD = (U + 3) / 4;  // groups a block; staged entries a thread
+    constexpr int RF = fold_row_floats(GB);  // fold rows [16][RF] (k_gemv1 without SPLIT)
+    __shared__ int s_x[GB * 16];
+    __shared__ __attribute__((aligned(16))) float s_d[SPLIT ? 1 : 16][SPLIT ? 4 : RF],
+        s_w[SPLIT ? 1 : 16][SPLIT ? 4 : RF], s_xs[SPLIT ? 4 : RF];
+    const int groups = k >> 6;
+    int strip = blockIdx.x / parts, part = blockIdx.x % parts;
+    if (SPLIT) {
+        // the parts of strip s run on one XCD (blocks are dealt to the 8 XCDs
+        // in turn): block x + 8 (parts q + p) is part p of strip 8 q + x
+        // (strips % 8 == 0), so the fold kernel's block for s -- on the same
+        // XCD -- finds the strip's dots in its own L2
+        const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
+        strip = 8 * (j / parts) + x;
+        part = j % parts;
+    }
+    const int gb0 = part * GB;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // GB * 16 entries to stage (the block's activation dwords; without SPLIT
+    // also the (group, row) scale products), XD a thread
+    int xv[XD];
+    uint16_t wsv[XD];
+    float xsv[XD];
+#pragma unroll
+    for (int i = 0; i < XD; i++) {
+        const int e = min(tid + i * 64 * W, GB * 16 - 1);
+        xv[i] = reinterpret_cast<const int *>(xq)[gb0 * 16 + e];
+        wsv[i] = SPLIT ? 0 : ws[((size_t)strip * groups + gb0) * 16 + e];
+        xsv[i] = SPLIT ? 0.0f : xs[gb0 + e / 16];
+    }
+    const uint4 *tiles = reinterpret_cast<const uint4 *>(w + (size_t)strip * 16 * k) + lane;
+    const int gw = gb0 + wave * U;
+    uint4 t[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) t[u] = tiles[(size_t)(gw + u) * 64];
+#pragma unroll
+    for (int i = 0; i < XD; i++) {
+        const int e = tid + i * 64 * W;
+        if (e < GB * 16) {
+            s_x[e] = xv[i];
+            if (!SPLIT) {
+                s_w[e % 16][e / 16] = half_bits_to_float(wsv[i]);
+                if (e % 16 == 0) s_xs[e / 16] = xsv[i];
+            }
+        }
+    }
+    __syncthreads();
+    const int chunk = lane >> 2, b2 = (lane >> 2) & 1, b3 = (lane >> 3) & 1;
+    const int row = 4 * (lane & 3) + 2 * b2 + b3;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        int d[1];
+        const int x4[1] = {s_x[(wave * U + u) * 16 + chunk]};
+        gemv_group_dots<1>(t[u], x4, b2, b3, d);
+        if (lane < 16) {
+            if (SPLIT)
+                dots[((size_t)strip * groups + gw + u) * 16 + row] = d[0];
+            else
+                s_d[row][wave * U + u] = (float)d[0];
+        }
+    }
+    if (SPLIT) return;
+    __syncthreads();
+    if (tid < 16) out[(size_t)strip * 16 + tid] = fold_lds_row(s_d[tid], s_w[tid], s_xs, GB, 0.0f);
+}
+
+// The in-order fold of k_gemv1's split dots (M = 1): one block per 16-row
+// strip.  Its 256 threads load the strip's dots and weight scales (and the
+// activation scales) into row-major LDS rows with all loads in flight at
+// once; then 16 threads fold the groups in order (gemma4.c:216-218) with
+// fold_lds_row.  G <= 256.
+__global__ __launch_bounds__(256) void k_gemv1_fold(float *__restrict__ out, const int32_t *__restrict__ dots,
+                                                    const float *__restrict__ xs,
+                                                    const uint16_t *__restrict__ ws, int groups) {
+    constexpr int RF = fold_row_floats(256);
+    __shared__ __attribute__((aligned(16))) float s_d[16][RF], s_w[16][RF], s_x[RF];
+    const int strip = blockIdx.x, tid = threadIdx.x;
+    const int4 *d4 = reinterpret_cast<const int4 *>(dots + (size_t)strip * groups * 16);
+    const uint2 *s4 = reinterpret_cast<const uint2 *>(ws + (size_t)strip * groups * 16);
+    // groups * 4 units of four (group, row) entries, 256 a pass
+    constexpr int P = 4;
+    int4 dv[P];
+    uint2 sv[P];
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        const int i = min(tid + 256 * p, groups * 4 - 1);
+        dv[p] = d4[i];
+        sv[p] = s4[i];
+    }
+    const float xv = xs[min(tid, groups - 1)];
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        const int i = tid + 256 * p;
+        if (i < groups * 4) {
+            const int g = i >> 2, r = 4 * (i & 3);
+            s_d[r][g] = (float)dv[p].x, s_d[r + 1][g] = (float)dv[p].y;
+            s_d[r + 2][g] = (float)dv[p].z, s_d[r + 3][g] = (float)dv[p].w;
+            s_w[r][g] = half_bits_to_float((uint16_t)(sv[p].x & 0xFFFF));
+            s_w[r + 1][g] = half_bits_to_float((uint16_t)(sv[p].x >> 16));
+            s_w[r + 2][g] = half_bits_to_float((uint16_t)(sv[p].y & 0xFFFF));
+            s_w[r + 3][g] = half_bits_to_float((uint16_t)(sv[p].y >> 16));
+        }
+    }
+    if (tid < groups) s_x[tid] = xv;
+    __syncthreads();
+    if (tid < 16) out[(size_t)strip * 16 + tid] = fold_lds_row(s_d[tid], s_w[tid], s_x, groups, 0.0f);
+}
+
+// One token's product through k_gemv1 where that was measured faster than
+// k_gemv / k_gemv_split (graph replay, weights rotated past the Infinity
+// Cache): K = 1536 (24 groups) in one block of 12 waves x 2 groups (up to 384
+// strips) or 8 waves x 3 groups (more); K = 2048 in 16 waves x 2 groups;
+// K = 4096 in 16 waves x 4 groups; K = 12288 split over blocks of 8 groups
+// and folded by k_gemv1_fold.  Returns false (nothing launched) for other
+// shapes (K = 256 and K = 6144 among them: the older kernels are faster).
+static bool launch_gemv1(hipStream_t s, float *out, const int8_t *xq, const float *xs, const int8_t *w,
+                         const uint16_t *ws, int n_out, int k) {
+    const int strips = n_out / 16, groups = k / 64;
+    const dim3 grid((unsigned)strips);
+    switch (groups) {
+    case 24:
+        if (strips <= 384)
+            hipLaunchKernelGGL((k_gemv1<12, 2, false>), grid, dim3(768), 0, s, out, xq, xs, w, ws, k, 1, nullptr);
+        else
+            hipLaunchKernelGGL((k_gemv1<8, 3, false>), grid, dim3(512), 0, s, out, xq, xs, w, ws, k, 1, nullptr);
+        return true;
+    case 32:
+        hipLaunchKernelGGL((k_gemv1<16, 2, false>), grid, dim3(1024), 0, s, out, xq, xs, w, ws, k, 1, nullptr);
+        return true;
+    case 64:
+        hipLaunchKernelGGL((k_gemv1<16, 4, false>), grid, dim3(1024), 0, s, out, xq, xs, w, ws, k, 1, nullptr);
+        return true;
+    case 192: {
+        if (strips % 8) return false;
+        const int parts = groups / 8;
+        if (scratch_reserve((size_t)n_out * groups * sizeof(int32_t), 0)) return false;
+        int32_t *dots = scratch().dots;
+        hipLaunchKernelGGL((k_gemv1<2, 4, true>), dim3((unsigned)(strips * parts)), dim3(128), 0, s, out, xq, xs, w,
+                           ws, k, parts, dots);
+        hipLaunchKernelGGL(k_gemv1_fold, grid, dim3(256), 0, s, out, dots, xs, ws, groups);
+        return true;
+    }
+    default:
+        return false;
+    }
+}
+
 // The group-ordered fold of split GEMV dots: one thread per output row.
 template <int M>
 __global__ __launch_bounds__(256) void k_gemv_fold(float *__restrict__ out, size_t out_stride,
@@ -984,6 +1149,7 @@ int launch_matmul(hipStream_t s, float *out, size_t out_stride, const int8_t *xq
                                out, out_stride, xq, xs, w, ws, rows, n_out, k);
         return G4_OK;
     }
+    if (rows == 1 && launch_gemv1(s, out, xq, xs, w, ws, n_out, k)) return G4_OK;
     const int m_pad = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
     // Enough waves to keep ~16 KB in flight on every CU: aim for >= 2048 waves,
     // each covering at least 8 groups (8 KB of weights).
