@@ -181,8 +181,15 @@ struct RowTailJob {
 };
 // tail 1: norm h, add, norm, quantize; 2: norm h, add, quantize the residual;
 // 3: norm the residual, quantize.  K must be 1536.  epi/W pairs with a kernel:
-// EPI_PLAIN with tails 1, 3; EPI_GELU_PAIR with 1; EPI_GELU_MUL with 2.
+// EPI_PLAIN with tails 1, 2, 3; EPI_GELU_PAIR with 1; EPI_GELU_MUL with 2.
 int launch_gemv_tail(hipStream_t s, const GemvJob &job, int epi, const RowTailJob &tj, int tail);
+
+// One token's product of K = 256 whose input is quantize(gelu(a) * b)
+// (gemma4.c:309-331 then 265-279; b = the per-layer input), computed by the
+// product's blocks themselves (k_gemv1).  Returns G4_ERR_ARG for other K.
+int launch_gemv_gelu(hipStream_t s, float *out, const float *a, const float *b, const float *gelu_table,
+                     int gelu_size, float gelu_lower, float gelu_upper, const int8_t *w, const uint16_t *ws,
+                     int n_out, int k);
 
 // Prefill products with a GELU epilogue (k_gemm_dma<EPI_GELU_*>): the output
 // is written quantized only (q_out [rows][n_out], qs_out [rows][n_out / 64]).

@@ -324,20 +324,36 @@ __global__ __launch_bounds__(1024) void k_gemv_split(float *__restrict__ out, si
 // (SPLIT false), or one of `parts` slices of them (SPLIT true) -- and wave
 // w takes U of those groups.  Each thread first loads its share of the
 // block's activation dwords (and, without SPLIT, of its (group, row) weight
-// and activation scales), then the wave issues its U tile
-// loads; the dwords and the scale products go to LDS while the tiles are in
-// flight (vector-memory loads complete in order, so the staging waits only
-// for the first loads).  The exact group dots (gemv_group_dots) then go to
-// LDS, and 16 threads fold the strip's groups in order (gemma4.c:216-218);
-// with SPLIT they go to dots [strip][group][16] and k_gemv1_fold folds them.
-// The scale product is the reference's f16(ws) * xs, one rounding.
-template <int W, int U, bool SPLIT>
+// and activation scales), then the wave issues its U tile loads; the dwords
+// and the scales go to LDS while the tiles are in flight (vector-memory loads
+// complete in order, so the staging waits only for the first loads).  The
+// exact group dots (gemv_group_dots) then go to LDS, and 16 threads fold the
+// strip's groups in order (gemma4.c:216-218); with SPLIT they go to dots
+// [strip][group][16] and k_gemv1_fold folds them.  The scale product is the
+// reference's f16(ws) * xs, one rounding.
+//
+// IN = GEMV_GELU_MUL (U a multiple of 4): the input is not given
+// quantized but as two fp32 rows a, b; the block quantizes its own groups of
+// gelu(a) * b on the way in -- geglu (gemma4.c:309-331) then quantize
+// (gemma4.c:265-279), k_quantize's arithmetic, four values a thread, a
+// group's 16 threads in one wave -- so the product that makes a and b needs
+// no GELU epilogue.  Every block that reads a group computes the same bits.
+enum { GEMV_X = 0, GEMV_GELU_MUL = 1 };
+struct GemvInput {
+    const float *a, *b;  // gelu(a) * b
+    const float *gelu_table;
+    int gelu_size;
+    float gelu_lower, gelu_upper;
+};
+
+template <int W, int U, bool SPLIT, int IN = GEMV_X>
 __global__ __launch_bounds__(64 * W) void k_gemv1(float *__restrict__ out, const int8_t *__restrict__ xq,
                                                   const float *__restrict__ xs,
                                                   const int8_t *__restrict__ w,
                                                   const uint16_t *__restrict__ ws, int k, int parts,
-                                                  int32_t *__restrict__ dots) {
+                                                  int32_t *__restrict__ dots, GemvInput in) {
     constexpr int GB = W * U, XD = (U + 3) / 4;  // groups a block; staged entries a thread
+    static_assert(IN == GEMV_X || (U % 4 == 0 && !SPLIT), "GELU inputs: groups of four values, one block a strip");
     constexpr int RF = fold_row_floats(GB);  // fold rows [16][RF] (k_gemv1 without SPLIT)
     __shared__ int s_x[GB * 16];
     __shared__ __attribute__((aligned(16))) float s_d[SPLIT ? 1 : 16][SPLIT ? 4 : RF],
@@ -356,22 +372,51 @@ __global__ __launch_bounds__(64 * W) void k_gemv1(float *__restrict__ out, const
     const int gb0 = part * GB;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     // GB * 16 entries to stage (the block's activation dwords; without SPLIT
-    // also the (group, row) scale products), XD a thread
+    // also the (group, row) weight scales and the group scales), XD a thread
     int xv[XD];
     uint16_t wsv[XD];
     float xsv[XD];
+    float4 av[XD], bv[XD];
 #pragma unroll
     for (int i = 0; i < XD; i++) {
         const int e = min(tid + i * 64 * W, GB * 16 - 1);
-        xv[i] = reinterpret_cast<const int *>(xq)[gb0 * 16 + e];
+        if (IN == GEMV_X) {
+            xv[i] = reinterpret_cast<const int *>(xq)[gb0 * 16 + e];
+            xsv[i] = SPLIT ? 0.0f : xs[gb0 + e / 16];
+        } else {
+            av[i] = reinterpret_cast<const float4 *>(in.a)[gb0 * 16 + e];
+            bv[i] = reinterpret_cast<const float4 *>(in.b)[gb0 * 16 + e];
+        }
         wsv[i] = SPLIT ? 0 : ws[((size_t)strip * groups + gb0) * 16 + e];
-        xsv[i] = SPLIT ? 0.0f : xs[gb0 + e / 16];
     }
     const uint4 *tiles = reinterpret_cast<const uint4 *>(w + (size_t)strip * 16 * k) + lane;
     const int gw = gb0 + wave * U;
     uint4 t[U];
 #pragma unroll
     for (int u = 0; u < U; u++) t[u] = tiles[(size_t)(gw + u) * 64];
+    if (IN != GEMV_X) {  // dword e: values 4 e .. 4 e + 3 of the block's groups
+#pragma unroll
+        for (int i = 0; i < XD; i++) {
+            const float va[4] = {av[i].x, av[i].y, av[i].z, av[i].w}, vb[4] = {bv[i].x, bv[i].y, bv[i].z, bv[i].w};
+            float v[4], m = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[j] = gelu_table_lookup(va[j], in.gelu_table, in.gelu_size, in.gelu_lower, in.gelu_upper) * vb[j];
+                m = fmaxf(m, fabsf(v[j]));
+            }
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+            const float scale = m / 127.0f;
+            const float inverse = scale > 0.0f ? 1.0f / scale : 0.0f;
+            char4 q;
+            q.x = (signed char)(int)rintf(v[0] * inverse);
+            q.y = (signed char)(int)rintf(v[1] * inverse);
+            q.z = (signed char)(int)rintf(v[2] * inverse);
+            q.w = (signed char)(int)rintf(v[3] * inverse);
+            xv[i] = __builtin_bit_cast(int, q);
+            xsv[i] = scale;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < XD; i++) {
         const int e = tid + i * 64 * W;
@@ -459,15 +504,19 @@ static bool launch_gemv1(hipStream_t s, float *out, const int8_t *xq, const floa
     switch (groups) {
     case 24:
         if (strips <= 384)
-            hipLaunchKernelGGL((k_gemv1<12, 2, false>), grid, dim3(768), 0, s, out, xq, xs, w, ws, k, 1, nullptr);
+            hipLaunchKernelGGL((k_gemv1<12, 2, false>), grid, dim3(768), 0, s, out, xq, xs, w, ws, k, 1, nullptr,
+                               GemvInput{});
         else
-            hipLaunchKernelGGL((k_gemv1<8, 3, false>), grid, dim3(512), 0, s, out, xq, xs, w, ws, k, 1, nullptr);
+            hipLaunchKernelGGL((k_gemv1<8, 3, false>), grid, dim3(512), 0, s, out, xq, xs, w, ws, k, 1, nullptr,
+                               GemvInput{});
         return true;
     case 32:
-        hipLaunchKernelGGL((k_gemv1<16, 2, false>), grid, dim3(1024), 0, s, out, xq, xs, w, ws, k, 1, nullptr);
+        hipLaunchKernelGGL((k_gemv1<16, 2, false>), grid, dim3(1024), 0, s, out, xq, xs, w, ws, k, 1, nullptr,
+                           GemvInput{});
         return true;
     case 64:
-        hipLaunchKernelGGL((k_gemv1<16, 4, false>), grid, dim3(1024), 0, s, out, xq, xs, w, ws, k, 1, nullptr);
+        hipLaunchKernelGGL((k_gemv1<16, 4, false>), grid, dim3(1024), 0, s, out, xq, xs, w, ws, k, 1, nullptr,
+                           GemvInput{});
         return true;
     case 192: {
         if (strips % 8) return false;
@@ -475,13 +524,24 @@ static bool launch_gemv1(hipStream_t s, float *out, const int8_t *xq, const floa
         if (scratch_reserve((size_t)n_out * groups * sizeof(int32_t), 0)) return false;
         int32_t *dots = scratch().dots;
         hipLaunchKernelGGL((k_gemv1<2, 4, true>), dim3((unsigned)(strips * parts)), dim3(128), 0, s, out, xq, xs, w,
-                           ws, k, parts, dots);
+                           ws, k, parts, dots, GemvInput{});
         hipLaunchKernelGGL(k_gemv1_fold, grid, dim3(256), 0, s, out, dots, xs, ws, groups);
         return true;
     }
     default:
         return false;
     }
+}
+
+int launch_gemv_gelu(hipStream_t s, float *out, const float *a, const float *b, const float *gelu_table,
+                     int gelu_size, float gelu_lower, float gelu_upper, const int8_t *w, const uint16_t *ws,
+                     int n_out, int k) {
+    if (n_out <= 0 || n_out % 16 || k != 256)
+        return set_error(G4_ERR_ARG, "one-token GELU product: shape %d x %d does not fit", n_out, k);
+    const GemvInput in{a, b, gelu_table, gelu_size, gelu_lower, gelu_upper};
+    hipLaunchKernelGGL((k_gemv1<1, 4, false, GEMV_GELU_MUL>), dim3((unsigned)(n_out / 16)), dim3(64), 0, s, out,
+                       nullptr, nullptr, w, ws, k, 1, nullptr, in);
+    return G4_OK;
 }
 
 // The group-ordered fold of split GEMV dots: one thread per output row.

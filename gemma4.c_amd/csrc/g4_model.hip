@@ -503,8 +503,9 @@ static int enqueue_forward(Context &c, const Lane &ln, int n, int start_pos, con
     const bool fused = order() == G4_ORDER_REFERENCE;
     // One token in reference order: the products fused with their neighbours
     // (k_gemv_tail): each row tail runs inside the product it feeds (q, k and
-    // v in one launch; gate/up with geglu and the quantize that follows it;
-    // the per-layer-embedding gate likewise, into q8b).  The tails alternate
+    // v in one launch; gate/up with geglu and the quantize that follows it,
+    // into q8b; the per-layer-embedding gate, whose geglu with the per-layer
+    // input and quantize run inside the projection that reads it).  The tails alternate
     // two residual rows, since every block of a product reads the residual
     // that block 0 updates: 104 updates a step, so the step ends in
     // ln.residual again.
@@ -664,22 +665,26 @@ static int enqueue_forward(Context &c, const Lane &ln, int n, int start_pos, con
             G4_TRY(launch_matmul_gelu(s, ln.q8, ln.qs, L.ple_gate.data, L.ple_gate.scales, G4_PLE,
                                       G4_HIDDEN, n, EPI_GELU_MUL, ep));
         } else if (one) {
+            // the gate as a plain product of the tail's row; geglu with the
+            // per-layer input and its quantize run inside the projection
             GemvJob job = job_on();
             job.k = G4_HIDDEN;
-            job.m[0] = GemvMat{L.ple_gate.data, L.ple_gate.scales, nullptr, G4_PLE / 16};
+            job.m[0] = GemvMat{L.ple_gate.data, L.ple_gate.scales, ln.aux, G4_PLE / 16};
             job.count = 1;
-            job.mul = ln.ple + (size_t)l * G4_PLE;
-            job.q_out = ln.q8b;
-            job.qs_out = ln.qsb;
             const RowTailJob tj = tail_job(ln.hidden, L.post_ffn_ln, 1.0f, nullptr);
-            G4_TRY(launch_gemv_tail(s, job, EPI_GELU_MUL, tj, 2));
+            G4_TRY(launch_gemv_tail(s, job, EPI_PLAIN, tj, 2));
         } else {
             G4_TRY(matmul(ln.hidden, G4_PLE, L.ple_gate, n));
             launch_geglu(s, ln.hidden, ln.ple + (size_t)l * G4_PLE, n, G4_PLE, ple_width, c.gelu,
                          c.gelu_size, c.gelu_lower, c.gelu_upper);
             launch_quantize(s, ln.q8, ln.qs, ln.hidden, (size_t)n * G4_PLE / 64);
         }
-        G4_TRY(matmul(ln.hidden, G4_HIDDEN, L.ple_proj, n, one || gemm_fused));
+        if (one)
+            G4_TRY(launch_gemv_gelu(s, ln.hidden, ln.aux, ln.ple + (size_t)l * G4_PLE, c.gelu, c.gelu_size,
+                                    c.gelu_lower, c.gelu_upper, L.ple_proj.data, L.ple_proj.scales, G4_HIDDEN,
+                                    G4_PLE));
+        else
+            G4_TRY(matmul(ln.hidden, G4_HIDDEN, L.ple_proj, n, gemm_fused));
         if (one) {
             if (l + 1 == G4_LAYERS)  // the last tail, in place (the others run in the next q/k/v)
                 launch_row_tail(s, ln.hidden, L.post_ple_ln, res[p], L.layer_scalar, nullptr, nullptr,

@@ -915,6 +915,7 @@ int launch_gemv_tail(hipStream_t s, const GemvJob &job, int epi, const RowTailJo
     // matrices of one wave (24 groups); the per-layer-embedding gate: 4 strips
     // of 2 waves (12 groups)
     G4_GT(EPI_PLAIN, 6, 1)
+    G4_GT(EPI_PLAIN, 6, 2)
     G4_GT(EPI_PLAIN, 6, 3)
     G4_GT(EPI_GELU_PAIR, 1, 1)
     G4_GT(EPI_GELU_MUL, 2, 2)
