@@ -764,9 +764,12 @@ constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 // quantization group, the group-ordered fp32 fold of the reference
 // (bit-identical).  Requires groups % 8 == 0.
 //   A  64 rows x 64 B per group: wave w fetches rows 16w .. 16w + 15, lane L
-//      the 16-byte part (L & 3) ^ ((row >> 2) & 3) of row 16w + L / 4, so the
+//      the 16-byte part (L & 3) ^ ((row >> 1) & 3) of row 16w + L / 4, so the
 //      parts of a row are stored XOR-swizzled and a lane's 16-byte operand
-//      read (row, part q) is bank-conflict free;
+//      read (row, part q) is bank-conflict free: the LDS serves a 16-byte
+//      read 8 lanes (128 bytes) a cycle, and rows r .. r + 7 then fall on 8
+//      distinct 16-byte bank groups (with (row >> 2) & 3, rows r and r + 2
+//      shared one: 4 conflict cycles a read, SQ_LDS_BANK_CONFLICT);
 //   B  4 packed tiles per group: wave w fetches tile w; LDS slot s holds the
 //      tile's 16-byte unit s ^ (4 (s / 16) & 12), so the four 4-byte reads of
 //      a lane's operand are conflict free;
@@ -851,7 +854,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
     const int part = wave & 3;
     const int a_row = 16 * part + (lane >> 2);
     const int8_t *a_src = xq + (size_t)min(m0 + a_row, rows - 1) * k +
-                          16 * ((lane & 3) ^ ((a_row >> 2) & 3));
+                          16 * ((lane & 3) ^ ((a_row >> 1) & 3));
     const int unit = lane ^ ((lane >> 4) << 2);
     const size_t b_at = (size_t)min(nb0 + part, n_blocks - 1) * groups * 1024 + unit * 16;
     const int8_t *b_src = w + b_at, *b2_src = NB == 2 ? ep.w2 + b_at : nullptr;
@@ -900,7 +903,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
 #pragma unroll
     for (int mi = 0; mi < 2; mi++) {
         const int r = wm * 32 + mi * 16 + l16;
-        a_off[mi] = r * 64 + 16 * (q ^ ((r >> 2) & 3));
+        a_off[mi] = r * 64 + 16 * (q ^ ((r >> 1) & 3));
     }
     int b_off[NI][4];
 #pragma unroll
