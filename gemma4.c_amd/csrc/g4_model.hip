@@ -65,8 +65,8 @@ struct Context {
     // once a lane's pass has written layer l's key/value rows.
     LaneBuffers extra[kLanes - 1];
     hipEvent_t kv_written[kLanes][15] = {};
-    void *lane_attn[kLanes] = {};  // each lane's attention scratch (lane_attn_bytes each)
-    size_t lane_attn_bytes = 0;
+    void *lane_attn[kLanes] = {};  // each lane's attention scratch
+    size_t lane_attn_bytes[kLanes] = {};
     int pending = -1;    // the lane whose last pass may still run (-1: none)
     int next_pos = 0;    // the position after that pass
     int last_lane = 0;   // the lane holding the last pass's residual rows
@@ -770,17 +770,17 @@ static int ensure_kv(Context &c, int last_pos) {
     return G4_OK;
 }
 
-// Each lane's attention scratch, grown (every lane drained first) to `bytes`.
-static int reserve_lane_attn(Context &c, size_t bytes) {
-    if (bytes <= c.lane_attn_bytes) return G4_OK;
-    G4_TRY(drain(c));
-    for (void *&p : c.lane_attn) {
-        release(p);
-        p = nullptr;
-    }
-    c.lane_attn_bytes = 0;
-    for (void *&p : c.lane_attn) G4_HIP(hipMalloc(&p, bytes));
-    c.lane_attn_bytes = bytes;
+// A lane's attention scratch, grown to `bytes` once the lane's previous pass
+// has finished.  Each lane grows its own when it runs, so a prefill run one
+// chunk at a time holds one lane's score rows, not four.
+static int reserve_lane_attn(Context &c, int lane, hipStream_t stream, size_t bytes) {
+    if (bytes <= c.lane_attn_bytes[lane]) return G4_OK;
+    G4_HIP(hipStreamSynchronize(stream));
+    release(c.lane_attn[lane]);
+    c.lane_attn[lane] = nullptr;
+    c.lane_attn_bytes[lane] = 0;
+    G4_HIP(hipMalloc(&c.lane_attn[lane], bytes));
+    c.lane_attn_bytes[lane] = bytes;
     return G4_OK;
 }
 
@@ -817,14 +817,14 @@ static int forward(Context &c, const int *tokens, int n, int start_pos) {
         c.last_lane = 0;
         return G4_OK;
     }
-    G4_TRY(ensure_kv(c, last_pos));  // these two drain before they move a buffer
-    G4_TRY(reserve_lane_attn(c, attend_scratch_bytes(G4_BATCH, last_pos)));
+    G4_TRY(ensure_kv(c, last_pos));  // drains before it moves a buffer
     const bool follow = c.pending >= 0 && start_pos == c.next_pos;
     if (!follow) G4_TRY(drain(c));
     const int lane = follow ? (c.pending + 1) % kLanes : 0;
     Lane ln = make_lane(c, lane);
     G4_HIP(hipStreamSynchronize(ln.stream));  // the lane's previous pass: its buffers are free
-    const FixedScratch attn{c.lane_attn[lane], c.lane_attn_bytes};
+    G4_TRY(reserve_lane_attn(c, lane, ln.stream, attend_scratch_bytes(G4_BATCH, last_pos)));
+    const FixedScratch attn{c.lane_attn[lane], c.lane_attn_bytes[lane]};
     ln.attn_scratch = &attn;
     ln.record_kv = c.kv_written[lane];
     ln.wait_kv = follow ? c.kv_written[c.pending] : nullptr;
