@@ -391,29 +391,31 @@ __device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0,
     const float du = nonempty ? ldexpf((float)e.d, e_run - 150) : 0.0f;
     const bool sp = e.meta & 1;
     const float fa = sp ? e.t : 1.0f, fb = sp ? 1.0f : e.t;
-    float sv = s, at_start = 0.0f, at_end = 0.0f;
-    // entries is the same in every lane (a count read back from LDS, which the
-    // compiler cannot see): made scalar, the loop runs on scalar branches
-    // instead of as a divergent loop with exec-mask updates per step
+    // The chain through the entries in order: entry i's start reaches lane i
+    // from lane i - 1's end by a DPP wave shift, so a step is the run's add,
+    // the event's step and one move for the whole wave (lane 0 keeps the
+    // pass's start).  After step i lane i holds its entry's exact start and
+    // its run's end for good (its input no longer changes), so steps past the
+    // entry count change nothing and the count is rounded up to fours.
+    // entries is the same in every lane (a count read back from LDS, which
+    // the compiler cannot see): made scalar, the loop runs on scalar branches.
     const int n_entries = __builtin_amdgcn_readfirstlane(entries);
-    auto chain_step = [&](int i) __attribute__((always_inline)) {
-        at_start = lane == i ? sv : at_start;
-        sv += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(du), i));
-        at_end = lane == i ? sv : at_end;
-        const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fb), i));
+    float at_start = s, at_end = s, outv = s;
+    auto chain_step = [&]() __attribute__((always_inline)) {
+        at_end = at_start + du;
         if constexpr (SPECIAL)  // s t + 1 at a new maximum, s + t (t * 1 exact) otherwise
-            sv = sv * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fa), i)) + b;
+            outv = at_end * fa + fb;
         else
-            sv = sv + b;
+            outv = at_end + fb;
+        at_start = dpp_float<0x138, 0xf>(outv, at_start);  // wave_shr:1, lane 0 keeps its own
     };
-    int i_chain = 0;
-    for (; i_chain + 4 <= n_entries; i_chain += 4) {  // the readlanes of four steps issue ahead
-        chain_step(i_chain);
-        chain_step(i_chain + 1);
-        chain_step(i_chain + 2);
-        chain_step(i_chain + 3);
+    for (int i = 0; i < n_entries; i += 4) {
+        chain_step();
+        chain_step();
+        chain_step();
+        chain_step();
     }
-    for (; i_chain < n_entries; i_chain++) chain_step(i_chain);
+    const float sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(outv), n_entries - 1));
     const int e0 = biased_exponent(at_start), e1 = biased_exponent(at_end);
     const uint64_t bad = __ballot(lane < entries && nonempty &&
                                   (e0 != e_run || (unsigned)(e0 - 27) > 200u || e1 != e_run));
