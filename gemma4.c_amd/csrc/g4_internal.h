@@ -248,6 +248,11 @@ int launch_attend(hipStream_t s, float *out, const float *q, const float *key_ca
 // Scratch bytes launch_attend needs for n query rows (8 heads, head_dim <= 512)
 // whose last position is last_pos, in the current summation order.
 size_t attend_scratch_bytes(size_t n, int last_pos);
+// Device bytes of the split softmax's terms, flags and per-row results for
+// `rows` decode rows of `stride` values (they follow the scores in the
+// attention scratch).  Decode rows longer than kSoftmaxSplitMin take the split.
+constexpr int kSoftmaxSplitMin = 8192;
+size_t softmax_split_bytes(size_t rows, size_t stride);
 int launch_attend_parallel(hipStream_t s, float *out, const float *q, const float *key_cache,
                            const float *value_cache, int cache_len, int head_dim, int heads,
                            int full, int start_pos, size_t n, const FixedScratch *fixed = nullptr);

@@ -1752,7 +1752,11 @@ __global__ __launch_bounds__(256) void k_attn_combine(float *__restrict__ out,
 
 size_t attend_scratch_bytes(size_t n, int last_pos) {
     const size_t keys = (size_t)last_pos + 1, heads = 8;
-    if (order() == G4_ORDER_REFERENCE) return n * heads * ((keys + 63) & ~(size_t)63) * sizeof(float);
+    if (order() == G4_ORDER_REFERENCE) {  // the scores, and the split softmax of long decode rows
+        const size_t stride = (keys + 63) & ~(size_t)63;
+        const size_t scores = (n * heads * stride * sizeof(float) + 255) & ~(size_t)255;
+        return scores + (n <= 4 && keys > (size_t)kSoftmaxSplitMin ? softmax_split_bytes(n * heads, stride) : 0);
+    }
     return n * ((keys + kAttnChunk - 1) / kAttnChunk) * heads * (512 + 2) * sizeof(float);  // partials
 }
 

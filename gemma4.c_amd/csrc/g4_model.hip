@@ -395,10 +395,11 @@ static int init(const g4_tensor *records, int device) {
     for (char *&p : c.pieces_pinned) G4_HIP(hipHostMalloc((void **)&p, kCopyPiece, hipHostMallocDefault));
     for (hipEvent_t &e : c.piece_done) G4_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     // Split-K scratch for the widest few-row product (1536 x 12288), and the
-    // one-token attention scratch at full context (8 score rows), so that a
-    // captured decode step never needs a larger buffer.
+    // one-token attention scratch at full context (8 score rows and their
+    // split softmax), so that a captured decode step never needs a larger
+    // buffer.
     G4_TRY(scratch_reserve((size_t)G4_VOCAB * (G4_HIDDEN / 64) * sizeof(int32_t),
-                           (size_t)G4_MAX_CONTEXT * 8 * sizeof(float)));
+                           attend_scratch_bytes(1, G4_MAX_CONTEXT - 1)));
     // the other lanes' buffers (struct Lane)
     for (LaneBuffers &b : c.extra) {
         G4_HIP(hipMalloc(&b.residual, (size_t)G4_BATCH * G4_HIDDEN * sizeof(float)));

@@ -1225,19 +1225,15 @@ struct SoftmaxRows {
     }
 };
 
+// One row of `count` values at x, by the whole block (s_max: NW floats of LDS).
 template <int NW, int J>
-__global__ __launch_bounds__(64 * NW) void k_softmax_block(float *__restrict__ v, size_t stride,
-                                                           SoftmaxRows spec) {
+__device__ __forceinline__ void softmax_row_block(float *x, int count, int pad64, EsumShared &sh, float *s_max) {
     constexpr int C = 64 * NW * J;
-    __shared__ EsumShared sh;
-    __shared__ float s_max[NW];
-    const int row = blockIdx.x, count = spec.count(row);
     const int T = threadIdx.x, lane = T & 63, wave = T >> 6;
-    float *x = v + (size_t)row * stride;
     float run_max = x[0], sum = 1.0f;  // gemma4.c:401
     // 16-byte loads of a thread's J consecutive values when the row allows it
     // (each lane then touches a quarter of the cache lines)
-    const bool wide = J % 4 == 0 && (((uintptr_t)x | stride * sizeof(float)) & 15) == 0;
+    const bool wide = J % 4 == 0 && ((uintptr_t)x & 15) == 0;
     for (int base = 0; base < count; base += C) {
         float val[J];
 #pragma unroll
@@ -1279,8 +1275,17 @@ __global__ __launch_bounds__(64 * NW) void k_softmax_block(float *__restrict__ v
         sum = exact_sum_events<NW, J, true>(t, fresh, sum, sh);
         run_max = chunk_max;
     }
-    const int end = spec.pad64 ? (count + 63) & ~63 : count;
+    const int end = pad64 ? (count + 63) & ~63 : count;
     for (int i = T; i < end; i += 64 * NW) x[i] = i < count ? expf_libm(x[i] - run_max) / sum : 0.0f;
+}
+
+template <int NW, int J>
+__global__ __launch_bounds__(64 * NW) void k_softmax_block(float *__restrict__ v, size_t stride,
+                                                           SoftmaxRows spec) {
+    __shared__ EsumShared sh;
+    __shared__ float s_max[NW];
+    const int row = blockIdx.x;
+    softmax_row_block<NW, J>(v + (size_t)row * stride, spec.count(row), spec.pad64, sh, s_max);
 }
 
 // Softmax of `rows` rows (attention rows (t, head) or rows of a fixed count)
@@ -1293,6 +1298,212 @@ static void launch_softmax_block(hipStream_t s, float *v, size_t stride, int max
         hipLaunchKernelGGL((k_softmax_block<16, 4>), dim3(rows), dim3(1024), 0, s, v, stride, spec);
     else  // chunks of 8192 (16384 in one chunk was 1% slower on the decode step at 16K keys)
         hipLaunchKernelGGL((k_softmax_block<16, 8>), dim3(rows), dim3(1024), 0, s, v, stride, spec);
+}
+
+// ---------------------------------------------------------------------------
+// Long rows of a decode step, in three launches so that only the sequential
+// sum stays on one block per row (k_softmax_block, same results bit for bit):
+//   k_softmax_terms (every CU): a row is cut into kSplitBlocks ranges of whole
+//     64-value tiles; each block takes the maximum before its range (x_0, the
+//     starting maximum, and every value before the range: a maximum is the
+//     same in any order), then runs k_softmax_block's per-chunk scan over its
+//     range and writes each term e_i and whether v_i is a new maximum; the
+//     block holding the row's last value writes the row's maximum;
+//   k_softmax_sum (a block per row): the reference's running sum over those
+//     terms in order (exact_sum_events, which is exact whatever the chunks);
+//   k_softmax_norm (every CU): v_i = expf(v_i - max) / sum, and the zeros up
+//     to the tile end.
+// A row of at most kSplitMin values (known on the device only, with a
+// device-side position) is done whole by k_softmax_sum's block, as
+// k_softmax_block does it, and the other two launches leave it alone.
+constexpr int kSplitBlocks = 32;  // blocks per row: 8 rows of a decode step fill 256 CUs
+constexpr int kSplitMin = kSoftmaxSplitMin;
+
+struct SoftmaxSplit {
+    float *terms;    // [row][stride] the terms e_i (+0 for v_0 and the padding)
+    uint8_t *fresh;  // [row][stride] 1 where v_i is a new maximum
+    float *max, *sum;  // [row]
+};
+
+// Device bytes the split needs for `rows` rows of `stride` values (each part
+// 256-byte aligned).
+size_t softmax_split_bytes(size_t rows, size_t stride) {
+    auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    return up(rows * stride * sizeof(float)) + up(rows * stride) + 2 * up(rows * sizeof(float));
+}
+
+static SoftmaxSplit softmax_split_carve(void *work, size_t rows, size_t stride) {
+    auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    char *p = static_cast<char *>(work);
+    SoftmaxSplit w;
+    w.terms = reinterpret_cast<float *>(p);
+    p += up(rows * stride * sizeof(float));
+    w.fresh = reinterpret_cast<uint8_t *>(p);
+    p += up(rows * stride);
+    w.max = reinterpret_cast<float *>(p);
+    w.sum = reinterpret_cast<float *>(p + up(rows * sizeof(float)));
+    return w;
+}
+
+// The block's range of row values: whole 64-value tiles, the row's tiles
+// spread over the grid's x blocks.
+__device__ __forceinline__ void split_range(int count, int &lo, int &hi) {
+    const int tiles = (count + 63) / 64, per = (tiles + (int)gridDim.x - 1) / (int)gridDim.x;
+    lo = (int)blockIdx.x * per * 64;
+    hi = min(lo + per * 64, tiles * 64);
+}
+
+template <int J>
+__global__ __launch_bounds__(256) void k_softmax_terms(const float *__restrict__ v, size_t stride,
+                                                       SoftmaxRows spec, SoftmaxSplit w) {
+    constexpr int NW = 4, C = 64 * NW * J;
+    __shared__ float s_max[NW];
+    const int row = blockIdx.y, count = spec.count(row);
+    const int T = threadIdx.x, lane = T & 63, wave = T >> 6;
+    int lo, hi;
+    split_range(count, lo, hi);
+    if (count <= kSplitMin || lo >= hi) return;  // uniform
+    static_assert(J == 2, "a thread's two values are one 8-byte load and store");
+    const float *x = v + (size_t)row * stride;
+    // values past the row (and v_0, the starting maximum) are -inf: a zero
+    // term; values past the range belong to the next block and only follow
+    // this block's values
+    auto load_chunk = [&](int base, float (&val)[J]) __attribute__((always_inline)) {
+        const int i = base + J * T;  // even, and lo, hi, count's tile end are multiples of 64
+        const float2 f = i < hi ? *reinterpret_cast<const float2 *>(x + i) : make_float2(0.0f, 0.0f);
+        val[0] = i > 0 && i < count && i < hi ? f.x : -INFINITY;
+        val[1] = i + 1 < count && i < hi ? f.y : -INFINITY;
+    };
+    float val[J];
+    load_chunk(lo, val);  // in flight with the maximum's loads
+    // the maximum before the range (lo is a multiple of 64: 16-byte loads,
+    // eight a thread in flight per pass)
+    float m = x[0];
+    constexpr int PASS = 8 * 4 * 64 * NW;
+    for (int i0 = 0; i0 < lo; i0 += PASS) {
+        float4 f[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = i0 + (k * 64 * NW + T) * 4;
+            f[k] = i < lo ? *reinterpret_cast<const float4 *>(x + i) : make_float4(m, m, m, m);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) m = fmaxf(m, fmaxf(fmaxf(f[k].x, f[k].y), fmaxf(f[k].z, f[k].w)));
+    }
+    m = wave_max_scan(m);
+    if (lane == 63) s_max[wave] = m;
+    __syncthreads();
+    float pre = s_max[0];
+#pragma unroll
+    for (int k = 1; k < NW; k++) pre = fmaxf(pre, s_max[k]);
+    __syncthreads();
+    float *terms = w.terms + (size_t)row * stride;
+    uint8_t *fresh_out = w.fresh + (size_t)row * stride;
+    for (int base = lo; base < hi; base += C) {
+        if (base > lo) load_chunk(base, val);
+        float mt = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < J; j++) mt = fmaxf(mt, val[j]);
+        const float incl = wave_max_scan(mt);
+        if (lane == 63) s_max[wave] = incl;
+        __syncthreads();
+        float before = pre, chunk_max = pre;
+#pragma unroll
+        for (int k = 0; k < NW; k++) {
+            if (k < wave) before = fmaxf(before, s_max[k]);
+            chunk_max = fmaxf(chunk_max, s_max[k]);
+        }
+        before = fmaxf(before, dpp_float<0x138, 0xf>(incl, -INFINITY));  // lanes below
+        float t[J];
+        uint32_t fresh = 0;
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const bool is_new = val[j] > before;
+            t[j] = is_new ? expf_libm(before - val[j]) : expf_libm(val[j] - before);
+            fresh |= (uint32_t)is_new << (8 * j);
+            before = fmaxf(before, val[j]);
+        }
+        const int i = base + J * T;
+        if (i < hi) {
+            *reinterpret_cast<float2 *>(terms + i) = make_float2(t[0], t[1]);
+            *reinterpret_cast<uint16_t *>(fresh_out + i) = (uint16_t)fresh;
+        }
+        pre = chunk_max;
+        __syncthreads();  // s_max is rewritten by the next chunk
+    }
+    if (hi >= count && T == 0) w.max[row] = pre;
+}
+
+template <int NW, int J>
+__global__ __launch_bounds__(64 * NW) void k_softmax_sum(float *__restrict__ v, SoftmaxRows spec, size_t stride,
+                                                         SoftmaxSplit w) {
+    static_assert(J == 8, "a thread loads its 8 terms as two 16-byte loads and its flags as 8 bytes");
+    constexpr int C = 64 * NW * J;
+    __shared__ EsumShared sh;
+    __shared__ float s_max[NW];
+    const int row = blockIdx.x, count = spec.count(row);
+    const int T = threadIdx.x;
+    if (count <= kSplitMin) {  // a short row: all of it here
+        softmax_row_block<NW, J>(v + (size_t)row * stride, count, spec.pad64, sh, s_max);
+        return;
+    }
+    const float *terms = w.terms + (size_t)row * stride;
+    const uint8_t *fresh_in = w.fresh + (size_t)row * stride;
+    auto load = [&](int base, float (&t)[J], uint32_t &fresh) __attribute__((always_inline)) {
+        const int i0 = base + J * T;
+        fresh = 0;
+        if (i0 + J <= count) {
+            const float4 a = *reinterpret_cast<const float4 *>(terms + i0);
+            const float4 b = *reinterpret_cast<const float4 *>(terms + i0 + 4);
+            const uint2 f = *reinterpret_cast<const uint2 *>(fresh_in + i0);
+            t[0] = a.x, t[1] = a.y, t[2] = a.z, t[3] = a.w, t[4] = b.x, t[5] = b.y, t[6] = b.z, t[7] = b.w;
+#pragma unroll
+            for (int j = 0; j < 4; j++) fresh |= ((f.x >> (8 * j)) & 1u) << j | ((f.y >> (8 * j)) & 1u) << (j + 4);
+        } else {
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                const int i = i0 + j;
+                t[j] = i < count ? terms[i] : 0.0f;  // past the row: a zero term
+                fresh |= (i < count ? (uint32_t)fresh_in[i] : 0u) << j;
+            }
+        }
+    };
+    float sum = 1.0f;  // gemma4.c:401
+    float t[J];
+    uint32_t fresh;
+    load(0, t, fresh);
+    for (int base = 0; base < count; base += C) {
+        // the next chunk's terms are loaded while this one is summed
+        float t_next[J] = {};
+        uint32_t fresh_next = 0;
+        if (base + C < count) load(base + C, t_next, fresh_next);
+        sum = exact_sum_events<NW, J, true>(t, fresh, sum, sh);
+#pragma unroll
+        for (int j = 0; j < J; j++) t[j] = t_next[j];
+        fresh = fresh_next;
+    }
+    if (T == 0) w.sum[row] = sum;
+}
+
+__global__ __launch_bounds__(256) void k_softmax_norm(float *__restrict__ v, size_t stride, SoftmaxRows spec,
+                                                      SoftmaxSplit w) {
+    const int row = blockIdx.y, count = spec.count(row);
+    int lo, hi;
+    split_range(count, lo, hi);
+    const int end = spec.pad64 ? hi : min(hi, count);
+    if (count <= kSplitMin || lo >= end) return;
+    const float mx = w.max[row], sum = w.sum[row];
+    float *x = v + (size_t)row * stride;
+    for (int i = lo + (int)threadIdx.x; i < end; i += 256) x[i] = i < count ? expf_libm(x[i] - mx) / sum : 0.0f;
+}
+
+// The three launches over `rows` rows; `work` holds softmax_split_bytes(rows, stride).
+static void launch_softmax_split(hipStream_t s, float *v, size_t stride, SoftmaxRows spec, unsigned rows,
+                                 void *work) {
+    const SoftmaxSplit w = softmax_split_carve(work, rows, stride);
+    hipLaunchKernelGGL(k_softmax_terms<2>, dim3(kSplitBlocks, rows), dim3(256), 0, s, v, stride, spec, w);
+    hipLaunchKernelGGL((k_softmax_sum<16, 8>), dim3(rows), dim3(1024), 0, s, v, spec, stride, w);
+    hipLaunchKernelGGL(k_softmax_norm, dim3(kSplitBlocks, rows), dim3(256), 0, s, v, stride, spec, w);
 }
 
 // Attention probabilities of every (token, head) row, one wave each.
@@ -1821,22 +2032,42 @@ __global__ __launch_bounds__(128) void k_attn_values_decode_pc(float *__restrict
         put(2, 2, ring[2]);
         __syncthreads();
         __syncthreads();  // the chain has read tile 0: slot 0 is free
-        // m = 4 i + k: tiles 2m + 3 and 2m + 4 = 8 i + 2k + 3 and 8 i + 2k + 4
-        for (int m = 0; 2 * m + 1 < tiles; m += 4) {
+        // One barrier per pair of tiles: pair m puts tiles 2m + 3 and 2m + 4.
+        // Whole passes of four pairs run in a loop with no exit inside, so that
+        // the compiler keeps each refill where it is written and waits for a
+        // tile's own loads only (an early exit made it sink the refills past
+        // the exits and wait for nearly every load in flight); the last pairs
+        // follow the loop.
+        const int pairs = tiles / 2;
+        int m = 0;
+        for (; m + 4 <= pairs; m += 4) {
             put(3, 2 * m + 3, ring[3]);
             put(0, 2 * m + 4, ring[4]);
             __syncthreads();
-            if (2 * m + 3 >= tiles) break;
             put(1, 2 * m + 5, ring[5]);
             put(2, 2 * m + 6, ring[6]);
             __syncthreads();
-            if (2 * m + 5 >= tiles) break;
             put(3, 2 * m + 7, ring[7]);
             put(0, 2 * m + 8, ring[0]);
             __syncthreads();
-            if (2 * m + 7 >= tiles) break;
             put(1, 2 * m + 9, ring[1]);
             put(2, 2 * m + 10, ring[2]);
+            __syncthreads();
+        }
+        const int rest = pairs - m;
+        if (rest > 0) {
+            put(3, 2 * m + 3, ring[3]);
+            put(0, 2 * m + 4, ring[4]);
+            __syncthreads();
+        }
+        if (rest > 1) {
+            put(1, 2 * m + 5, ring[5]);
+            put(2, 2 * m + 6, ring[6]);
+            __syncthreads();
+        }
+        if (rest > 2) {
+            put(3, 2 * m + 7, ring[7]);
+            put(0, 2 * m + 8, ring[0]);
             __syncthreads();
         }
         return;
@@ -1906,27 +2137,40 @@ __global__ __launch_bounds__(128) void k_attn_values_decode_pc(float *__restrict
         __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
         pin(next);
     };
-    for (int u = 0; u < tiles; u += DEPTH) {
+    // whole passes of 8 tiles with no exit inside (exact waits, as for the
+    // producer), then the last 0-7 tiles; a barrier after every odd tile
+    int u = 0;
+    for (; u + DEPTH <= tiles; u += DEPTH) {
         step(1, u + 0, col_a, col_b, p_ring[0]);
-        if (u + 1 >= tiles) break;
         step(2, u + 1, col_b, col_a, p_ring[1]);
         __syncthreads();
-        if (u + 2 >= tiles) break;
         step(3, u + 2, col_a, col_b, p_ring[2]);
-        if (u + 3 >= tiles) break;
         step(0, u + 3, col_b, col_a, p_ring[3]);
         __syncthreads();
-        if (u + 4 >= tiles) break;
         step(1, u + 4, col_a, col_b, p_ring[4]);
-        if (u + 5 >= tiles) break;
         step(2, u + 5, col_b, col_a, p_ring[5]);
         __syncthreads();
-        if (u + 6 >= tiles) break;
         step(3, u + 6, col_a, col_b, p_ring[6]);
-        if (u + 7 >= tiles) break;
         step(0, u + 7, col_b, col_a, p_ring[7]);
         __syncthreads();
     }
+    const int rem = tiles - u;
+    if (rem > 0) step(1, u + 0, col_a, col_b, p_ring[0]);
+    if (rem > 1) {
+        step(2, u + 1, col_b, col_a, p_ring[1]);
+        __syncthreads();
+    }
+    if (rem > 2) step(3, u + 2, col_a, col_b, p_ring[2]);
+    if (rem > 3) {
+        step(0, u + 3, col_b, col_a, p_ring[3]);
+        __syncthreads();
+    }
+    if (rem > 4) step(1, u + 4, col_a, col_b, p_ring[4]);
+    if (rem > 5) {
+        step(2, u + 5, col_b, col_a, p_ring[5]);
+        __syncthreads();
+    }
+    if (rem > 6) step(3, u + 6, col_a, col_b, p_ring[6]);
     out[((size_t)t * 8 + 4 * blockIdx.y + r) * HD + c0 + j] = o;
 }
 
@@ -1944,14 +2188,19 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
                                  : full ? last_pos + 1 : (last_pos + 1 < G4_WINDOW ? last_pos + 1 : G4_WINDOW);
     const size_t stride = ((size_t)max_keys + 63) & ~(size_t)63;
     const size_t score_floats = n * heads * stride;
+    // decode rows that may be long: the softmax split over the CUs, its
+    // buffers after the scores
+    const bool split = n <= 4 && max_keys > kSplitMin;
+    const size_t score_bytes = (score_floats * sizeof(float) + 255) & ~(size_t)255;
+    const size_t need = score_bytes + (split ? softmax_split_bytes(n * heads, stride) : 0);
     float *scores = nullptr;
     if (fixed) {
-        if (score_floats * sizeof(float) > fixed->bytes)
+        if (need > fixed->bytes)
             return set_error(G4_ERR_ARG, "attention needs %zu bytes of scratch, more than the fixed %zu",
-                             score_floats * sizeof(float), fixed->bytes);
+                             need, fixed->bytes);
         scores = (float *)fixed->ptr;
     } else {
-        int rc = scratch_reserve(0, score_floats * sizeof(float));
+        int rc = scratch_reserve(0, need);
         if (rc) return rc;
         scores = scratch().attn;
     }
@@ -1989,9 +2238,13 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
         G4_SCORES(512, 1, 4);
     }
 #undef G4_SCORES
-    if (n <= 4) {  // decode: few rows, a block per row
+    if (n <= 4) {  // decode: few rows, a block per row (the sum's block, when split)
         const SoftmaxRows spec{heads, full, start_pos, 0, pos_dev, 1};
-        launch_softmax_block(s, scores, stride, max_keys, spec, (unsigned)(n * heads));
+        if (split)
+            launch_softmax_split(s, scores, stride, spec, (unsigned)(n * heads),
+                                 reinterpret_cast<char *>(scores) + score_bytes);
+        else
+            launch_softmax_block(s, scores, stride, max_keys, spec, (unsigned)(n * heads));
     } else {
         hipLaunchKernelGGL(k_attn_softmax_reference, dim3((unsigned)heads, nn), dim3(64), 0, s,
                            scores, heads, full, start_pos, pos_dev, stride);
