@@ -259,6 +259,37 @@ __device__ __forceinline__ int wave_segmented_inclusive(int x) {
     return x;
 }
 
+// The same scans within each 16-lane row: the per-wave values of a block
+// (at most kEsumMaxWaves = 16), one a lane, combined by every wave at once
+// instead of one wave value after another (blocks of 8 or 16 waves).
+__device__ __forceinline__ int row16_segmented_inclusive(int x) {
+    x = segmented_step<0x111, 0xf>(x);
+    x = segmented_step<0x112, 0xf>(x);
+    x = segmented_step<0x114, 0xf>(x);
+    x = segmented_step<0x118, 0xf>(x);
+    return x;
+}
+__device__ __forceinline__ int row16_add_inclusive(int x) {
+    x += dpp_int<0x111, 0xf>(x, 0);
+    x += dpp_int<0x112, 0xf>(x, 0);
+    x += dpp_int<0x114, 0xf>(x, 0);
+    x += dpp_int<0x118, 0xf>(x, 0);
+    return x;
+}
+__device__ __forceinline__ float row16_fadd_inclusive(float x) {
+    x += dpp_float<0x111, 0xf>(x, 0.0f);
+    x += dpp_float<0x112, 0xf>(x, 0.0f);
+    x += dpp_float<0x114, 0xf>(x, 0.0f);
+    x += dpp_float<0x118, 0xf>(x, 0.0f);
+    return x;
+}
+__device__ __forceinline__ void row16_affine_inclusive(float &a, float &b) {
+    affine_step<0x111, 0xf>(a, b);
+    affine_step<0x112, 0xf>(a, b);
+    affine_step<0x114, 0xf>(a, b);
+    affine_step<0x118, 0xf>(a, b);
+}
+
 template <int NW>
 __device__ __forceinline__ void esum_barrier() {
     if constexpr (NW > 1) __syncthreads();
@@ -290,6 +321,9 @@ __device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0,
             }
         }
         float x = s;  // the sum before this wave's first term
+        // (the maps of the earlier waves; from 8 waves on, lane w of every row
+        // holds wave w's, scanned within the row, and this wave takes lane
+        // wave - 1's -- fewer waves run the loop, which measured faster there)
         if (SPECIAL) {
             wave_affine_inclusive(la, lb);
             if constexpr (NW > 1) {
@@ -298,7 +332,16 @@ __device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0,
                     sh.wave_b[wave] = lb;
                 }
                 esum_barrier<NW>();
-                for (int w = 0; w < wave; w++) x = fmaf(x, sh.wave_a[w], sh.wave_b[w]);
+                if constexpr (NW >= 8) {
+                    const int r = lane & 15;
+                    float pa = r < NW ? sh.wave_a[r] : 1.0f, pb = r < NW ? sh.wave_b[r] : 0.0f;
+                    row16_affine_inclusive(pa, pb);
+                    if (wave > 0)
+                        x = fmaf(x, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pa), wave - 1)),
+                                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pb), wave - 1)));
+                } else {
+                    for (int w = 0; w < wave; w++) x = fmaf(x, sh.wave_a[w], sh.wave_b[w]);
+                }
             }
             c = fmaf(x, dpp_float<0x138, 0xf>(la, 1.0f), dpp_float<0x138, 0xf>(lb, 0.0f));
         } else {
@@ -306,7 +349,13 @@ __device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0,
             if constexpr (NW > 1) {
                 if (lane == 63) sh.wave_b[wave] = lb;
                 esum_barrier<NW>();
-                for (int w = 0; w < wave; w++) x += sh.wave_b[w];
+                if constexpr (NW >= 8) {
+                    const int r = lane & 15;
+                    const float pb = row16_fadd_inclusive(r < NW ? sh.wave_b[r] : 0.0f);
+                    if (wave > 0) x += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pb), wave - 1));
+                } else {
+                    for (int w = 0; w < wave; w++) x += sh.wave_b[w];
+                }
             }
             c = x + dpp_float<0x138, 0xf>(lb, 0.0f);
         }
@@ -344,14 +393,25 @@ __device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0,
         }
         esum_barrier<NW>();
         int incoming = 0;
-        total = 0;
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            if (w < wave) {
-                incoming = segmented_join(incoming, sh.wave_seg[w]);
-                idx += sh.wave_count[w];
+        if constexpr (NW >= 8) {
+            const int r = lane & 15;  // (as for the maps above)
+            const int vs = row16_segmented_inclusive(r < NW ? sh.wave_seg[r] : 0);
+            const int vc = row16_add_inclusive(r < NW ? sh.wave_count[r] : 0);
+            if (wave > 0) {
+                incoming = __builtin_amdgcn_readlane(vs, wave - 1);
+                idx += __builtin_amdgcn_readlane(vc, wave - 1);
             }
-            total += sh.wave_count[w];
+            total = __builtin_amdgcn_readlane(vc, NW - 1);
+        } else {
+            total = 0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                if (w < wave) {
+                    incoming = segmented_join(incoming, sh.wave_seg[w]);
+                    idx += sh.wave_count[w];
+                }
+                total += sh.wave_count[w];
+            }
         }
         carry = segmented_join(incoming, carry);
     } else {
