@@ -299,10 +299,14 @@ __device__ __forceinline__ void esum_barrier() {
 // every term is summed (s is then the result); otherwise s and k0 are the
 // exact state the next pass starts from.  Every thread of the NW waves calls
 // it (all lanes active); s and k0 are the same in all of them.
+// Phases 1-4 of a pass from term k0 with the sum s before it: the event
+// table in sh (its first kEsumEvents entries, sh.last_d the final run) and,
+// for each thread, P (the run sum through each of its terms) and carry (the
+// run sum coming into its first term).  Returns the number of events.
 template <int NW, int J, bool SPECIAL>
-__device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0, EsumShared &sh) {
+__device__ __forceinline__ int esum_table(const float (&t)[J], uint32_t spec, float s, int k0, EsumShared &sh,
+                                          int (&P)[J], int &carry) {
     static_assert(NW >= 1 && NW <= kEsumMaxWaves && J <= 32, "esum shape");
-    constexpr int N = 64 * NW * J;
     const int lane = threadIdx.x & 63, wave = NW > 1 ? (int)(threadIdx.x >> 6) : 0;
     const int kb = (wave * 64 + lane) * J;
     // 1. the predicted prefix before this thread's first term
@@ -361,7 +365,6 @@ __device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0,
         }
     }
     // 2. events, grid steps and this thread's run sums
-    int P[J];
     uint32_t evbits = 0;
     {
         float A = c;
@@ -383,7 +386,7 @@ __device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0,
     }
     // 3. run sums across threads, event numbering
     const int seg = wave_segmented_inclusive((evbits ? kEsumFlag : 0) | P[J - 1]);
-    int carry = dpp_int<0x138, 0xf>(seg, 0);  // through the previous thread, flagged if a run starts
+    carry = dpp_int<0x138, 0xf>(seg, 0);  // through the previous thread, flagged if a run starts
     const int count = __popc(evbits), numbered = wave_add_scan(count);
     int idx = numbered - count, total;
     if constexpr (NW > 1) {
@@ -439,6 +442,16 @@ __device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0,
         if (wave == NW - 1 && lane == 63) sh.last_d = P[J - 1];
     }
     esum_barrier<NW>();
+    return total;
+}
+
+template <int NW, int J, bool SPECIAL>
+__device__ bool esum_pass(const float (&t)[J], uint32_t spec, float &s, int &k0, EsumShared &sh) {
+    constexpr int N = 64 * NW * J;
+    const int lane = threadIdx.x & 63, wave = NW > 1 ? (int)(threadIdx.x >> 6) : 0;
+    const int kb = (wave * 64 + lane) * J;
+    int P[J], carry;
+    const int total = esum_table<NW, J, SPECIAL>(t, spec, s, k0, sh, P, carry);
     // 5. resolve: entry i (lane i) is the run before event i and the event; the
     // final run is one more entry, with no step
     const bool more = total > kEsumEvents;
@@ -1379,21 +1392,45 @@ static void launch_softmax_block(hipStream_t s, float *v, size_t stride, int max
 constexpr int kSplitBlocks = 32;  // blocks per row: 8 rows of a decode step fill 256 CUs
 constexpr int kSplitMin = kSoftmaxSplitMin;
 
+// The running sum is cut into chunks of kSumChunk terms.  Each chunk's
+// events and runs (esum_table's, from a predicted start) become entries of a
+// list; one wave then walks the list in order from the exact start.
+constexpr int kSumChunk = 512;            // 4 waves x 64 lanes x 2 terms
+constexpr int kSumFlat = 1024;            // entries the walk holds at once (32 KB of LDS)
+struct SumEntry {
+    int d;      // run sum in the run's grid (units of its predicted ulp)
+    float t;    // the step after the run: its term
+    int start;  // the run's first term
+    int k;      // the step's term (the chunk's end for a final run, which has no step)
+    int meta;   // bit 0: a new maximum (s t + 1); bit 1: no step (a chunk's final run);
+                // bit 2: a chunk of too many events (taken by the exact engine);
+                // bits 8..15: the run's predicted biased exponent
+    int pad[3];
+};
+
 struct SoftmaxSplit {
     float *terms;    // [row][stride] the terms e_i (+0 for v_0 and the padding)
     uint8_t *fresh;  // [row][stride] 1 where v_i is a new maximum
     float *max, *sum;  // [row]
+    float2 *maps;    // [row][chunks] each chunk's map s -> A s + B (fp32, a prediction)
+    SumEntry *ent;   // [row][chunks][64] each chunk's entries
+    int *nent;       // [row][chunks] their count, -1 for more than kEsumEvents events
+    int chunks;      // per row: stride / kSumChunk, rounded up
 };
 
 // Device bytes the split needs for `rows` rows of `stride` values (each part
 // 256-byte aligned).
 size_t softmax_split_bytes(size_t rows, size_t stride) {
     auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
-    return up(rows * stride * sizeof(float)) + up(rows * stride) + 2 * up(rows * sizeof(float));
+    const size_t chunks = (stride + kSumChunk - 1) / kSumChunk;
+    return up(rows * stride * sizeof(float)) + up(rows * stride) + 2 * up(rows * sizeof(float)) +
+           up(rows * chunks * sizeof(float2)) + up(rows * chunks * 64 * sizeof(SumEntry)) +
+           up(rows * chunks * sizeof(int));
 }
 
 static SoftmaxSplit softmax_split_carve(void *work, size_t rows, size_t stride) {
     auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t chunks = (stride + kSumChunk - 1) / kSumChunk;
     char *p = static_cast<char *>(work);
     SoftmaxSplit w;
     w.terms = reinterpret_cast<float *>(p);
@@ -1401,23 +1438,34 @@ static SoftmaxSplit softmax_split_carve(void *work, size_t rows, size_t stride) 
     w.fresh = reinterpret_cast<uint8_t *>(p);
     p += up(rows * stride);
     w.max = reinterpret_cast<float *>(p);
-    w.sum = reinterpret_cast<float *>(p + up(rows * sizeof(float)));
+    p += up(rows * sizeof(float));
+    w.sum = reinterpret_cast<float *>(p);
+    p += up(rows * sizeof(float));
+    w.maps = reinterpret_cast<float2 *>(p);
+    p += up(rows * chunks * sizeof(float2));
+    w.ent = reinterpret_cast<SumEntry *>(p);
+    p += up(rows * chunks * 64 * sizeof(SumEntry));
+    w.nent = reinterpret_cast<int *>(p);
+    w.chunks = (int)chunks;
     return w;
 }
 
-// The block's range of row values: whole 64-value tiles, the row's tiles
-// spread over the grid's x blocks.
+// The block's range of row values: whole chunks of kSumChunk, the row's
+// chunks spread over the grid's x blocks (the last range ends at the row's
+// last 64-value tile).
 __device__ __forceinline__ void split_range(int count, int &lo, int &hi) {
-    const int tiles = (count + 63) / 64, per = (tiles + (int)gridDim.x - 1) / (int)gridDim.x;
-    lo = (int)blockIdx.x * per * 64;
-    hi = min(lo + per * 64, tiles * 64);
+    const int chunks = (count + kSumChunk - 1) / kSumChunk;
+    const int per = (chunks + (int)gridDim.x - 1) / (int)gridDim.x;
+    lo = (int)blockIdx.x * per * kSumChunk;
+    hi = min(lo + per * kSumChunk, (count + 63) & ~63);
 }
 
 template <int J>
 __global__ __launch_bounds__(256) void k_softmax_terms(const float *__restrict__ v, size_t stride,
                                                        SoftmaxRows spec, SoftmaxSplit w) {
     constexpr int NW = 4, C = 64 * NW * J;
-    __shared__ float s_max[NW];
+    static_assert(C == kSumChunk, "a pass of the loop below is one chunk of the running sum");
+    __shared__ float s_max[NW], s_ma[NW], s_mb[NW];
     const int row = blockIdx.y, count = spec.count(row);
     const int T = threadIdx.x, lane = T & 63, wave = T >> 6;
     int lo, hi;
@@ -1488,27 +1536,256 @@ __global__ __launch_bounds__(256) void k_softmax_terms(const float *__restrict__
             *reinterpret_cast<float2 *>(terms + i) = make_float2(t[0], t[1]);
             *reinterpret_cast<uint16_t *>(fresh_out + i) = (uint16_t)fresh;
         }
+        // the chunk's map s -> A s + B, in fp32 (the running sum's prediction)
+        float la = 1.0f, lb = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const bool f = (fresh >> (8 * j)) & 1;
+            const float a = f ? t[j] : 1.0f, b = f ? 1.0f : t[j];
+            lb = fmaf(lb, a, b);
+            la *= a;
+        }
+        wave_affine_inclusive(la, lb);
+        if (lane == 63) {
+            s_ma[wave] = la;
+            s_mb[wave] = lb;
+        }
         pre = chunk_max;
-        __syncthreads();  // s_max is rewritten by the next chunk
+        __syncthreads();  // s_max is rewritten by the next chunk, s_ma after its first barrier
+        if (T == 0) {
+            float A = 1.0f, B = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NW; k++) {
+                B = fmaf(s_ma[k], B, s_mb[k]);
+                A *= s_ma[k];
+            }
+            w.maps[(size_t)row * w.chunks + base / kSumChunk] = make_float2(A, B);
+        }
     }
     if (hi >= count && T == 0) w.max[row] = pre;
 }
 
+// Each chunk of a long row's running sum (every CU): esum_table from the
+// chunk's predicted start -- the fp32 maps of the chunks before it composed
+// and applied to the sum's start, 1 -- its events and runs written as
+// entries; a chunk of more than kEsumEvents events is marked for the exact
+// engine.  A run's sum d is in the grid of its predicted binade, which the
+// walk checks against the exact sums.
+__global__ __launch_bounds__(256) void k_softmax_chunks(SoftmaxRows spec, size_t stride, SoftmaxSplit w) {
+    constexpr int NW = 4, J = 2;
+    static_assert(64 * NW * J == kSumChunk, "one pass of the engine a chunk");
+    __shared__ EsumShared sh;
+    __shared__ float s_a[NW], s_b[NW], s_start;
+    const int row = blockIdx.y, count = spec.count(row);
+    const int T = threadIdx.x, lane = T & 63, wave = T >> 6;
+    int lo, hi;
+    split_range(count, lo, hi);
+    if (count <= kSplitMin || lo >= hi) return;  // uniform
+    const float2 *maps = w.maps + (size_t)row * w.chunks;
+    const int c0 = lo / kSumChunk, c1 = (hi + kSumChunk - 1) / kSumChunk;
+    {  // the predicted start of chunk c0 (c0 < 256: one map a thread)
+        float a = 1.0f, b = 0.0f;
+        if (T < c0) {
+            const float2 m = maps[T];
+            a = m.x;
+            b = m.y;
+        }
+        wave_affine_inclusive(a, b);
+        if (lane == 63) {
+            s_a[wave] = a;
+            s_b[wave] = b;
+        }
+        __syncthreads();
+        if (T == max(c0 - 1, 0)) {
+            float x = 1.0f;  // gemma4.c:401
+            if (c0 > 0) {
+                for (int k = 0; k < wave; k++) x = fmaf(s_a[k], x, s_b[k]);
+                x = fmaf(a, x, b);
+            }
+            s_start = x;
+        }
+        __syncthreads();
+    }
+    float s_hat = s_start;
+    const float *terms = w.terms + (size_t)row * stride;
+    const uint8_t *fresh_in = w.fresh + (size_t)row * stride;
+    for (int c = c0; c < c1; c++) {
+        const int base = c * kSumChunk, i = base + J * T;
+        float t[J];
+        uint32_t fresh = 0;
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            t[j] = i + j < count ? terms[i + j] : 0.0f;  // past the row: a zero term
+            fresh |= (i + j < count ? (uint32_t)(fresh_in[i + j] & 1) : 0u) << j;
+        }
+        int P[J], carry;
+        const int total = esum_table<NW, J, true>(t, fresh, s_hat, 0, sh, P, carry);
+        const int events = min(total, kEsumEvents);
+        SumEntry *out = w.ent + ((size_t)row * w.chunks + c) * 64;
+        if (T <= events) {  // entry T: the run before event T and the event, or the final run
+            const int erun = T == 0 ? biased_exponent(s_hat) : (sh.table[T - 1].meta >> 8) & 0xff;
+            SumEntry e;
+            e.start = base + (T == 0 ? 0 : sh.table[T - 1].k + 1);
+            if (T < events) {
+                const EsumEvent x = sh.table[T];
+                e.d = x.d;
+                e.t = x.t;
+                e.k = base + x.k;
+                e.meta = (x.meta & 1) | erun << 8;
+            } else {
+                e.d = sh.last_d;
+                e.t = 0.0f;
+                e.k = base + kSumChunk;
+                e.meta = 2 | erun << 8;
+            }
+            e.pad[0] = e.pad[1] = e.pad[2] = 0;
+            out[T] = e;
+        }
+        if (T == 0) w.nent[(size_t)row * w.chunks + c] = total > kEsumEvents ? -1 : events + 1;
+        const float2 m = maps[c];
+        s_hat = fmaf(m.x, s_hat, m.y);
+        __syncthreads();  // the table is rewritten by the next chunk
+    }
+}
+
+// The running sum of a long row from its chunks' entries, or the whole
+// softmax of a short one (a block per row).  The entries go to LDS in order
+// (at most kSumFlat; beyond that the whole row takes the exact engine); wave
+// 0 walks them 64 at a time from the exact sum as esum_pass's resolve does:
+// a run adds d u exactly where the exact sum is in the run's predicted binade
+// at its start and end, an event is the plain step.  At the first entry whose
+// check fails (or a marked chunk), the exact sum before it is known: the
+// block runs the exact engine from that run's start to its chunk's end, and
+// the walk goes on from the next chunk's first entry.
 template <int NW, int J>
 __global__ __launch_bounds__(64 * NW) void k_softmax_sum(float *__restrict__ v, SoftmaxRows spec, size_t stride,
                                                          SoftmaxSplit w) {
-    static_assert(J == 8, "a thread loads its 8 terms as two 16-byte loads and its flags as 8 bytes");
+    static_assert(NW == 16 && J == 8, "the walk's exact engine fills the chunk into 16 waves x 64 lanes");
     constexpr int C = 64 * NW * J;
     __shared__ EsumShared sh;
     __shared__ float s_max[NW];
+    __shared__ SumEntry s_flat[kSumFlat];
+    __shared__ int s_off[257], s_pos, s_fall;
+    __shared__ float s_sum;
     const int row = blockIdx.x, count = spec.count(row);
-    const int T = threadIdx.x;
+    const int T = threadIdx.x, lane = T & 63, wave = T >> 6;
     if (count <= kSplitMin) {  // a short row: all of it here
         softmax_row_block<NW, J>(v + (size_t)row * stride, count, spec.pad64, sh, s_max);
         return;
     }
     const float *terms = w.terms + (size_t)row * stride;
     const uint8_t *fresh_in = w.fresh + (size_t)row * stride;
+    const int nch = (count + kSumChunk - 1) / kSumChunk;  // <= 256
+    const int *nent = w.nent + (size_t)row * w.chunks;
+    // entry offsets: chunk c at s_off[c] (a marked chunk takes one entry)
+    if (wave == 0) {
+        int n[4], tot = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int c = 4 * lane + q;
+            n[q] = c < nch ? max(nent[c], 1) : 0;
+            tot += n[q];
+        }
+        int off = wave_add_scan(tot) - tot;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            s_off[4 * lane + q] = off;
+            off += n[q];
+        }
+        if (lane == 63) s_off[256] = off;
+    }
+    __syncthreads();
+    const int total = s_off[nch];
+    if (total <= kSumFlat) {
+        for (int c = wave; c < nch; c += NW) {  // a wave a chunk
+            const int n = nent[c], at = s_off[c];
+            const SumEntry *src = w.ent + ((size_t)row * w.chunks + c) * 64;
+            if (n < 0) {
+                if (lane == 0) {
+                    SumEntry e = {};
+                    e.start = c * kSumChunk;
+                    e.k = (c + 1) * kSumChunk;
+                    e.meta = 4;
+                    s_flat[at] = e;
+                }
+            } else if (lane < n) {
+                s_flat[at + lane] = src[lane];
+            }
+        }
+        if (T == 0) {
+            s_sum = 1.0f;  // gemma4.c:401
+            s_pos = 0;
+        }
+        __syncthreads();
+        while (true) {
+            if (wave == 0) {
+                float s = s_sum;
+                int p = s_pos, fall = -1;
+                const int m = min(64, total - p);
+                if (m > 0) {
+                    SumEntry e = {};
+                    e.meta = 2;
+                    if (lane < m) e = s_flat[p + lane];
+                    const int erun = (e.meta >> 8) & 0xff;
+                    const bool nonempty = e.k > e.start;
+                    const float du = nonempty ? ldexpf((float)e.d, erun - 150) : 0.0f;
+                    const bool sp = e.meta & 1, nostep = (e.meta & 6) != 0;
+                    const float fa = sp ? e.t : 1.0f, fb = sp ? 1.0f : nostep ? 0.0f : e.t;
+                    const int n_entries = __builtin_amdgcn_readfirstlane(m);
+                    float at_start = s, at_end = s, outv = s;
+                    auto chain_step = [&]() __attribute__((always_inline)) {
+                        at_end = at_start + du;
+                        outv = at_end * fa + fb;  // s t + 1 at a new maximum, s + t otherwise
+                        at_start = dpp_float<0x138, 0xf>(outv, at_start);  // wave_shr:1, lane 0 keeps its own
+                    };
+                    for (int i = 0; i < n_entries; i += 4) {
+                        chain_step();
+                        chain_step();
+                        chain_step();
+                        chain_step();
+                    }
+                    const int e0 = biased_exponent(at_start), e1 = biased_exponent(at_end);
+                    const uint64_t bad = __ballot(lane < m && ((e.meta & 4) || (nonempty && (e0 != erun || (unsigned)(e0 - 27) > 200u || e1 != erun))));
+                    if (!bad) {
+                        s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(outv), n_entries - 1));
+                        p += m;
+                    } else {
+                        const int i = (int)__builtin_ctzll(bad);
+                        s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(at_start), i));
+                        fall = __builtin_amdgcn_readlane(e.start, i);
+                    }
+                }
+                if (lane == 0) {
+                    s_sum = s;
+                    s_pos = p;
+                    s_fall = fall;
+                }
+            }
+            __syncthreads();
+            const int fall = s_fall, pos = s_pos;
+            __syncthreads();  // read by every wave before wave 0 writes them again
+            if (fall < 0 && pos >= total) break;  // uniform
+            if (fall >= 0) {  // the exact engine from term fall to its chunk's end
+                const int cb = fall / kSumChunk, base = cb * kSumChunk, i = base + T;
+                float t1[1];
+                t1[0] = T < kSumChunk && i < count ? terms[i] : 0.0f;  // past the chunk: zero terms
+                const uint32_t f1 = T < kSumChunk && i < count ? (uint32_t)(fresh_in[i] & 1) : 0u;
+                float s = s_sum;
+                int k0 = fall - base;
+                while (!esum_pass<NW, 1, true>(t1, f1, s, k0, sh)) {
+                }
+                __syncthreads();  // every thread has s before it is stored
+                if (T == 0) {
+                    s_sum = s;
+                    s_pos = s_off[cb + 1];
+                }
+                __syncthreads();
+            }
+        }
+        if (T == 0) w.sum[row] = s_sum;
+        return;
+    }
+    // more entries than the walk holds: the exact engine over the whole row
     auto load = [&](int base, float (&t)[J], uint32_t &fresh) __attribute__((always_inline)) {
         const int i0 = base + J * T;
         fresh = 0;
@@ -1562,6 +1839,7 @@ static void launch_softmax_split(hipStream_t s, float *v, size_t stride, Softmax
                                  void *work) {
     const SoftmaxSplit w = softmax_split_carve(work, rows, stride);
     hipLaunchKernelGGL(k_softmax_terms<2>, dim3(kSplitBlocks, rows), dim3(256), 0, s, v, stride, spec, w);
+    hipLaunchKernelGGL(k_softmax_chunks, dim3(kSplitBlocks, rows), dim3(256), 0, s, spec, stride, w);
     hipLaunchKernelGGL((k_softmax_sum<16, 8>), dim3(rows), dim3(1024), 0, s, v, spec, stride, w);
     hipLaunchKernelGGL(k_softmax_norm, dim3(kSplitBlocks, rows), dim3(256), 0, s, v, stride, spec, w);
 }
