@@ -1209,6 +1209,135 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float *__restrict__ q
     }
 }
 
+// The same scores for many tokens on the fp32 matrix cores (gemma4.c:281-294).
+// v_mfma_f32_16x16x1_4b adds one product to each of its 4 x 16 x 16 outputs
+// with a single rounding -- fmaf(a, b, c) bit for bit, subnormals, signed
+// zeros and overflow included (checked on the chip against the host's fmaf
+// over 3.7 M outputs of one and of 16 chained steps) -- so each output can
+// carry one of the 16 fma chains the reference runs per score.  A wave holds
+// 32 (token, head) rows x 16 keys: lane (b, i) supplies row i of block b's A
+// operand and key i of its B operand, so block b of product g steps chain
+// m = 4 b + g by channel 16 s + m.  For each s the lane reads one float4 of its
+// key (channels 16 s + 4 b .. + 3, components g = 0..3) and one float4 of each
+// 16-row half of the queries from LDS, and issues 8 products into 8
+// accumulators (2 row halves x 4 g).  Output (block b, register v, lane l) is
+// row 4 (l / 16) + v, key l % 16; the reference's tree -- chains (m, m + 8),
+// then (m, m + 4), then (0 + 2) + (1 + 3) -- pairs blocks 0/2 and 1/3 of one
+// product, then products, all in the same lane and register.
+//
+// A block stages the 32 query rows of 4 tokens in LDS (the first pass's keys
+// already loading) and its 4 waves take 16 keys each per pass; the next pass's
+// first keys load while the tree and the stores run.  The grid holds about 512
+// blocks (two a CU), each striding over several 64-key passes: with one pass
+// a block, staging and pipeline fill cost more than the products.
+template <int HD>
+__global__ __launch_bounds__(256, 2) void k_attn_scores_mfma(const float *__restrict__ q,
+                                                             const float *__restrict__ key_cache,
+                                                             int cache_len, int full, int start_pos,
+                                                             int n, size_t stride,
+                                                             float *__restrict__ scores) {
+    typedef float v16 __attribute__((ext_vector_type(16)));
+    // CH channel steps of the key per load batch, two batches in flight; QP:
+    // the query rows' LDS pitch, +4 floats so the 8 rows one 16-byte read
+    // serves per cycle fall on 8 bank groups
+    constexpr int S = HD / 16, CH = 2, NCH = S / CH, QP = HD + 4;
+    static_assert(NCH % 2 == 0, "the next pass's first batch lands in buffer 0");
+    __shared__ __attribute__((aligned(16))) float s_q[32][QP];
+    const int t0 = blockIdx.y * 4;
+    const int tn = n - t0 < 4 ? n - t0 : 4;
+    const int pos_last = start_pos + t0 + tn - 1;
+    const int kfirst = first_visible(start_pos + t0, full);
+    if (kfirst + (int)blockIdx.x * 64 > pos_last) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, mask = cache_len - 1;
+    const int b = lane >> 4, i16 = lane & 15;
+    // lane (b, i16)'s slice of key kb + i16 (past the last key: a valid row,
+    // never stored)
+    auto key_row = [&](int kb) {
+        const int p = min(kb + i16, pos_last);
+        return key_cache + (size_t)(p & mask) * HD + 4 * b;
+    };
+    float4 kv[2][CH];
+    int kb = kfirst + blockIdx.x * 64 + 16 * wave;
+    {
+        const float *kr = key_row(kb);
+#pragma unroll
+        for (int s = 0; s < CH; s++) kv[0][s] = *reinterpret_cast<const float4 *>(kr + 16 * s);
+    }
+    {
+        constexpr int QV = 32 * HD / 4 / 256;
+        const float *qt = q + (size_t)t0 * 8 * HD;
+        const int count = tn * 8 * HD;
+        float4 qv[QV];
+#pragma unroll
+        for (int u = 0; u < QV; u++) {
+            const int i = 4 * (tid + 256 * u);
+            qv[u] = i < count ? *reinterpret_cast<const float4 *>(qt + i) : make_float4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < QV; u++) {
+            const int i = 4 * (tid + 256 * u);
+            *reinterpret_cast<float4 *>(&s_q[i / HD][i % HD]) = qv[u];
+        }
+    }
+    __syncthreads();
+    const int kstep = gridDim.x * 64;
+    for (; kb <= pos_last; kb += kstep) {  // uniform per wave
+        const float *kr = key_row(kb);
+        const float *kn = key_row(kb + kstep <= pos_last ? kb + kstep : kb);
+        v16 acc[2][4];
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[r][g][v] = 0.0f;
+        // batch c from `use` while `fill` receives batch c + 1, or the next
+        // pass's first batch after the last one
+        auto batch = [&](int c, const float4 (&use)[CH], float4 (&fill)[CH]) __attribute__((always_inline)) {
+            const float *src = c + 1 < NCH ? kr + 16 * CH * (c + 1) : kn;
+#pragma unroll
+            for (int s = 0; s < CH; s++) fill[s] = *reinterpret_cast<const float4 *>(src + 16 * s);
+#pragma unroll
+            for (int s = 0; s < CH; s++) {
+                const int d = 16 * (CH * c + s) + 4 * b;
+                const float4 k4 = use[s];
+                const float4 qa = *reinterpret_cast<const float4 *>(&s_q[i16][d]);
+                const float4 qb = *reinterpret_cast<const float4 *>(&s_q[16 + i16][d]);
+                acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x1f32(qa.x, k4.x, acc[0][0], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x1f32(qb.x, k4.x, acc[1][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x1f32(qa.y, k4.y, acc[0][1], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x1f32(qb.y, k4.y, acc[1][1], 0, 0, 0);
+                acc[0][2] = __builtin_amdgcn_mfma_f32_16x16x1f32(qa.z, k4.z, acc[0][2], 0, 0, 0);
+                acc[1][2] = __builtin_amdgcn_mfma_f32_16x16x1f32(qb.z, k4.z, acc[1][2], 0, 0, 0);
+                acc[0][3] = __builtin_amdgcn_mfma_f32_16x16x1f32(qa.w, k4.w, acc[0][3], 0, 0, 0);
+                acc[1][3] = __builtin_amdgcn_mfma_f32_16x16x1f32(qb.w, k4.w, acc[1][3], 0, 0, 0);
+            }
+        };
+        // a rolled loop: unrolled whole, the compiler hoists every LDS read of
+        // the pass and spills
+#pragma unroll 1
+        for (int c = 0; c < NCH; c += 2) {
+            batch(c, kv[0], kv[1]);
+            batch(c + 1, kv[1], kv[0]);
+        }
+        const int key = kb + i16;
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                float u[4];
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    u[g] = (acc[r][g][v] + acc[r][g][8 + v]) + (acc[r][g][4 + v] + acc[r][g][12 + v]);
+                const float x = (u[0] + u[2]) + (u[1] + u[3]);
+                const int row = 16 * r + 4 * b + v, t = t0 + row / 8, h = row % 8;
+                const int pos = start_pos + t, first = first_visible(pos, full);
+                if (t < n && key >= first && key <= pos)
+                    scores[((size_t)t * 8 + h) * stride + (key - first)] = x;
+            }
+    }
+}
+
 // Inclusive max-scan over the 64 lanes (max is exact in any order): DPP row
 // shifts within each 16-lane row, then row broadcasts across rows.
 template <int CTRL, int ROW_MASK>
@@ -2566,20 +2695,29 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
         return n > 4 && blocks > cap ? cap : blocks;
     };
     const unsigned nn = (unsigned)n;
-    // 4 keys per 16-lane group in prefill (8 would halve the query reads from
-    // LDS, but its 250 registers leave 2 waves a SIMD against 3); 2 in decode
-    // over the window, where the 512 keys then span 16 blocks instead of 8.
-    // One token per block
-    // in prefill: a block's waves run one chain of work each, so more blocks
-    // (more waves a SIMD) hide more of its latencies than staging the keys
-    // for more tokens saves.
+    // Decode (at most 4 tokens) on the VALU kernel: 2 keys per 16-lane group
+    // over the window, where the 512 keys then span 16 blocks instead of 8; 4
+    // over a long context.  The matrix-core kernel's 32-row tiles would be
+    // three quarters empty there.
 #define G4_SCORES(HD, TQ, KG)                                                                     \
     hipLaunchKernelGGL((k_attn_scores<HD, TQ, KG>), dim3(key_blocks(TQ, 16 * KG), (nn + TQ - 1) / TQ), \
                        dim3(256), 0, s, q, key_cache, cache_len, full, start_pos, (int)n, pos_dev,  \
                        stride, scores)
-    if (head_dim == 256) {
-        if (n <= 4) G4_SCORES(256, 6, 2);  // decode: 32-key blocks, twice the blocks over the window
-        else G4_SCORES(256, 1, 4);
+    if (n > 4) {
+        // many tokens: the matrix-core kernel, 4 tokens a block; about 512
+        // blocks (two a CU), each striding over the rest of its key blocks
+        const unsigned ty = (nn + 3) / 4;
+        unsigned bx = key_blocks(4, 64);
+        const unsigned fit = 512u / ty > 1u ? 512u / ty : 1u;
+        if (bx > fit) bx = fit;
+        if (head_dim == 256)
+            hipLaunchKernelGGL(k_attn_scores_mfma<256>, dim3(bx, ty), dim3(256), 0, s, q, key_cache,
+                               cache_len, full, start_pos, (int)n, stride, scores);
+        else
+            hipLaunchKernelGGL(k_attn_scores_mfma<512>, dim3(bx, ty), dim3(256), 0, s, q, key_cache,
+                               cache_len, full, start_pos, (int)n, stride, scores);
+    } else if (head_dim == 256) {
+        G4_SCORES(256, 6, 2);  // decode: 32-key blocks, twice the blocks over the window
     } else {
         G4_SCORES(512, 1, 4);
     }
