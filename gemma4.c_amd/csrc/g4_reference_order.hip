@@ -14,10 +14,11 @@
 //   softmax (gemma4.c:400-408): the running maximum is a prefix maximum, so
 //     every expf term is computed in parallel; only the sum recurrence
 //     s = s*e + 1 (new maximum) / s = s + e runs on one lane per (token, head);
-//   value sums (gemma4.c:296-307): one lane per output channel runs the fma
-//     chain over keys in order;
-//   scores (gemma4.c:281-294): already order-exact in the parallel kernels'
-//     16-lane trees, reused here.
+//   value sums (gemma4.c:296-307): one fma chain per output channel over the
+//     keys in order (a lane per chain in decode; in prefill an output of the
+//     fp32 matrix cores' K = 1 products, which round once a step like fmaf);
+//   scores (gemma4.c:281-294): 16 fma chains per score and a fixed tree (16
+//     lanes per score in decode, matrix-core outputs in prefill).
 //   expf is the host libm's: the table-driven exp2 method of ARM's
 //   optimized-routines (32-entry 2^(i/32) table, degree-3 polynomial, double
 //   evaluation with the range reduction fused), which glibc >= 2.28 ships.
@@ -1999,32 +2000,22 @@ __global__ __launch_bounds__(64) void k_softmax_rows(float *values, int count, s
     softmax_row_reference(values + (size_t)blockIdx.x * stride, count);
 }
 
-// o = fma(p from lane J of this lane's 16-lane row, v, o): one VALU
-// instruction, the broadcast being the fma's DPP source operand.  The caller
-// issues s_nop 1 first when p may have been written by the VALU within the
-// two preceding instructions (the DPP source read hazard).
-#define G4_FMA_ROW_BROADCAST(J)                                                            \
-    __device__ __forceinline__ void fma_row_broadcast_##J(float &o, float p, float v) {     \
-        asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:" #J " row_mask:0xf bank_mask:0xf" \
-                     : "+v"(o)                                                              \
-                     : "v"(p), "v"(v));                                                     \
-    }
-G4_FMA_ROW_BROADCAST(0) G4_FMA_ROW_BROADCAST(1) G4_FMA_ROW_BROADCAST(2) G4_FMA_ROW_BROADCAST(3)
-G4_FMA_ROW_BROADCAST(4) G4_FMA_ROW_BROADCAST(5) G4_FMA_ROW_BROADCAST(6) G4_FMA_ROW_BROADCAST(7)
-G4_FMA_ROW_BROADCAST(8) G4_FMA_ROW_BROADCAST(9) G4_FMA_ROW_BROADCAST(10) G4_FMA_ROW_BROADCAST(11)
-G4_FMA_ROW_BROADCAST(12) G4_FMA_ROW_BROADCAST(13) G4_FMA_ROW_BROADCAST(14) G4_FMA_ROW_BROADCAST(15)
-#undef G4_FMA_ROW_BROADCAST
-
-// out[t][h][d] = fma chain over keys in order (gemma4.c:296-307): one lane
-// per output channel and (token, head) chain.  A block takes a 64-channel
-// slice for WAVES waves; wave w runs the chains of token t0 + w / (8 / HPW)
-// for HPW heads.  Per 64-key tile, V rows are staged in LDS transposed to
-// [channel][key] (a lane reads four keys with one 16-byte load) and each
-// wave's probabilities [head][key] beside them (read as broadcasts); both are
-// prefetched DEPTH tiles ahead in registers with unconditional loads.  A key
-// outside a token's window is skipped by that token's chains (the order of
-// the keys it does see is unchanged).
-template <int HD, int WAVES, int HPW, int DEPTH>
+// out[t][h][d] = fma chain over keys in order (gemma4.c:296-307), on the fp32
+// matrix cores: v_mfma_f32_4x4x1_16b adds one product to each output with a
+// single rounding (fmaf bit for bit), so one product per key steps 256 chains.
+// A wave holds one token's 8 heads x 64 channels as two accumulators of 4
+// heads: its 16 blocks are 4-channel groups, lane l supplying channel d0 + l
+// of V (operand B) and, as row l % 4 of its block, the probability of head
+// h0 + l % 4 (operand A); lane l's output register v is then head h0 + v,
+// channel d0 + l.  All 8 heads of a token see the same keys, so a product per
+// key visible to the token and none for any other keeps every chain the
+// reference's.  A block takes a 64-channel slice for WAVES tokens (one a
+// wave); per 64-key tile, V rows are staged in LDS transposed to
+// [channel][key] (a lane reads four keys' operand with one 16-byte load) and
+// each wave's probabilities [head][key] beside them (rows padded by 4 floats,
+// so the 4 heads one read serves sit on different banks); both are prefetched
+// DEPTH tiles ahead in registers with unconditional loads.
+template <int HD, int WAVES, int DEPTH>
 __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ out,
                                                             const float *__restrict__ probs,
                                                             const float *__restrict__ value_cache,
@@ -2032,28 +2023,29 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
                                                             int n, const int *__restrict__ pos_dev,
                                                             size_t stride, int8_t *__restrict__ q8,
                                                             float *__restrict__ qs) {
+    typedef float v4 __attribute__((ext_vector_type(4)));
+    constexpr int HEADS = 8;
     constexpr int THREADS = WAVES * 64;
     if (pos_dev) start_pos = *pos_dev;
-    constexpr int TOKENS = WAVES * HPW / 8;     // tokens per block
     constexpr int F4 = 64 * 64 / 4 / THREADS;   // float4 per thread per tile
     __shared__ __attribute__((aligned(16))) float s_v[64][64 + 4];
-    __shared__ __attribute__((aligned(16))) float s_p[WAVES][HPW][64];
+    __shared__ __attribute__((aligned(16))) float s_p[WAVES][HEADS][64 + 4];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // last tokens first: their windows hold the most tiles
-    const int d0 = blockIdx.x * 64, t0 = (gridDim.y - 1 - blockIdx.y) * TOKENS;
-    const int tn = n - t0 < TOKENS ? n - t0 : TOKENS;
+    const int d0 = blockIdx.x * 64, t0 = (gridDim.y - 1 - blockIdx.y) * WAVES;
+    const int tn = n - t0 < WAVES ? n - t0 : WAVES;
     const int mask = cache_len - 1;
     const int pos_last = start_pos + t0 + tn - 1;
     const int kfirst = first_visible(start_pos + t0, full);
     const int tiles = (pos_last - kfirst + 64) / 64;
 
-    const int my_t = t0 + wave / (8 / HPW), h0 = (wave % (8 / HPW)) * HPW;
+    const int my_t = t0 + wave;
     const bool active = my_t < t0 + tn;
     const int ld_t = active ? my_t : t0 + tn - 1;  // inactive waves load a valid row
     const int my_pos = start_pos + ld_t, my_first = first_visible(my_pos, full);
     const int my_keys = my_pos - my_first + 1;
-    const float *prow = probs + ((size_t)ld_t * 8 + h0) * stride;
+    const float *prow = probs + (size_t)ld_t * HEADS * stride;
 
     // V tile loader: thread (kq, cc) covers keys 4 kq .. 4 kq + 3 of channels
     // d0 + 4 cc .. + 3, stored transposed as four 16-byte rows (bank-conflict
@@ -2069,35 +2061,33 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
             r[i] = *reinterpret_cast<const float4 *>(value_cache + (size_t)(p & mask) * HD + d0 + 4 * cc);
         }
     };
-    // probability loader: lane covers key kfirst + 64 tile + lane of its rows
-    auto load_p = [&](int tile, float (&r)[HPW]) {
+    // probability loader: lane covers key kfirst + 64 tile + lane of its heads
+    auto load_p = [&](int tile, float (&r)[HEADS]) {
         const int j = min(max(kfirst + tile * 64 + lane - my_first, 0), my_keys - 1);
 #pragma unroll
-        for (int e = 0; e < HPW; e++) r[e] = prow[(size_t)e * stride + j];
+        for (int e = 0; e < HEADS; e++) r[e] = prow[(size_t)e * stride + j];
     };
     float4 ring[DEPTH][F4];
-    float pring[DEPTH][HPW];
+    float pring[DEPTH][HEADS];
 #pragma unroll
     for (int s = 0; s < DEPTH; s++) {
         load_tile(min(s, tiles - 1), ring[s]);
         load_p(min(s, tiles - 1), pring[s]);
     }
 
-    float o[HPW];
-#pragma unroll
-    for (int e = 0; e < HPW; e++) o[e] = 0.0f;
+    v4 acc_lo = {0.0f, 0.0f, 0.0f, 0.0f}, acc_hi = {0.0f, 0.0f, 0.0f, 0.0f};  // heads 0-3, 4-7
 
     // One tile: stage ring slot `s` in LDS, refill the slot DEPTH tiles ahead,
     // then run this wave's chains over the tile.  The loop below is unrolled by
     // DEPTH so every slot index is a compile-time constant (precise waits).
-    auto step = [&](int tile, float4 (&slot)[F4], float (&pslot)[HPW]) {
+    auto step = [&](int tile, float4 (&slot)[F4], float (&pslot)[HEADS]) {
         __syncthreads();  // previous tile fully consumed
         *reinterpret_cast<float4 *>(&s_v[4 * cc + 0][4 * kq]) = make_float4(slot[0].x, slot[1].x, slot[2].x, slot[3].x);
         *reinterpret_cast<float4 *>(&s_v[4 * cc + 1][4 * kq]) = make_float4(slot[0].y, slot[1].y, slot[2].y, slot[3].y);
         *reinterpret_cast<float4 *>(&s_v[4 * cc + 2][4 * kq]) = make_float4(slot[0].z, slot[1].z, slot[2].z, slot[3].z);
         *reinterpret_cast<float4 *>(&s_v[4 * cc + 3][4 * kq]) = make_float4(slot[0].w, slot[1].w, slot[2].w, slot[3].w);
 #pragma unroll
-        for (int e = 0; e < HPW; e++) s_p[wave][e][lane] = pslot[e];
+        for (int e = 0; e < HEADS; e++) s_p[wave][e][lane] = pslot[e];
         load_tile(min(tile + DEPTH, tiles - 1), slot);  // unconditional refill
         load_p(min(tile + DEPTH, tiles - 1), pslot);
         __syncthreads();
@@ -2106,55 +2096,23 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
         int k_lo = my_first - p0, k_hi = my_pos - p0 + 1;  // this token's keys in the tile
         if (k_lo < 0) k_lo = 0;
         if (k_hi > 64) k_hi = 64;
+        const float *vr = s_v[lane];
+        const float *pa = s_p[wave][lane & 3], *pb = s_p[wave][4 + (lane & 3)];
         if (k_lo == 0 && k_hi == 64) {
-            // V of this lane's channel for the 64 keys; probabilities laid out
-            // for a DPP row broadcast: pr[e][c] in lane 16 r + j is key 16 c + j
-            // of head h0 + e, the same in every row, so the fma reads key
-            // 16 c + J of every row's lane J.  The HPW chains of a lane
-            // alternate, so consecutive fmas are independent.
-            typedef float f4 __attribute__((ext_vector_type(4)));
-            f4 v4[16];
-            const f4 *vr = reinterpret_cast<const f4 *>(s_v[lane]);
 #pragma unroll
-            for (int k4 = 0; k4 < 16; k4++) v4[k4] = vr[k4];
-            float pr[HPW][4];
+            for (int k4 = 0; k4 < 16; k4++) {
+                const v4 v = reinterpret_cast<const v4 *>(vr)[k4];
+                const v4 a = reinterpret_cast<const v4 *>(pa)[k4], b = reinterpret_cast<const v4 *>(pb)[k4];
 #pragma unroll
-            for (int e = 0; e < HPW; e++)
-#pragma unroll
-                for (int c = 0; c < 4; c++) pr[e][c] = s_p[wave][e][16 * c + (lane & 15)];
-            // Keys 16 c .. 16 c + 15 for the 8 heads: 128 fmas in one asm block
-            // (nothing inside writes a DPP source, so they issue back to back;
-            // s_nop 1 first for probabilities just written by the VALU).
-            static_assert(HPW == 8, "the asm block below is written for 8 heads per wave");
-#define G4_PVE(E, P, V, J) \
-    "v_fmac_f32_dpp %" #E ", %" #P ", %" #V " row_newbcast:" #J " row_mask:0xf bank_mask:0xf\n"
-#define G4_PV8(J, V)                                                                               \
-    G4_PVE(0, 8, V, J) G4_PVE(1, 9, V, J) G4_PVE(2, 10, V, J) G4_PVE(3, 11, V, J) G4_PVE(4, 12, V, J) \
-    G4_PVE(5, 13, V, J) G4_PVE(6, 14, V, J) G4_PVE(7, 15, V, J)
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                asm volatile("s_nop 1\n"
-                             G4_PV8(0, 16) G4_PV8(1, 17) G4_PV8(2, 18) G4_PV8(3, 19) G4_PV8(4, 20)
-                             G4_PV8(5, 21) G4_PV8(6, 22) G4_PV8(7, 23) G4_PV8(8, 24) G4_PV8(9, 25)
-                             G4_PV8(10, 26) G4_PV8(11, 27) G4_PV8(12, 28) G4_PV8(13, 29) G4_PV8(14, 30)
-                             G4_PV8(15, 31)
-                             : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(o[4]), "+v"(o[5]),
-                               "+v"(o[6]), "+v"(o[7])
-                             : "v"(pr[0][c]), "v"(pr[1][c]), "v"(pr[2][c]), "v"(pr[3][c]), "v"(pr[4][c]),
-                               "v"(pr[5][c]), "v"(pr[6][c]), "v"(pr[7][c]), "v"(v4[4 * c][0]),
-                               "v"(v4[4 * c][1]), "v"(v4[4 * c][2]), "v"(v4[4 * c][3]),
-                               "v"(v4[4 * c + 1][0]), "v"(v4[4 * c + 1][1]), "v"(v4[4 * c + 1][2]),
-                               "v"(v4[4 * c + 1][3]), "v"(v4[4 * c + 2][0]), "v"(v4[4 * c + 2][1]),
-                               "v"(v4[4 * c + 2][2]), "v"(v4[4 * c + 2][3]), "v"(v4[4 * c + 3][0]),
-                               "v"(v4[4 * c + 3][1]), "v"(v4[4 * c + 3][2]), "v"(v4[4 * c + 3][3]));
+                for (int j = 0; j < 4; j++) {
+                    acc_lo = __builtin_amdgcn_mfma_f32_4x4x1f32(a[j], v[j], acc_lo, 0, 0, 0);
+                    acc_hi = __builtin_amdgcn_mfma_f32_4x4x1f32(b[j], v[j], acc_hi, 0, 0, 0);
+                }
             }
-#undef G4_PV8
-#undef G4_PVE
         } else {
             for (int k = k_lo; k < k_hi; k++) {
-                const float vv = s_v[lane][k];
-#pragma unroll
-                for (int e = 0; e < HPW; e++) o[e] = fmaf(s_p[wave][e][k], vv, o[e]);
+                acc_lo = __builtin_amdgcn_mfma_f32_4x4x1f32(pa[k], vr[k], acc_lo, 0, 0, 0);
+                acc_hi = __builtin_amdgcn_mfma_f32_4x4x1f32(pb[k], vr[k], acc_hi, 0, 0, 0);
             }
         }
     };
@@ -2163,21 +2121,27 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_values(float *__restrict__ 
         for (int s = 0; s < DEPTH; s++) step(tile + s, ring[s], pring[s]);
     }
     if (!active) return;
+    float o[HEADS];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        o[e] = acc_lo[e];
+        o[4 + e] = acc_hi[e];
+    }
     if (!q8) {
 #pragma unroll
-        for (int e = 0; e < HPW; e++) out[((size_t)my_t * 8 + h0 + e) * HD + d0 + lane] = o[e];
+        for (int e = 0; e < HEADS; e++) out[((size_t)my_t * HEADS + e) * HD + d0 + lane] = o[e];
         return;
     }
     // the o projection's input quantized here (k_quantize's arithmetic): the
-    // wave's 64 lanes of head h0 + e are one 64-channel group of the row
+    // wave's 64 lanes of head e are one 64-channel group of the row
 #pragma unroll
-    for (int e = 0; e < HPW; e++) {
+    for (int e = 0; e < HEADS; e++) {
         float m = fabsf(o[e]);
 #pragma unroll
         for (int x = 32; x > 0; x >>= 1) m = fmaxf(m, __shfl_xor(m, x));
         const float gscale = m / 127.0f;
         const float inverse = gscale > 0.0f ? 1.0f / gscale : 0.0f;
-        const size_t at = ((size_t)my_t * 8 + h0 + e) * HD + d0;
+        const size_t at = ((size_t)my_t * HEADS + e) * HD + d0;
         q8[at + lane] = (int8_t)(int)rintf(o[e] * inverse);
         if (lane == 0) qs[at / 64] = gscale;
     }
@@ -2770,14 +2734,14 @@ int launch_attend_reference(hipStream_t s, float *out, const float *q, const flo
         if (q8 && !fuse) launch_quantize(s, q8, qs, out, n * heads * head_dim / 64);
         return G4_OK;
     } else {  // prefill: 4 tokens x 8 heads per block share each V tile; one
-              // tile of prefetch (deeper rings cost registers, hence waves)
+              // tile of prefetch (two or three measured no faster)
         dim3 grid(slices, (nn + 3) / 4);
         // with q8 the kernel writes the quantized rows (and no fp32 ones)
         if (head_dim == 256)
-            hipLaunchKernelGGL((k_attn_values<256, 4, 8, 1>), grid, dim3(256), 0, s, out, scores,
+            hipLaunchKernelGGL((k_attn_values<256, 4, 1>), grid, dim3(256), 0, s, out, scores,
                                value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride, q8, qs);
         else
-            hipLaunchKernelGGL((k_attn_values<512, 4, 8, 1>), grid, dim3(256), 0, s, out, scores,
+            hipLaunchKernelGGL((k_attn_values<512, 4, 1>), grid, dim3(256), 0, s, out, scores,
                                value_cache, cache_len, full, start_pos, (int)n, pos_dev, stride, q8, qs);
         return G4_OK;
     }
