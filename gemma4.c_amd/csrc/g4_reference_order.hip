@@ -1479,7 +1479,43 @@ __device__ __forceinline__ void softmax_row_block(float *x, int count, int pad64
         run_max = chunk_max;
     }
     const int end = pad64 ? (count + 63) & ~63 : count;
-    for (int i = T; i < end; i += 64 * NW) x[i] = i < count ? expf_libm(x[i] - run_max) / sum : 0.0f;
+    if (count <= C) {  // one chunk: a value a lane at a time (short rows skip lanes)
+        for (int i = T; i < end; i += 64 * NW) x[i] = i < count ? expf_libm(x[i] - run_max) / sum : 0.0f;
+        return;
+    }
+    // Longer rows chunk by chunk, a chunk's loads all issued first (a value a
+    // lane at a time waits out a memory round trip per value: 8K keys on 4
+    // waves, 32 of them): each thread rewrites the J values it read in the
+    // first pass, every read of which came before the engine's barriers.
+    for (int base = 0; base < end; base += C) {
+        float v[J];
+#pragma unroll
+        for (int j = 0; j < J; j += 4) {
+            const int i = base + J * T + j;
+            if (J % 4 == 0 && wide && i + 3 < count) {
+                const float4 f = *reinterpret_cast<const float4 *>(x + i);
+                v[j] = f.x, v[j + 1] = f.y, v[j + 2] = f.z, v[j + 3] = f.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4 && j + e < J; e++) v[j + e] = i + e < count ? x[i + e] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < J; j += 4) {
+            const int i = base + J * T + j;
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4 && j + e < J; e++)
+                o[e] = i + e < count ? expf_libm(v[j + e] - run_max) / sum : 0.0f;
+            if (J % 4 == 0 && wide && i + 3 < end) {
+                *reinterpret_cast<float4 *>(x + i) = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4 && j + e < J; e++)
+                    if (i + e < end) x[i + e] = o[e];
+            }
+        }
+    }
 }
 
 template <int NW, int J>
