@@ -45,6 +45,10 @@ CASES = [
     (512, 2048, 1, 1000, 21, "ties"),
     (512, 2048, 1, 900, 53, "scaled"),
     (512, 2048, 1, 64, 9, "flat"),
+    # more than 512 tokens in one call: one key block per 4-token group,
+    # each block striding over every pass of its keys
+    (256, 2048, 0, 100, 1100, "normal"),
+    (512, 4096, 1, 0, 700, "normal"),
 ]
 
 
