@@ -1053,6 +1053,21 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
     }
     fold(d1);  // the last group (groups % 8 == 0: it went to d1)
     };
+    // EPI_GELU_MUL: the multipliers do not depend on the products; loaded
+    // before the group loop, they arrive during it (memory operations retire
+    // in order, so the loop's vmcnt waits still cover the DMA they count)
+    float mulv[2][NI][4];
+    if constexpr (EPI == EPI_GELU_MUL) {
+#pragma unroll
+        for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = min(m0 + wm * 32 + mi * 16 + 4 * q + v, rows - 1);
+#pragma unroll
+                for (int ni = 0; ni < NI; ni++)
+                    mulv[mi][ni][v] = ep.mul[(size_t)m * ep.mul_stride + nb0 * 16 + wn * WN + ni * 16 + l16];
+            }
+    }
     if (WAVES == 6 && wave == 0)
         run(std::true_type{});
     else
@@ -1080,19 +1095,16 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_dma(float *__restrict__ out
     // wave, and the other N-half's wave through LDS), scale = absmax / 127.
     __shared__ float s_rowmax[NWN][BM];  // [wn][row]
     float val[2][NI][4], rmax[2][4];
-    // every lookup (and multiplier) first, so that their loads go out together
+    // every lookup first, so that their loads go out together
 #pragma unroll
     for (int mi = 0; mi < 2; mi++)
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const int m = min(m0 + wm * 32 + mi * 16 + 4 * q + v, rows - 1);
 #pragma unroll
             for (int ni = 0; ni < NI; ni++) {
-                const int n = nb0 * 16 + wn * WN + ni * 16 + l16;
                 const float gl = gelu_table_lookup(acc[0][mi][ni][v], ep.gelu_table, ep.gelu_size,
                                                    ep.gelu_lower, ep.gelu_upper);
-                val[mi][ni][v] = EPI == EPI_GELU_PAIR ? gl * acc[NB - 1][mi][ni][v]
-                                                      : gl * ep.mul[(size_t)m * ep.mul_stride + n];
+                val[mi][ni][v] = EPI == EPI_GELU_PAIR ? gl * acc[NB - 1][mi][ni][v] : gl * mulv[mi][ni][v];
             }
         }
 #pragma unroll
