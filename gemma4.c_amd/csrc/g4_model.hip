@@ -109,7 +109,7 @@ static Context g_ctx;
 // Bytes of one piece of a many-row logits copy (g4_logits_all), and the host
 // threads that copy a piece out of its pinned buffer.
 constexpr size_t kCopyPiece = (size_t)32 << 20;
-constexpr int kCopyThreads = 4;
+constexpr int kCopyThreads = 8;
 
 // memcpy split over kCopyThreads threads (one copy alone runs at ~20 GB/s);
 // a thread that cannot start leaves its part to this one.
