@@ -11,7 +11,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <condition_variable>
 #include <map>
+#include <mutex>
 #include <system_error>
 #include <thread>
 #include <vector>
@@ -111,26 +113,87 @@ static Context g_ctx;
 constexpr size_t kCopyPiece = (size_t)32 << 20;
 constexpr int kCopyThreads = 8;
 
-// memcpy split over kCopyThreads threads (one copy alone runs at ~20 GB/s);
-// a thread that cannot start leaves its part to this one.
-static void copy_parallel(char *dst, const char *src, size_t bytes) {
-    const size_t part = (bytes / kCopyThreads + 4095) & ~(size_t)4095;
-    std::thread workers[kCopyThreads - 1];
-    bool started[kCopyThreads - 1] = {};
-    for (int t = 1; t < kCopyThreads; t++) {
-        const size_t lo = t * part < bytes ? t * part : bytes, hi = lo + part < bytes ? lo + part : bytes;
-        if (lo >= hi) continue;
-        try {
-            workers[t - 1] = std::thread([=] { memcpy(dst + lo, src + lo, hi - lo); });
-            started[t - 1] = true;
-        } catch (const std::system_error &) {
-            memcpy(dst + lo, src + lo, hi - lo);
+// memcpy split over kCopyThreads threads (one copy alone runs at ~20 GB/s).
+// kCopyThreads - 1 workers live from the first copy until g4_shutdown (or
+// process exit): starting threads for every 32 MiB piece cost more than the
+// copy's own time.  Each copy is a numbered job: a worker takes its part of
+// every job after the one it last saw (a worker starts knowing the number
+// before its first job), the caller takes part 0 and the parts of workers
+// that could not start, then waits until every worker's part is done.
+class CopyPool {
+  public:
+    ~CopyPool() { stop(); }
+    void copy(char *dst, const char *src, size_t bytes) {
+        std::unique_lock<std::mutex> lock(m_);
+        if (!started_) start_locked();
+        dst_ = dst;
+        src_ = src;
+        bytes_ = bytes;
+        part_ = ((bytes + kCopyThreads - 1) / kCopyThreads + 4095) & ~(size_t)4095;  // > 0 for any bytes > 0
+        pending_ = running_;
+        ++job_;
+        lock.unlock();
+        work_.notify_all();
+        for (int t = 1 + running_; t < kCopyThreads; t++) take(t);
+        take(0);
+        lock.lock();
+        done_.wait(lock, [&] { return pending_ == 0; });
+    }
+    void stop() {
+        {
+            std::lock_guard<std::mutex> guard(m_);
+            stopping_ = true;
+        }
+        work_.notify_all();
+        for (std::thread &t : threads_)
+            if (t.joinable()) t.join();
+        threads_.clear();
+        started_ = stopping_ = false;
+        running_ = 0;
+    }
+
+  private:
+    void take(int t) {
+        const size_t lo = t * part_ < bytes_ ? t * part_ : bytes_;
+        const size_t hi = lo + part_ < bytes_ ? lo + part_ : bytes_;
+        if (lo < hi) memcpy(dst_ + lo, src_ + lo, hi - lo);
+    }
+    void start_locked() {  // m_ held
+        started_ = true;
+        for (int t = 1; t < kCopyThreads; t++) {
+            try {
+                threads_.emplace_back([this, t, seen = job_] { work(t, seen); });
+            } catch (const std::system_error &) {
+                break;  // the caller takes this part and the ones after it
+            }
+            running_++;
         }
     }
-    memcpy(dst, src, part < bytes ? part : bytes);
-    for (int t = 1; t < kCopyThreads; t++)
-        if (started[t - 1]) workers[t - 1].join();
-}
+    void work(int t, unsigned seen) {
+        std::unique_lock<std::mutex> lock(m_);
+        for (;;) {
+            work_.wait(lock, [&] { return stopping_ || job_ != seen; });
+            if (stopping_) return;
+            seen = job_;
+            lock.unlock();
+            take(t);
+            lock.lock();
+            if (--pending_ == 0) done_.notify_one();
+        }
+    }
+    std::mutex m_;
+    std::condition_variable work_, done_;
+    std::vector<std::thread> threads_;
+    char *dst_ = nullptr;
+    const char *src_ = nullptr;
+    size_t bytes_ = 0, part_ = 0;
+    unsigned job_ = 0;
+    int pending_ = 0, running_ = 0;
+    bool started_ = false, stopping_ = false;
+};
+static CopyPool g_copy_pool;
+
+static void copy_parallel(char *dst, const char *src, size_t bytes) { g_copy_pool.copy(dst, src, bytes); }
 
 // Initial positions of a global-attention ring (a power of two).
 constexpr int kGlobalStart = 4096;
@@ -162,6 +225,7 @@ static void release(void *p) {
 }
 
 static void free_all(Context &c) {
+    g_copy_pool.stop();
     for (LaneBuffers &b : c.extra)
         if (b.stream) (void)hipStreamSynchronize(b.stream);
     if (c.stream) (void)hipStreamSynchronize(c.stream);
