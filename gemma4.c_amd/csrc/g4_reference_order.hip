@@ -168,7 +168,11 @@ __device__ __forceinline__ float block_advance(float s, float tb, int p0, uint64
 //     sums, then scans over lanes and waves; only its binade is used);
 //  2. marks as an event every step that is not a grid step under that
 //     prediction: the predicted binade changes, a tie, a softmax new maximum,
-//     a term or partial sum outside the normal range;
+//     a term or partial sum outside the normal range.  Every step of a run
+//     must be on the run's one grid, also where the run passes from one
+//     thread to the next, whose start comes from the scans (another order)
+//     and can lie on the other side of a power of two: a thread's first step
+//     takes the binade the previous thread's prediction ends in;
 //  3. takes R_k = rint(t_k / u), u from the predicted binade, for every
 //     other step, and the prefix sums of R within each run between events;
 //  4. lists the events in order in LDS: the run sum before each, its term,
@@ -365,11 +369,25 @@ __device__ __forceinline__ int esum_table(const float (&t)[J], uint32_t spec, fl
             c = x + dpp_float<0x138, 0xf>(lb, 0.0f);
         }
     }
-    // 2. events, grid steps and this thread's run sums
+    // 2. events, grid steps and this thread's run sums, each step on the grid
+    // of the binade its prediction is in before it.  A run that goes on from
+    // the previous thread must keep that thread's grid: the binade the
+    // previous thread's prediction ends in, lane l - 1's over DPP.  Where that
+    // is not c's, the first step (taken on c's grid in the loop) becomes an
+    // event instead, and its R leaves the run sums up to the next event.
+    // Lane 0 of a later wave cannot see the previous wave's end before the
+    // next barrier; there c and that end are two fp32 evaluations of the same
+    // prefix with nonnegative operands (+, x, fma) and at most 2J + 23
+    // roundings on any path, so each is within (2J + 23) 2^-24 of the exact
+    // prefix and the two are apart by less than 2^-16 of it (J <= 32): unless
+    // c lies within 2^-12 of a power of two they share a binade, c's.  Within
+    // that margin the first step is an event -- except just above 1 in a
+    // softmax sum, where s >= 1 and every step keeps the sum >= 1.  Where
+    // every term before the thread is inactive, c is s itself.
     uint32_t evbits = 0;
     {
         float A = c;
-        int run = 0;
+        int run = 0, R0 = 0;
 #pragma unroll
         for (int j = 0; j < J; j++) {
             const bool act = kb + j >= k0, sp = SPECIAL && ((spec >> j) & 1);
@@ -380,9 +398,27 @@ __device__ __forceinline__ int esum_table(const float (&t)[J], uint32_t spec, fl
             const float R = rintf(T);  // nearest, ties to even
             const bool ev = act && (sp || ep != ec || (unsigned)(ep - 27) > 200u ||
                                     fabsf(T - R) == 0.5f || !(t[j] <= 3.40282347e38f));
+            if (j == 0) R0 = act ? (int)R : 0;
             run = ev ? 0 : min(run + (act ? (int)R : 0), kEsumCap);
             P[j] = run;
             evbits |= (uint32_t)ev << j;
+        }
+        const int ec = biased_exponent(c);
+        int e_first = ec;  // wave 0's lane 0: c is s
+        if constexpr (NW > 1) {
+            const uint32_t m = __float_as_uint(c) & 0x7fffffu;
+            const bool near_low = m < (1u << 11) && !(SPECIAL && ec == 127);
+            if (wave > 0 && kb > k0 && (near_low || m >= (1u << 23) - (1u << 12))) e_first = -1;
+        }
+        const int e_in = dpp_int<0x138, 0xf>(biased_exponent(A), e_first);
+        if (e_in != ec && kb >= k0 && !(evbits & 1u)) {
+            // (sums below 2^24 are exact after the subtraction; larger ones,
+            // saturated or not, stay above it and fail the checks either way)
+            const int stop = (int)__builtin_ctzll((uint64_t)evbits | 1ull << J);  // J: no later event
+#pragma unroll
+            for (int j = 0; j < J; j++)
+                if (j < stop) P[j] -= R0;
+            evbits |= 1u;
         }
     }
     // 3. run sums across threads, event numbering

@@ -9,10 +9,17 @@ terms J T .. J T + J - 1), a predicted prefix whose binade marks events
 (binade change, tie, new maximum, out-of-range value), integer run sums
 saturating at 2^29, at most 63 events per pass, the chain computed before the
 checks, and the two ways a run can fail (predicted binade wrong; run leaves
-its binade early).  The GPU kernels are held to the oracle bit for bit by the
-GPU tests; this test pins the method itself on inputs chosen to hit every
-branch (ties, zeros, huge dynamic range, overflow to inf, many events per
-pass)."""
+its binade early).  The prediction has the kernel's structure: each thread's
+start comes from its own J-term map composed over lanes and waves by scans,
+and the thread then runs its J steps from that start, so the start and the
+previous thread's end are two evaluations of one prefix in different orders.
+A thread's first step takes the binade of the previous thread's end (lane
+l - 1's; for a wave's lane 0, its start's unless that lies within 2^-12 of a
+power of two, then an event), as the kernel does.  The GPU kernels are held
+to the oracle bit for bit by the GPU tests; this test pins the method itself
+on inputs chosen to hit every branch (ties, zeros, huge dynamic range,
+overflow to inf, many events per pass, sums that pass a power of two an ulp
+at a time) and shows that the first-step rule is needed."""
 
 import numpy as np
 
@@ -36,20 +43,81 @@ def sequential(t, spec, s=0.0):
     return s
 
 
-def one_pass(t, spec, s, k0):
-    """Returns (s, k0, done), as esum_pass does."""
+def fma32(a, b, c):
+    """fp32 a * b + c (the product exact in float64, then one rounding to
+    float64 and one to float32: a prediction, so a rare double rounding does
+    not matter)."""
+    return (np.asarray(a, np.float64) * np.asarray(b, np.float64) + np.asarray(c, np.float64)).astype(np.float32)
+
+
+def predict(t, spec, s, k0, J, rule, softmax):
+    """A_prev, A_cur per term (the prediction before and after each step),
+    the binade each thread's first step is taken on and its start's."""
+    n = len(t)
+    nt = -(-n // J)
+    tt = np.concatenate([t, np.zeros(nt * J - n, np.float32)])
+    sp = np.concatenate([spec, np.zeros(nt * J - n, bool)])
+    act = np.arange(nt * J) >= k0
+    idx = np.arange(nt) * J
+    # each thread's map x -> la x + lb over its J terms
+    la, lb = np.ones(nt, np.float32), np.zeros(nt, np.float32)
+    for j in range(J):
+        i = idx + j
+        a = np.where(act[i] & sp[i], tt[i], f32(1)).astype(np.float32)
+        b = np.where(act[i], np.where(sp[i], f32(1), tt[i]), f32(0)).astype(np.float32)
+        lb = fma32(lb, a, b)
+        la = (la * a).astype(np.float32)
+    # inclusive scan over the 64 lanes of each wave (Hillis-Steele), then the
+    # waves' maps in order: the start of each thread
+    nw = -(-nt // 64)
+    A = np.ones(nw * 64, np.float32)
+    B = np.zeros(nw * 64, np.float32)
+    A[:nt], B[:nt] = la, lb
+    A, B = A.reshape(nw, 64), B.reshape(nw, 64)
+    for sh in (1, 2, 4, 8, 16, 32):
+        pa = np.concatenate([np.ones((nw, sh), np.float32), A[:, :-sh]], axis=1)
+        pb = np.concatenate([np.zeros((nw, sh), np.float32), B[:, :-sh]], axis=1)
+        B = fma32(pb, A, B)
+        A = (pa * A).astype(np.float32)
+    x = np.empty(nw, np.float32)
+    xv = f32(s)
+    for w in range(nw):
+        x[w] = xv
+        xv = fma32(xv, A[w, 63], B[w, 63])
+    ex_a = np.concatenate([np.ones((nw, 1), np.float32), A[:, :-1]], axis=1).reshape(-1)[:nt]
+    ex_b = np.concatenate([np.zeros((nw, 1), np.float32), B[:, :-1]], axis=1).reshape(-1)[:nt]
+    c = fma32(np.repeat(x, 64)[:nt], ex_a, ex_b)
+    # each thread's J steps from its start
+    A_prev = np.empty(nt * J, np.float32)
+    A_cur = np.empty(nt * J, np.float32)
+    a = c.copy()
+    for j in range(J):
+        i = idx + j
+        A_prev[i] = a
+        nxt = np.where(sp[i], fma32(a, tt[i], 1), (a + tt[i]).astype(np.float32))
+        a = np.where(act[i], nxt, a).astype(np.float32)
+        A_cur[i] = a
+    e_first = biased_exponent(c)
+    if rule == "thread":
+        end = biased_exponent(a)  # each thread's predicted end
+        lane0 = (np.arange(nt) % 64) == 0
+        e_first = np.where(lane0, e_first, np.concatenate([[0], end[:-1]]))
+        m = c.view(np.uint32) & 0x7FFFFF
+        near = ((m < (1 << 11)) & ~(softmax & (biased_exponent(c) == 127))) | (m >= (1 << 23) - (1 << 12))
+        e_first = np.where(lane0 & (np.arange(nt) > 0) & (idx > k0) & near, -1, e_first)
+    return A_prev[:n], A_cur[:n], e_first, biased_exponent(c)
+
+
+def one_pass(t, spec, s, k0, J=8, rule="thread", softmax=False):
+    """Returns (s, k0, done), as esum_pass does.  rule "thread": a thread's
+    first step takes the binade the previous thread's prediction ends in;
+    "start": its own start's (the rule without the thread boundary).
+    softmax: the engine's new-maximum mode (s >= 1 throughout)."""
     n = len(t)
     k = np.arange(n)
     act = k >= k0
-    # 1. predicted prefix (fp32, any association; here left to right)
-    A_prev = np.empty(n, np.float32)
-    A_cur = np.empty(n, np.float32)
-    a = f32(s)
-    for i in range(n):
-        A_prev[i] = a
-        if act[i]:
-            a = f32(f32(a * t[i]) + f32(1)) if spec[i] else f32(a + t[i])
-        A_cur[i] = a
+    # 1. predicted prefix
+    A_prev, A_cur, e_first, e_start = predict(t, spec, s, k0, J, rule, softmax)
     ep, ec = biased_exponent(A_prev), biased_exponent(A_cur)
     with np.errstate(over="ignore", invalid="ignore"):
         T = np.minimum(np.ldexp(t.astype(np.float32), (150 - ep).astype(np.int32)).astype(np.float32),
@@ -57,6 +125,9 @@ def one_pass(t, spec, s, k0):
     R = np.rint(T)
     ev = act & (spec | (ep != ec) | ((ep - 27) > 200) | ((ep - 27) < 0) | (np.abs(T - R) == 0.5)
                 | ~(t <= f32(3.40282347e38)))
+    # a thread's first step on another grid than the run's: an event
+    first = k[k % J == 0]
+    ev[first] |= act[first] & (e_first[first // J] != e_start[first // J])
     # 3. run sums (segmented at events, saturating)
     P = np.zeros(n, np.int64)
     run = 0
@@ -106,14 +177,14 @@ def one_pass(t, spec, s, k0):
     raise AssertionError("a run that fails its end check has a crossing step")
 
 
-def exact_sum(t, spec, s=0.0, stats=None):
+def exact_sum(t, spec, s=0.0, stats=None, J=8, rule="thread", softmax=False):
     t = np.asarray(t, np.float32)
     spec = np.asarray(spec, bool)
     s, k0 = f32(s), 0
     passes = 0
     while True:
         passes += 1
-        s2, k1, done = one_pass(t, spec, s, k0)
+        s2, k1, done = one_pass(t, spec, s, k0, J, rule, softmax)
         assert done or k1 > k0, "a pass that neither finishes nor moves forward"
         s, k0 = s2, k1
         if done:
@@ -185,7 +256,7 @@ def test_softmax_running_sums():
         if trial % 3 == 0:
             x = np.sort(x)  # a new maximum at every step: hundreds of events
         t, spec = softmax_terms(x)
-        assert same(exact_sum(t, spec, 1.0), sequential(t, spec, 1.0)), trial
+        assert same(exact_sum(t, spec, 1.0, softmax=True), sequential(t, spec, 1.0)), trial
 
 
 def test_planted_mistake_is_caught():
@@ -207,3 +278,56 @@ def test_planted_mistake_is_caught():
         else:
             s = f32(s + x)
     assert s != exact
+
+
+def crawl(g, n, boundary, cross, lo, hi, start=0.0):
+    """Terms whose sequential sum (from `start`) is brought to boundary - m u
+    by its first term and then gains R = rint(r) ulps a term (r uniform in
+    [lo, hi], u the ulp below boundary), passing boundary near term `cross`."""
+    u = boundary * 2.0 ** -24
+    R = round((lo + hi) / 2)
+    t = (g.uniform(lo, hi, n) * u).astype(np.float32)
+    t[0] = f32(boundary - R * (cross - 1) * u - start)
+    return t
+
+
+def crawl_rows(seed, n, count):
+    g = np.random.default_rng(seed)
+    rows = []
+    for i in range(count):
+        boundary = (2.0, 4.0, 1024.0, 2.0 ** -10)[i % 4]
+        lo, hi = ((2.05, 2.45), (1.55, 2.45), (0.55, 0.95))[(i // 4) % 3]
+        rows.append(crawl(g, n, boundary, int(g.integers(n // 10, n * 9 // 10)), lo, hi))
+    return rows
+
+
+def test_sums_crawling_past_a_power_of_two():
+    """Sums of squares and softmax sums that pass a power of two a few ulps a
+    term (each term rounds to R ulps below it and to another count above it),
+    over the block shapes of the kernels (4 waves x 6 and x 8 terms a thread,
+    16 x 4 and x 8, 8 x 1)."""
+    for J, n in ((6, 1536), (8, 2048), (4, 4096), (8, 8192), (1, 512)):
+        for i, t in enumerate(crawl_rows(100 + J, n, 12)):
+            spec = np.zeros(n, bool)
+            assert same(exact_sum(t, spec, J=J), sequential(t, spec)), (J, n, i)
+    g = np.random.default_rng(15)
+    for J, n in ((8, 2048), (8, 8192), (1, 512)):
+        for i in range(9):
+            boundary = (2.0, 4.0, 8.0)[i % 3]
+            lo, hi = ((2.05, 2.45), (1.55, 2.45), (0.55, 0.95))[(i // 3) % 3]
+            t = crawl(g, n, boundary, int(g.integers(n // 10, n * 9 // 10)), lo, hi, start=1.0)
+            spec = np.zeros(n, bool)
+            assert same(exact_sum(t, spec, 1.0, J=J, softmax=True), sequential(t, spec, 1.0)), (J, n, i)
+
+
+def test_first_step_rule_is_needed():
+    """Without the thread-boundary rule (each thread's first step on the grid
+    of its own start's binade) the same crawling sums come out wrong: a run
+    then mixes two grids where the scanned start of a thread and the end of
+    the previous thread's prediction lie on two sides of a power of two."""
+    wrong = 0
+    for J, n in ((6, 1536), (8, 2048), (4, 4096)):
+        for t in crawl_rows(100 + J, n, 12):
+            spec = np.zeros(n, bool)
+            wrong += not same(exact_sum(t, spec, J=J, rule="start"), sequential(t, spec))
+    assert wrong > 0
