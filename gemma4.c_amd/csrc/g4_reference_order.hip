@@ -2064,7 +2064,23 @@ __global__ __launch_bounds__(64 * NW) void k_attn_softmax_reference(float *__res
     // start first and the short ones fill in behind them
     const int h = blockIdx.x, t = gridDim.y - 1 - blockIdx.y;
     const int pos = start_pos + t, keys = pos + 1 - first_visible(pos, full);
-    softmax_row_block<NW, 8>(scores + ((size_t)t * heads + h) * stride, keys, 0, sh, s_max);
+    float *row = scores + ((size_t)t * heads + h) * stride;
+    if constexpr (NW == 1) {
+        // the fewest terms a lane that hold the row in one chunk: the engine's
+        // per-term phases shrink with them (a causal chunk's early tokens have
+        // short rows; 512 tokens x 8 heads from position 0: 14.2 against
+        // 15.6 us with 8 terms a lane)
+        if (keys <= 64)
+            softmax_row_block<1, 1>(row, keys, 0, sh, s_max);
+        else if (keys <= 128)
+            softmax_row_block<1, 2>(row, keys, 0, sh, s_max);
+        else if (keys <= 256)
+            softmax_row_block<1, 4>(row, keys, 0, sh, s_max);
+        else
+            softmax_row_block<1, 8>(row, keys, 0, sh, s_max);
+    } else {
+        softmax_row_block<NW, 8>(row, keys, 0, sh, s_max);
+    }
 }
 
 // Independent rows of `count` values at `stride` (the per-op entry point).
