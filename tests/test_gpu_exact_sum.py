@@ -15,11 +15,14 @@ ranges leave gaps or overlap right where the sum passes B; and a term rounded
 on the grid of the binade above (rint(r / 2)) differs from R, so a step taken
 on the wrong grid changes the sum.  The sum passes B near a chosen term, or
 stops just short of it.  Each row goes through every block shape that
-evaluates such a sum: softmax rows of 300 .. 20000 values (8 waves x 1 term a thread, 16 x 4,
-16 x 8 in chunks of 8192), rmsnorm rows of 1536 (4 waves x 6), attention over
-designed scores (q a unit vector, so each score is one key component exactly):
-prefill rows (4 waves x 8 in chunks of 2048) and decode rows of 12001 keys
-(the split path: per-chunk predicted starts, then the walk).  Bit for bit
+evaluates such a sum: per-op softmax rows of 300 and 511 values (64-term
+blocks advanced from the exact sum) and of 3000 .. 20000 (16 waves x 4 terms
+a thread, 16 x 8 in chunks of 8192), rmsnorm rows of 1536 (4 waves x 6), and
+attention over designed scores (q a unit vector, so each score is one key
+component exactly): global prefill rows (one wave x 8 terms, or 4 waves x 8
+in chunks of 2048), global decode rows of 12001 keys (the split path:
+per-chunk predicted starts, then the walk), and sliding-window rows of 512
+keys in decode (8 waves x 1) and prefill (one wave x 8).  Bit for bit
 against the oracle.
 """
 
@@ -118,42 +121,50 @@ def test_rmsnorm_sum_of_squares_crawls_past_power_of_two(pkg, g4lib, torch_gpu, 
     assert not bad, f"rows {bad}"
 
 
-# tokens, start position, seed (full attention, head_dim 512, a ring of 16384)
+# head_dim, ring, full, tokens, start position, seed
 ATTEND = [
-    (64, 3000, 0),   # prefill rows of 3001 .. 3064 keys: two chunks of 2048
-    (64, 3000, 1),
-    (32, 1800, 2),   # one chunk
-    (1, 12000, 0),   # decode over 12001 keys: the split path
-    (1, 12000, 1),
-    (3, 12000, 2),
+    (512, 16384, 1, 64, 3000, 0),   # global prefill rows of 3001 .. 3064 keys: two chunks of 2048
+    (512, 16384, 1, 64, 3000, 1),
+    (512, 16384, 1, 32, 800, 2),    # one wave a row
+    (512, 16384, 1, 1, 12000, 0),   # global decode over 12001 keys: the split path
+    (512, 16384, 1, 1, 12000, 1),
+    (512, 16384, 1, 3, 12000, 2),
+    (256, 1024, 0, 1, 5000, 0),     # window decode: rows of 512 keys
+    (256, 1024, 0, 1, 5000, 1),
+    (256, 1024, 0, 2, 5000, 2),
+    (256, 1024, 0, 16, 900, 3),     # window prefill
 ]
 
 
-@pytest.mark.parametrize("n,start,seed", ATTEND)
-def test_attention_softmax_crawls_past_power_of_two(pkg, g4lib, torch_gpu, oracle_lib, n, start, seed):
+@pytest.mark.parametrize("hd,ring,full,n,start,seed", ATTEND)
+def test_attention_softmax_crawls_past_power_of_two(pkg, g4lib, torch_gpu, oracle_lib, hd, ring, full, n,
+                                                    start, seed):
     """Head h's query is the unit vector e_h, so its scores are component h
-    of the keys, which holds a crawling row (a different crossing a head)."""
-    hd, ring, heads = 512, 16384, 8
+    of the keys, which holds a crawling row (a different crossing a head),
+    laid out from the first key token 0 sees (later tokens see it shifted)."""
+    heads = 8
     g = rng(7300 + 10 * seed + n + start)
-    keys = start + n
+    first = 0 if full else start - 511
+    keys = start + n - first
+    slots = (first + np.arange(keys)) % ring
     kc = np.zeros((ring, hd), np.float32)
     for h in range(heads):
         boundary, r = (2, 4, 8)[(h + seed) % 3], RANGES[(h + 2 * seed) % 3]
         if h == 7:  # ends short
-            kc[:keys, h] = crawl_scores(g, keys, boundary, 0, short_by=3, r=r)
+            kc[slots, h] = crawl_scores(g, keys, boundary, 0, short_by=3, r=r)
         else:
-            kc[:keys, h] = crawl_scores(g, keys, boundary, int(g.integers(start // 5, start)), r=r)
+            kc[slots, h] = crawl_scores(g, keys, boundary, int(g.integers(min(keys, start) // 5, min(keys, start))), r=r)
     vc = g.standard_normal((ring, hd)).astype(np.float32)
     q = np.zeros((n, heads, hd), np.float32)
     for h in range(heads):
         q[:, h, h] = 1.0
     ref = np.empty_like(q)
     oracle_lib.oracle().orc_attend(ref.ctypes.data, q.ctypes.data, kc.ctypes.data, vc.ctypes.data,
-                                   ring, hd, heads, 1, start, n)
+                                   ring, hd, heads, full, start, n)
     out = torch_gpu.empty(q.shape, dtype=torch_gpu.float32, device="cuda")
     kd, vd, qd = dev(torch_gpu, kc), dev(torch_gpu, vc), dev(torch_gpu, q)
     pkg.check(g4lib.g4_attend(None, out.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
-                              ring, hd, heads, 1, start, n))
+                              ring, hd, heads, full, start, n))
     torch_gpu.cuda.synchronize()
     o = out.cpu().numpy()
     bad = [(t, h) for t in range(n) for h in range(heads)
