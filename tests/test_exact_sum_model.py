@@ -305,8 +305,9 @@ def test_sums_crawling_past_a_power_of_two():
     """Sums of squares and softmax sums that pass a power of two a few ulps a
     term (each term rounds to R ulps below it and to another count above it),
     over the block shapes of the kernels (4 waves x 6 and x 8 terms a thread,
-    16 x 4 and x 8, 8 x 1)."""
-    for J, n in ((6, 1536), (8, 2048), (4, 4096), (8, 8192), (1, 512)):
+    8 x 3 and 6 x 4 (the one-token products' row tails), 16 x 4 and x 8,
+    8 x 1)."""
+    for J, n in ((6, 1536), (3, 1536), (4, 1536), (8, 2048), (4, 4096), (8, 8192), (1, 512)):
         for i, t in enumerate(crawl_rows(100 + J, n, 12)):
             spec = np.zeros(n, bool)
             assert same(exact_sum(t, spec, J=J), sequential(t, spec)), (J, n, i)
