@@ -75,9 +75,23 @@ def build_oracle(with_ref: bool = True) -> None:
         run(["make", "-s", "-C", ORACLE, "run_g4", f"REF={REFERENCE}"])
 
 
+def build_test_bins() -> None:
+    """Test programs that run library code the C ABI does not reach (the
+    exact-sum engine in every block shape): built with the library's device
+    flags, linked to libg4.so, into tests/_bin/."""
+    out_dir = os.path.join(ROOT, "tests", "_bin")
+    os.makedirs(out_dir, exist_ok=True)
+    flags = [f for f in HIP_FLAGS if f not in ("-shared", "-fPIC")]
+    out = os.path.join(out_dir, "esum_fuzz")
+    run([HIPCC, *flags, f"-I{os.path.join(PKG, 'csrc')}", os.path.join(ROOT, "tests", "esum_fuzz.hip"),
+         "-o", out + ".tmp", f"-L{PKG}", "-lg4", "-Wl,-rpath,$ORIGIN/../../gemma4.c_amd"])
+    os.replace(out + ".tmp", out)
+
+
 def build_all(with_ref: bool = True) -> None:
     build_img()
     build_hip()
+    build_test_bins()
     build_oracle(with_ref)
 
 

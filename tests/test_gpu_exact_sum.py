@@ -28,6 +28,9 @@ against the oracle.
 
 from __future__ import annotations
 
+import os
+import subprocess
+
 import numpy as np
 import pytest
 
@@ -170,3 +173,21 @@ def test_attention_softmax_crawls_past_power_of_two(pkg, g4lib, torch_gpu, oracl
     bad = [(t, h) for t in range(n) for h in range(heads)
            if not np.array_equal(o[t, h].view(np.uint32), ref[t, h].view(np.uint32))]
     assert not bad, f"(token, head) {bad[:16]}"
+
+
+FUZZ = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_bin", "esum_fuzz")
+
+
+def test_engine_in_every_block_shape_against_the_sequential_loop(torch_gpu):
+    """The engine itself (tests/esum_fuzz.hip, built by build(): it includes
+    the library's source), one row of 64 NW J terms a block, in every block
+    shape the kernels use and both modes, over 45,600 generated rows (random
+    magnitudes, sums crawling past powers of two, peaked rows, a new maximum
+    at every step, ties, zeros, subnormal and huge terms), against the plain
+    sequential fp32 loop on the host, bit for bit.  The engine as it was
+    before the thread-boundary rule fails rows of every shape here."""
+    assert os.path.exists(FUZZ), "tests/_bin/esum_fuzz is missing: run __graft_entry__.build()"
+    run = subprocess.run([FUZZ], capture_output=True, text=True, timeout=120)
+    print(run.stdout)
+    assert run.returncode == 0, run.stdout[-3000:] + run.stderr[-2000:]
+    assert "all rows equal" in run.stdout
